@@ -1,0 +1,55 @@
+"""Build recipe for the native libraries (gfx950 only, built in-tree).
+
+  libparakeet_hip.so      HIP kernels + C ABI      (csrc/pk_decode.hip)
+  libparakeet_decoder.so  C++ decoder API           (csrc/parakeet_decoder.cpp, csrc/gguf_reader.cpp)
+
+Called by __graft_entry__.build(); every call recompiles.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INC = os.path.join(ROOT, "include")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-Wall", "-Wno-unused-result", f"-I{INC}"]
+
+
+def _run(cmd):
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(l for l in proc.stderr.splitlines() if "packed-fp32-ops" not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{err}")
+    return err
+
+
+def build_hip():
+    out = os.path.join(HERE, "libparakeet_hip.so")
+    _run([HIPCC, *HIP_FLAGS, "-shared", os.path.join(CSRC, "pk_decode.hip"), "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def build_decoder():
+    srcs = [os.path.join(CSRC, f) for f in ("parakeet_decoder.cpp", "gguf_reader.cpp")]
+    if not all(os.path.exists(s) for s in srcs):
+        return None
+    out = os.path.join(HERE, "libparakeet_decoder.so")
+    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", f"-I{INC}", f"-I{CSRC}", *srcs,
+          f"-L{HERE}", "-lparakeet_hip", "-Wl,-rpath,$ORIGIN", "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
+def build_all():
+    return [build_hip(), build_decoder()]
+
+
+if __name__ == "__main__":
+    print(build_all())

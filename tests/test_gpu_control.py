@@ -1,0 +1,148 @@
+"""Control flow on the device with scripted logits (weights zeroed, biases set
+so the argmax is forced), where token/duration sequences have closed forms;
+blank bias; determinism; error codes."""
+import numpy as np
+import pytest
+
+from conftest import small_eou, small_tdt
+
+pytestmark = pytest.mark.gpu
+
+
+def _zero_out(path, writer, out_bias, **kw):
+    """Decoder whose joint output is exactly out_bias (joint.out weight zero)."""
+    from parakeet_amd import pk
+    p = "tdt" if writer is small_tdt else "eou"
+    J = kw.get("J", 96)
+    Vo = len(out_bias)
+    ov = {f"{p}.joint.out.weight": np.zeros((Vo, J), np.float32),
+          f"{p}.joint.out.bias": np.asarray(out_bias, np.float32)}
+    writer(path, overrides=ov, **kw)
+    return pk.Decoder.from_gguf(path, n_slots=4)
+
+
+def test_tdt_nonblank_dur0_hits_symbol_cap(tmp_path):
+    """token 5 with duration index 0 (dur 0): max_symbols emissions per frame."""
+    V1, Dn = 62, 5
+    bias = np.zeros(V1 + Dn, np.float32)
+    bias[5] = 3.0
+    bias[V1 + 0] = 2.0
+    dev = _zero_out(str(tmp_path / "a.gguf"), small_tdt, bias)
+    from parakeet_amd import synth
+    T = 9
+    for ms in (1, 3, 10):
+        dev.reset_state(0)
+        r = dev.decode([synth.encoder_frames(0, T, 128)], slots=[0], max_symbols=ms)[0]
+        assert r["tokens"].tolist() == [5] * (ms * T)
+        assert r["steps"] == ms * T
+
+
+def test_tdt_blank_dur0_advances_one(tmp_path):
+    V1, Dn = 62, 5
+    bias = np.zeros(V1 + Dn, np.float32)
+    bias[61] = 1.0          # blank
+    bias[V1 + 0] = 1.0      # duration 0 -> advance max(1, 0)
+    dev = _zero_out(str(tmp_path / "b.gguf"), small_tdt, bias)
+    from parakeet_amd import synth
+    r = dev.decode([synth.encoder_frames(0, 11, 128)], max_symbols=10)[0]
+    assert r["steps"] == 11 and len(r["tokens"]) == 0
+
+
+def test_tdt_duration_carry_across_windows(tmp_path):
+    """token with duration 4 over windows of 3 frames: carry_frames spills."""
+    V1, Dn = 62, 5
+    bias = np.zeros(V1 + Dn, np.float32)
+    bias[7] = 1.0
+    bias[V1 + 4] = 1.0
+    dev = _zero_out(str(tmp_path / "c.gguf"), small_tdt, bias)
+    from parakeet_amd import synth
+    enc = synth.encoder_frames(0, 3, 128)
+    expected_carry = []
+    t_global, emitted = 0, []
+    for w in range(5):
+        r = dev.decode([enc], slots=[0], max_symbols=10)[0]
+        emitted.append(len(r["tokens"]))
+        expected_carry.append(dev.read_state(0)["ctrl"][2])
+    # frames advance 4 per emission over a 15-frame stream split into 3-frame windows
+    # emissions at frames 0, 4, 8, 12 -> windows [0..3) [3..6) [6..9) [9..12) [12..15);
+    # after the third window t = 2 + 4 = 6 in a 3-frame window: carry 3, consumed whole by the fourth
+    assert emitted == [1, 1, 1, 0, 1], emitted
+    assert expected_carry == [1, 2, 3, 0, 1], expected_carry
+
+
+def test_eou_reset_and_segments(tmp_path):
+    """EOU token always wins: state reset each step, a boundary only when the
+    segment has tokens (src/parakeet_eou.cpp:292-310)."""
+    V1 = 36
+    bias = np.zeros(V1, np.float32)
+    bias[33] = 1.0          # eou
+    dev = _zero_out(str(tmp_path / "e.gguf"), small_eou, bias)
+    from parakeet_amd import synth
+    r = dev.decode([synth.encoder_frames(0, 6, 64)], max_symbols=5, tokens_base=[3])[0]
+    assert r["steps"] == 6 and len(r["tokens"]) == 0
+    # 3 tokens before the call, segment start 0 -> one boundary at 3
+    assert r["segments"].tolist() == [3]
+    st = dev.read_state(0)
+    assert st["ctrl"][3] == 35 and st["ctrl"][4] == 3      # last = blank, segment start
+
+
+def test_eou_special_piece_skips(tmp_path):
+    """token 0 is "<unk>": skipped, frame ends (src/parakeet_eou.cpp:315-320)."""
+    V1 = 36
+    bias = np.zeros(V1, np.float32)
+    bias[0] = 1.0
+    dev = _zero_out(str(tmp_path / "s.gguf"), small_eou, bias)
+    from parakeet_amd import synth
+    r = dev.decode([synth.encoder_frames(0, 4, 64)], max_symbols=5)[0]
+    assert r["steps"] == 4 and len(r["tokens"]) == 0
+
+
+def test_blank_bias_matches_oracle(tmp_path):
+    from parakeet_amd import gguf, pk, synth
+    import oracle
+    from parity import check_window
+    path = str(tmp_path / "m.gguf")
+    small_tdt(path)
+    dev = pk.Decoder.from_gguf(path, n_slots=3)
+    om = oracle.OracleModel.from_gguf(path, gguf)
+    encs = [synth.encoder_frames(u, 20, 128) for u in range(3)]
+    bb = np.array([0.0, 2.0, 4.0], np.float32)
+    res = dev.decode(encs, trace=True, blank_bias=bb)
+    blanks = []
+    for u in range(3):
+        st = om.new_state()
+        check_window(om, dev, u, encs[u], res[u], st, 10, blank_bias=float(bb[u]))
+        blanks.append(int((res[u]["trace"][:, 0] == 61).sum()))
+    assert blanks[0] <= blanks[1] <= blanks[2]
+
+
+def test_deterministic(tmp_path):
+    from parakeet_amd import synth
+    path = str(tmp_path / "m.gguf")
+    small_tdt(path)
+    from parakeet_amd import pk
+    dev = pk.Decoder.from_gguf(path, n_slots=6)
+    encs = [synth.encoder_frames(u, 40, 128) for u in range(6)]
+    a = dev.decode(encs, trace=True)
+    for u in range(6):
+        dev.reset_state(u)          # slots carry state: start the second run fresh too
+    b = dev.decode(encs, trace=True)
+    for x, y in zip(a, b):
+        assert np.array_equal(x["trace"], y["trace"])
+        assert np.array_equal(x["tokens"], y["tokens"])
+
+
+def test_error_codes(tmp_path):
+    from parakeet_amd import pk, synth
+    path = str(tmp_path / "m.gguf")
+    small_tdt(path)
+    dev = pk.Decoder.from_gguf(path, n_slots=2)
+    with pytest.raises(pk.PkError) as e:
+        dev.decode([synth.encoder_frames(0, 5, 100)])
+    assert e.value.rc == 1                        # encoder dim mismatch (reference rc 1)
+    with pytest.raises(pk.PkError) as e:
+        dev.decode([synth.encoder_frames(0, 40, 128)], token_cap=2)
+    assert e.value.rc == 11
+    with pytest.raises(pk.PkError) as e:
+        dev.decode([synth.encoder_frames(0, 5, 128)] * 2, slots=[1, 1])
+    assert e.value.rc == 3

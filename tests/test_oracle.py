@@ -1,0 +1,259 @@
+"""Pins the oracle (CPU restatement of the reference decoder) against things
+the reference does not get to define: library routines (numpy float16,
+torch.nn.LSTM golden vectors), float64 brute force, closed forms of scripted
+decoders, invariants (linearity, chunked == one-shot), and a planted mistake
+that the replay must flag."""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import small_eou, small_tdt
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+# ---------------------------------------------------------------- primitives
+
+def test_f16_to_f32_all_bit_patterns(oracle_mod):
+    lib = oracle_mod.lib()
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([lib.ora_f16_to_f32(int(b)) for b in bits[::7]], np.float32)
+    exp = ref[::7]
+    finite = np.isfinite(exp)
+    assert np.array_equal(got[finite].view(np.uint32), exp[finite].view(np.uint32))
+    assert np.all(np.isnan(got[np.isnan(exp)]))
+    assert np.array_equal(np.isinf(got), np.isinf(exp))
+
+
+def test_q8_0_dequant_known_blocks(oracle_mod):
+    """Hand-built q8_0 blocks {f16 d; int8 q[32]}: value = q * d."""
+    d = np.array([0.5, -0.25, 3.0], np.float16)
+    q = np.stack([np.arange(-16, 16), np.full(32, -128), np.arange(32) * 4 - 64]).astype(np.int8)
+    raw = np.zeros((3, 34), np.uint8)
+    raw[:, :2] = d.view(np.uint8).reshape(3, 2)
+    raw[:, 2:] = q.view(np.uint8)
+    out = np.zeros(96, np.float32)
+    oracle_mod.lib().ora_dequant(raw.ctypes.data, 8, 96, oracle_mod.fptr(out))
+    assert out[:32].tolist() == [0.5 * v for v in range(-16, 16)]
+    assert out[32:64].tolist() == [32.0] * 32
+    assert out[64:].tolist() == [3.0 * (4 * i - 64) for i in range(32)]
+
+
+def test_q8_0_quantizer_roundtrip(pkg):
+    from parakeet_amd import gguf
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((7, 64)).astype(np.float32)
+    raw = gguf.quantize_q8_0(x)
+    assert len(raw) == 7 * 2 * 34
+    y = gguf.dequantize(raw, gguf.GGML_Q8_0, x.size).reshape(x.shape)
+    amax = np.abs(x.reshape(-1, 32)).max(1)
+    err = np.abs(x - y).reshape(-1, 32).max(1)
+    assert np.all(err <= amax / 127 * 0.5 * 1.01 + 1e-7)
+
+
+def test_argmax_first_index(oracle_mod):
+    am = lambda a: oracle_mod.lib().ora_argmax(oracle_mod.fptr(np.asarray(a, np.float32)), len(a))
+    assert am([1, 3, 3, 2]) == 1
+    assert am([0, 0, 0]) == 0
+    assert am([-5]) == 0
+    assert am([-1, -0.5, -0.5000001]) == 1
+    assert am([2, 1, 2]) == 0
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_gemv_vs_float64(oracle_mod, seed):
+    rng = np.random.default_rng(seed)
+    W = rng.standard_normal((13, 40)).astype(np.float32)
+    x = rng.standard_normal(40).astype(np.float32)
+    b = rng.standard_normal(13).astype(np.float32)
+    y = np.zeros(13, np.float32)
+    lib = oracle_mod.lib()
+    lib.ora_gemv(oracle_mod.fptr(W), oracle_mod.fptr(x), oracle_mod.fptr(b), oracle_mod.fptr(y), 13, 40)
+    ref = W.astype(np.float64) @ x + b
+    assert np.allclose(y, ref, rtol=1e-5, atol=1e-5)
+    # gemv_add accumulates; W(2x) = 2 W x (linearity), bias-free
+    y2 = np.ones(13, np.float32)
+    x2 = (2 * x).astype(np.float32)
+    lib.ora_gemv_add(oracle_mod.fptr(W), oracle_mod.fptr(x2), oracle_mod.fptr(y2), 13, 40)
+    assert np.allclose(y2 - 1.0, 2 * (W.astype(np.float64) @ x), rtol=1e-5, atol=1e-5)
+
+
+def _golden_model(oracle_mod, g):
+    H = 16
+    weights = {"tdt.predict.embed.weight": np.zeros((2, H), np.float32)}
+    for l in range(2):
+        weights[f"tdt.predict.lstm.{l}.w_ih"] = g[f"weight_ih_l{l}"]
+        weights[f"tdt.predict.lstm.{l}.w_hh"] = g[f"weight_hh_l{l}"]
+        weights[f"tdt.predict.lstm.{l}.b_ih"] = g[f"bias_ih_l{l}"]
+        weights[f"tdt.predict.lstm.{l}.b_hh"] = g[f"bias_hh_l{l}"]
+    for n, shp in (("joint.enc.weight", (4, 4)), ("joint.enc.bias", (4,)), ("joint.pred.weight", (4, H)),
+                   ("joint.pred.bias", (4,)), ("joint.out.weight", (3, 4)), ("joint.out.bias", (3,))):
+        weights["tdt." + n] = np.zeros(shp, np.float32)
+    return oracle_mod.OracleModel(weights, "tdt", H, 2, 4, 4, 1, durations=[0])
+
+
+def test_lstm_matches_torch_golden(oracle_mod):
+    g = np.load(os.path.join(GOLDEN, "lstm_golden.npz"))
+    om = _golden_model(oracle_mod, g)
+    st = om.new_state()
+    for step in range(2):
+        om.lstm_step(g["x"][step], st)
+        assert np.allclose(st.h, g[f"h{step}"], rtol=2e-5, atol=2e-6), step
+        assert np.allclose(st.c, g[f"c{step}"], rtol=2e-5, atol=2e-6), step
+
+
+def test_lstm_golden_catches_gate_swap(oracle_mod):
+    """Planted mistake: swapping the f and g gate blocks must fail the golden check."""
+    g = dict(np.load(os.path.join(GOLDEN, "lstm_golden.npz")))
+    H = 16
+    for l in range(2):
+        for k in (f"weight_ih_l{l}", f"weight_hh_l{l}", f"bias_ih_l{l}", f"bias_hh_l{l}"):
+            a = g[k].copy()
+            a[H:2 * H], a[2 * H:3 * H] = g[k][2 * H:3 * H], g[k][H:2 * H]
+            g[k] = a
+    om = _golden_model(oracle_mod, g)
+    st = om.new_state()
+    om.lstm_step(g["x"][0], st)
+    assert not np.allclose(st.h, g["h0"], rtol=1e-3, atol=1e-4)
+
+
+def test_joint_closed_form(oracle_mod, tmp_path):
+    w = small_tdt(str(tmp_path / "m.gguf"))
+    from parakeet_amd import gguf
+    om = oracle_mod.OracleModel.from_gguf(str(tmp_path / "m.gguf"), gguf)
+    rng = np.random.default_rng(3)
+    enc = rng.standard_normal(128).astype(np.float32)
+    pred = rng.standard_normal(64).astype(np.float32)
+    f = lambda k: w[k].astype(np.float64)
+    hid = np.maximum(0, f("tdt.joint.enc.weight") @ enc + f("tdt.joint.enc.bias")
+                     + f("tdt.joint.pred.weight") @ pred + f("tdt.joint.pred.bias"))
+    ref = f("tdt.joint.out.weight") @ hid + f("tdt.joint.out.bias")
+    assert np.allclose(om.joint(enc, pred), ref, rtol=1e-4, atol=1e-4)
+
+
+# ---------------------------------------------------------------- control flow
+
+def _scripted(tmp_path, writer, bias, name="s.gguf", **kw):
+    from parakeet_amd import gguf
+    import oracle
+    p = "tdt" if writer is small_tdt else "eou"
+    J = 96
+    ov = {f"{p}.joint.out.weight": np.zeros((len(bias), J), np.float32),
+          f"{p}.joint.out.bias": np.asarray(bias, np.float32)}
+    path = str(tmp_path / name)
+    writer(path, overrides=ov, **kw)
+    return oracle.OracleModel.from_gguf(path, gguf)
+
+
+def test_tdt_symbol_cap_closed_form(tmp_path):
+    V1 = 62
+    bias = np.zeros(V1 + 5, np.float32)
+    bias[5], bias[V1] = 3.0, 2.0
+    om = _scripted(tmp_path, small_tdt, bias)
+    enc = np.zeros((9, 128), np.float32)
+    for ms in (1, 3, 10):
+        r = om.decode_window(enc, om.new_state(), ms)
+        assert r["tokens"].tolist() == [5] * (9 * ms) and r["steps"] == 9 * ms
+
+
+def test_tdt_duration_carry_closed_form(tmp_path):
+    V1 = 62
+    bias = np.zeros(V1 + 5, np.float32)
+    bias[7], bias[V1 + 4] = 1.0, 1.0
+    om = _scripted(tmp_path, small_tdt, bias)
+    st = om.new_state()
+    emitted, carry = [], []
+    for _ in range(5):
+        r = om.decode_window(np.zeros((3, 128), np.float32), st, 10)
+        emitted.append(len(r["tokens"]))
+        carry.append(st.st.carry_frames)
+    assert emitted == [1, 1, 1, 0, 1] and carry == [1, 2, 3, 0, 1]
+
+
+def test_tdt_blank_with_duration(tmp_path):
+    """blank with duration 3 advances 3 frames per step: ceil(T/3) steps."""
+    V1 = 62
+    bias = np.zeros(V1 + 5, np.float32)
+    bias[61], bias[V1 + 3] = 1.0, 1.0
+    om = _scripted(tmp_path, small_tdt, bias)
+    r = om.decode_window(np.zeros((10, 128), np.float32), om.new_state(), 10)
+    assert r["steps"] == 4 and len(r["tokens"]) == 0
+
+
+def test_eou_closed_forms(tmp_path):
+    V1 = 36
+    bias = np.zeros(V1, np.float32)
+    bias[33] = 1.0                                          # <EOU> always
+    om = _scripted(tmp_path, small_eou, bias)
+    st = om.new_state()
+    r = om.decode_window(np.zeros((6, 64), np.float32), st, 5, tokens_before=3)
+    assert r["steps"] == 6 and r["segments"].tolist() == [3]
+    assert st.st.last_token == 35 and st.st.segment_start_token == 3
+    bias = np.zeros(V1, np.float32)
+    bias[12] = 1.0                                          # ordinary token always
+    om = _scripted(tmp_path, small_eou, bias, name="t.gguf")
+    st = om.new_state()
+    r = om.decode_window(np.zeros((4, 64), np.float32), st, 5)
+    assert r["tokens"].tolist() == [12] * 20 and r["steps"] == 20
+    assert st.st.symbols_this_step == 5
+
+
+def test_chunked_equals_one_shot(oracle_mod, tmp_path):
+    from parakeet_amd import gguf, synth
+    small_tdt(str(tmp_path / "m.gguf"))
+    om = oracle_mod.OracleModel.from_gguf(str(tmp_path / "m.gguf"), gguf)
+    enc = synth.encoder_frames(5, 37, 128)
+    one = om.decode_window(enc, om.new_state(), 10)["tokens"].tolist()
+    for chunk in (3, 4, 8):
+        st = om.new_state()
+        toks = []
+        for s0 in range(0, 37, chunk):
+            toks += om.decode_window(enc[s0:s0 + chunk], st, 10)["tokens"].tolist()
+        assert toks == one, chunk
+
+
+def test_replay_flags_planted_mistake(oracle_mod, tmp_path):
+    from parakeet_amd import gguf, synth
+    small_tdt(str(tmp_path / "m.gguf"))
+    om = oracle_mod.OracleModel.from_gguf(str(tmp_path / "m.gguf"), gguf)
+    enc = synth.encoder_frames(9, 30, 128)
+    r = om.decode_window(enc, om.new_state(), 10, trace=True)
+    ok = om.replay_window(enc, om.new_state(), 10, r["trace"])
+    assert ok["stats"]["unexplained"] == 0 and ok["stats"]["structure_error"] == 0
+    assert ok["tokens"].tolist() == r["tokens"].tolist()
+    bad = r["trace"].copy()
+    bad[3, 0] = (bad[3, 0] + 1) % 61                     # a wrong token at step 3
+    rep = om.replay_window(enc, om.new_state(), 10, bad)
+    assert rep["stats"]["unexplained"] >= 1 and rep["stats"]["first_unexplained"] == 3
+
+
+def test_batch_driver_matches_single(oracle_mod, tmp_path):
+    from parakeet_amd import gguf, synth
+    small_tdt(str(tmp_path / "m.gguf"))
+    om = oracle_mod.OracleModel.from_gguf(str(tmp_path / "m.gguf"), gguf)
+    encs = [synth.encoder_frames(u, 10 + 3 * u, 128) for u in range(6)]
+    bb = np.array([0, 2, 4, 0, 2, 4], np.float32)
+    b = om.decode_batch(encs, 10, blank_bias=bb, n_threads=3)
+    assert b["rc"] == 0
+    for u, e in enumerate(encs):
+        r = om.decode_window(e, om.new_state(), 10, blank_bias=float(bb[u]))
+        assert b["tokens"][u].tolist() == r["tokens"].tolist() and b["steps"][u] == r["steps"]
+
+
+def test_carry_larger_than_window_is_dropped(tmp_path):
+    """Reference quirk kept on purpose: a carry that exceeds the next window is
+    consumed only up to that window's length, then overwritten with
+    max(0, t - n) (src/parakeet_tdt.cpp:906-910, 979)."""
+    V1 = 62
+    bias = np.zeros(V1 + 5, np.float32)
+    bias[7], bias[V1 + 4] = 1.0, 1.0            # token 7, duration 4, always
+    om = _scripted(tmp_path, small_tdt, bias)
+    st = om.new_state()
+    om.decode_window(np.zeros((1, 128), np.float32), st, 10)
+    assert st.st.carry_frames == 3
+    r = om.decode_window(np.zeros((1, 128), np.float32), st, 10)
+    assert r["steps"] == 0 and st.st.carry_frames == 0   # 2 frames of carry dropped
+    r = om.decode_window(np.zeros((1, 128), np.float32), st, 10)
+    assert r["steps"] == 1
