@@ -1,0 +1,193 @@
+// parakeet_decoder.h -- C++ transducer decoder API, shaped like parakeet.cpp's
+// (src/parakeet_tdt.h, src/parakeet_eou.h, include/parakeet/engine.h), running
+// on the MI355X kernels of libparakeet_hip.so through the C ABI in
+// parakeet_hip.h.
+//
+// Same names, argument meanings and status codes as the reference, so the
+// Engine call sites (src/parakeet_engine.cpp:273-297, 409-452, 808-838) keep
+// their shape.  Differences, all on purpose:
+//   - the model is decoder-only: load_from_gguf reads the prediction / joint
+//     tensors and the metadata; encoder tensors are not required;
+//   - decode state lives in a device slot of the runtime (the reference's GPU
+//     path also keeps h/c/pred on the device, src/parakeet_tdt.cpp:845-847, but
+//     shared per runtime; here every TdtDecodeState / EouDecodeState owns its
+//     own slot, which is the reference CPU path's semantics).  The host vectors
+//     h_state / c_state / pred_out stay empty, as on the reference GPU path;
+//   - *_decode_batch entry points decode many utterances in one lockstep launch.
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+struct pk_decoder;
+
+namespace parakeet {
+
+enum class ParakeetModelType { CTC, TDT, EOU, SORTFORMER };
+
+// src/sentencepiece_bpe.h: pieces plus the ids detokenize skips.
+struct BpeVocab {
+    std::vector<std::string> pieces;
+    int32_t blank_id = -1, unk_id = -1, bos_id = -1, eos_id = -1, pad_id = -1;
+};
+
+// The decoder fields of the reference's EncoderConfig (src/parakeet_ctc.h).
+struct EncoderConfig {
+    int d_model = 1024;
+    int tdt_pred_hidden = 640, tdt_pred_rnn_layers = 2, tdt_joint_hidden = 640, tdt_num_durations = 5;
+    int eou_pred_hidden = 640, eou_pred_rnn_layers = 1, eou_joint_hidden = 640;
+    int eou_max_symbols_per_step = 5;
+};
+
+struct ParakeetCtcModel {
+    ParakeetModelType model_type = ParakeetModelType::CTC;
+    EncoderConfig encoder_cfg;
+    BpeVocab vocab;
+    int32_t blank_id = 1024;
+    int32_t vocab_size = 1025;
+    int32_t eou_id = -1;
+    int32_t eob_id = -1;
+    std::vector<int32_t> tdt_durations;
+
+    struct Impl;
+    std::shared_ptr<Impl> impl;   // GGUF bytes + tensor directory
+};
+using ParakeetModel = ParakeetCtcModel;
+
+// src/parakeet_ctc.cpp:297.  Returns 0, or the reference's codes: 1 open
+// failure, 2 wrong architecture / missing decoder tensor.
+int load_from_gguf(const std::string &gguf_path, ParakeetCtcModel &out_model, int n_threads = 0,
+                   int n_gpu_layers = 1, bool verbose = false);
+
+namespace detail { struct SlotPool; struct SlotLease; }
+
+// ---- TDT (src/parakeet_tdt.h) ----
+
+struct TdtRuntimeWeights {
+    int H_pred = 640, H_joint = 640, D_enc = 1024, V_plus_1 = 8193, V_out = 8198, L = 2, num_durations = 5;
+    const ParakeetCtcModel *weights_model = nullptr;
+    std::shared_ptr<detail::SlotPool> pool;   // device decoder + state slots
+    bool ready() const { return pool != nullptr; }
+};
+
+struct TdtDecodeOptions {
+    int max_symbols_per_step = 10;
+};
+
+struct TdtDecodeResult {
+    std::vector<int32_t> token_ids;
+    std::string text;
+    int steps = 0;
+    double decode_ms = 0.0;
+};
+
+struct TdtDecodeState {
+    std::vector<float> h_state;   // left empty: state lives on the device
+    std::vector<float> c_state;
+    std::vector<float> pred_out;
+    int symbols_this_step = 0;    // mirrored from the device after every window
+    bool initialized = false;
+    int carry_frames = 0;
+    std::shared_ptr<detail::SlotLease> slot;
+};
+
+// n_slots: concurrent decode states the runtime can hold (default 1024).
+int tdt_prepare_runtime(const ParakeetCtcModel &model, TdtRuntimeWeights &out, int n_slots = 1024);
+void tdt_init_state(TdtRuntimeWeights &W, int blank_id, TdtDecodeState &state);
+int tdt_decode_window(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const float *encoder_out_window,
+                      int n_frames, int D_enc, const TdtDecodeOptions &opts, TdtDecodeState &state,
+                      std::vector<int32_t> &out_tokens, int &out_steps);
+int tdt_greedy_decode(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const float *encoder_out, int T_enc,
+                      int D_enc, const TdtDecodeOptions &opts, TdtDecodeResult &result);
+// Batched: utterance u decodes enc[u][0 .. n_frames[u]) with states[u].
+int tdt_decode_batch(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const std::vector<const float *> &enc,
+                     const std::vector<int> &n_frames, int D_enc, const TdtDecodeOptions &opts,
+                     const std::vector<TdtDecodeState *> &states, std::vector<std::vector<int32_t>> &out_tokens,
+                     std::vector<int> &out_steps);
+
+// ---- EOU (src/parakeet_eou.h) ----
+
+struct EouRuntimeWeights {
+    int H_pred = 640, H_joint = 640, D_enc = 512, V_plus_1 = 1027, L = 1;
+    int blank_id = 1026, eou_id = 1024, eob_id = 1025;
+    std::shared_ptr<detail::SlotPool> pool;
+};
+
+struct EouDecodeOptions {
+    int max_symbols_per_step = 5;
+};
+
+struct EouDecodeState {
+    std::vector<float> h_state, c_state, pred_out;   // left empty: state lives on the device
+    int32_t last_token = -1;
+    int symbols_this_step = 0;
+    bool initialized = false;
+    int segment_start_token = 0;
+    std::shared_ptr<detail::SlotLease> slot;
+};
+
+struct EouSegmentBoundary {
+    int token_index = 0;
+    bool is_eou_flush = true;
+};
+
+struct EouDecodeResult {
+    std::vector<int32_t> token_ids;
+    std::vector<EouSegmentBoundary> segments;
+    std::string text;
+    int steps = 0;
+    int eou_count = 0;
+    double decode_ms = 0.0;
+};
+
+int eou_prepare_runtime(const ParakeetCtcModel &model, EouRuntimeWeights &out, int n_slots = 1024);
+void eou_init_state(const EouRuntimeWeights &W, EouDecodeState &state);
+int eou_decode_window(const ParakeetCtcModel &model, const EouRuntimeWeights &W, const float *encoder_out_window,
+                      int n_frames, int D_enc, const EouDecodeOptions &opts, EouDecodeState &state,
+                      std::vector<int32_t> &out_tokens, std::vector<EouSegmentBoundary> &out_segments,
+                      int &out_steps);
+int eou_greedy_decode(const ParakeetCtcModel &model, const EouRuntimeWeights &W, const float *encoder_out,
+                      int T_enc, int D_enc, const EouDecodeOptions &opts, EouDecodeResult &result);
+int eou_decode_batch(const ParakeetCtcModel &model, const EouRuntimeWeights &W, const std::vector<const float *> &enc,
+                     const std::vector<int> &n_frames, int D_enc, const EouDecodeOptions &opts,
+                     const std::vector<EouDecodeState *> &states, std::vector<std::vector<int32_t>> &out_tokens,
+                     std::vector<std::vector<EouSegmentBoundary>> &out_segments, std::vector<int> &out_steps);
+
+// src/sentencepiece_bpe.cpp:9-38: pieces joined (blank/bos/eos/pad skipped), U+2581 -> ' ',
+// leading spaces trimmed.
+std::string detokenize(const BpeVocab &vocab, const std::vector<int32_t> &ids);
+
+// ---- Engine-shaped front (include/parakeet/engine.h) over encoder features ----
+
+struct EngineOptions {
+    std::string model_gguf_path;
+    int n_slots = 1024;
+};
+
+struct EngineResult {
+    std::string text;
+    std::vector<int32_t> token_ids;
+    double decode_ms = 0.0;
+    int encoder_frames = 0;
+    int steps = 0;
+};
+
+class Engine {
+public:
+    explicit Engine(const EngineOptions &opts);   // throws std::runtime_error, as the reference does
+    ~Engine();
+    // The decode half of Engine::transcribe_samples (src/parakeet_engine.cpp:271-317),
+    // dispatched on parakeet.model.type: features are the encoder output [T][D].
+    EngineResult transcribe_features(const float *encoder_out, int T_enc, int D_enc);
+    std::vector<EngineResult> transcribe_features_batch(const std::vector<const float *> &encoder_out,
+                                                        const std::vector<int> &T_enc, int D_enc);
+    const ParakeetCtcModel &model() const;
+
+private:
+    struct Impl;
+    std::unique_ptr<Impl> pimpl_;
+};
+
+}  // namespace parakeet

@@ -1,0 +1,606 @@
+// parakeet_decoder.cpp -- the reference-shaped C++ decoder API on top of the
+// C ABI (parakeet_hip.h).  See include/parakeet_decoder.h.
+#include "parakeet_decoder.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <stdexcept>
+
+#include "gguf_reader.h"
+#include "parakeet_hip.h"
+
+namespace parakeet {
+
+struct ParakeetCtcModel::Impl {
+    gguf::File file;
+};
+
+namespace detail {
+
+// The device decoder of one runtime and its pool of state slots.
+struct SlotPool {
+    pk_decoder *dec = nullptr;
+    std::mutex mu;
+    std::vector<int> free_slots;
+    ~SlotPool() { if (dec) pk_decoder_destroy(dec); }
+    int acquire() {
+        std::lock_guard<std::mutex> lk(mu);
+        if (free_slots.empty()) return -1;
+        const int s = free_slots.back();
+        free_slots.pop_back();
+        return s;
+    }
+    void release(int s) {
+        std::lock_guard<std::mutex> lk(mu);
+        free_slots.push_back(s);
+    }
+};
+
+// A state's claim on one slot, returned to the pool when the state goes away.
+struct SlotLease {
+    std::shared_ptr<SlotPool> pool;
+    int slot = -1;
+    ~SlotLease() { if (pool && slot >= 0) pool->release(slot); }
+};
+
+}  // namespace detail
+
+namespace {
+
+const char *prefix(ParakeetModelType t) { return t == ParakeetModelType::EOU ? "eou." : "tdt."; }
+
+pk_tensor tensor_of(const ParakeetCtcModel &m, const std::string &name) {
+    pk_tensor t{};
+    const gguf::Tensor *g = m.impl ? m.impl->file.tensor(name) : nullptr;
+    if (!g) return t;
+    t.data = g->data;
+    t.type = (int32_t)g->type;
+    t.ne0 = g->ne.empty() ? 0 : g->ne[0];
+    t.ne1 = g->ne.size() > 1 ? g->ne[1] : 1;
+    return t;
+}
+
+// Decoder description from the loaded model (the tensors bound at
+// src/parakeet_ctc.cpp:603-665 and the metadata read at :418-458).
+int make_pool(const ParakeetCtcModel &m, int n_slots, std::shared_ptr<detail::SlotPool> &out) {
+    pk_decoder_desc d{};
+    const bool eou = m.model_type == ParakeetModelType::EOU;
+    const EncoderConfig &c = m.encoder_cfg;
+    d.kind = eou ? PK_KIND_EOU : PK_KIND_TDT;
+    d.pred_hidden = eou ? c.eou_pred_hidden : c.tdt_pred_hidden;
+    d.pred_rnn_layers = eou ? c.eou_pred_rnn_layers : c.tdt_pred_rnn_layers;
+    d.joint_hidden = eou ? c.eou_joint_hidden : c.tdt_joint_hidden;
+    d.d_enc = c.d_model;
+    d.vocab_size = m.vocab_size;
+    d.blank_id = m.blank_id;
+    d.num_durations = eou ? 0 : c.tdt_num_durations;
+    d.n_duration_values = eou ? 0 : (int32_t)std::min<size_t>(m.tdt_durations.size(), PK_MAX_DURATIONS);
+    for (int i = 0; i < d.n_duration_values; ++i) d.durations[i] = m.tdt_durations[i];
+    d.eou_id = m.eou_id;
+    d.eob_id = m.eob_id;
+    std::vector<uint8_t> special(m.vocab.pieces.size());
+    for (size_t i = 0; i < special.size(); ++i) {
+        const std::string &p = m.vocab.pieces[i];
+        special[i] = (!p.empty() && p.front() == '<' && p.back() == '>') ? 1 : 0;
+    }
+    d.special = special.empty() ? nullptr : special.data();
+    d.n_special = (int32_t)special.size();
+    const std::string p = prefix(m.model_type);
+    d.embed = tensor_of(m, p + "predict.embed.weight");
+    if (d.pred_rnn_layers > PK_MAX_LAYERS) return 2;
+    for (int l = 0; l < d.pred_rnn_layers; ++l) {
+        const std::string pl = p + "predict.lstm." + std::to_string(l) + ".";
+        d.w_ih[l] = tensor_of(m, pl + "w_ih");
+        d.w_hh[l] = tensor_of(m, pl + "w_hh");
+        d.b_ih[l] = tensor_of(m, pl + "b_ih");
+        d.b_hh[l] = tensor_of(m, pl + "b_hh");
+    }
+    d.joint_enc_w = tensor_of(m, p + "joint.enc.weight");
+    d.joint_enc_b = tensor_of(m, p + "joint.enc.bias");
+    d.joint_pred_w = tensor_of(m, p + "joint.pred.weight");
+    d.joint_pred_b = tensor_of(m, p + "joint.pred.bias");
+    d.joint_out_w = tensor_of(m, p + "joint.out.weight");
+    d.joint_out_b = tensor_of(m, p + "joint.out.bias");
+    auto pool = std::make_shared<detail::SlotPool>();
+    if (int rc = pk_decoder_create(&d, n_slots, &pool->dec)) {
+        std::fprintf(stderr, "prepare_runtime: %s\n", pk_last_error());
+        return rc;
+    }
+    for (int s = n_slots - 1; s >= 0; --s) pool->free_slots.push_back(s);
+    out = std::move(pool);
+    return 0;
+}
+
+std::shared_ptr<detail::SlotLease> lease(const std::shared_ptr<detail::SlotPool> &pool) {
+    const int s = pool->acquire();
+    if (s < 0) throw std::runtime_error("parakeet: no free decoder state slot");
+    auto l = std::make_shared<detail::SlotLease>();
+    l->pool = pool;
+    l->slot = s;
+    return l;
+}
+
+// One batched device call; fills per-utterance tokens/steps (+ EOU segments).
+int run_batch(detail::SlotPool &pool, int D_enc, int max_symbols, const std::vector<const float *> &enc,
+              const std::vector<int> &n_frames, const std::vector<int> &slots, const std::vector<int> &tokens_base,
+              std::vector<std::vector<int32_t>> &tokens, std::vector<std::vector<int32_t>> *segments,
+              std::vector<int> &steps) {
+    const int n = (int)enc.size();
+    int64_t rows = 0;
+    int max_T = 0;
+    std::vector<int64_t> row(n);
+    for (int u = 0; u < n; ++u) {
+        row[u] = rows;
+        rows += std::max(0, n_frames[u]);
+        max_T = std::max(max_T, n_frames[u]);
+    }
+    std::vector<float> packed((size_t)std::max<int64_t>(rows, 1) * D_enc);
+    for (int u = 0; u < n; ++u)
+        if (n_frames[u] > 0)
+            memcpy(packed.data() + (size_t)row[u] * D_enc, enc[u], sizeof(float) * (size_t)n_frames[u] * D_enc);
+    const int cap = max_T * std::max(1, max_symbols) + 1;
+    std::vector<int32_t> tok((size_t)n * cap), ntok(n), st(n), seg((size_t)n * (cap + 1)), nseg(n);
+    std::vector<int32_t> T(n_frames.begin(), n_frames.end()), sl(slots.begin(), slots.end());
+    std::vector<int32_t> base(tokens_base.begin(), tokens_base.end());
+    pk_batch b{};
+    b.n_utts = n;
+    b.mem = PK_MEM_HOST;
+    b.d_enc = D_enc;
+    b.max_symbols = max_symbols;
+    b.enc = packed.data();
+    b.enc_row = row.data();
+    b.n_frames = T.data();
+    b.slot = sl.data();
+    b.tokens_base = base.empty() ? nullptr : base.data();
+    b.tokens = tok.data();
+    b.token_cap = cap;
+    b.n_tokens = ntok.data();
+    b.steps = st.data();
+    b.segments = seg.data();
+    b.seg_cap = cap + 1;
+    b.n_segments = nseg.data();
+    if (int rc = pk_decode(pool.dec, &b)) {
+        std::fprintf(stderr, "decode: %s\n", pk_last_error());
+        return rc;
+    }
+    tokens.assign(n, {});
+    if (segments) segments->assign(n, {});
+    steps.assign(n, 0);
+    for (int u = 0; u < n; ++u) {
+        tokens[u].assign(tok.begin() + (size_t)u * cap, tok.begin() + (size_t)u * cap + ntok[u]);
+        steps[u] = st[u];
+        if (segments)
+            (*segments)[u].assign(seg.begin() + (size_t)u * (cap + 1), seg.begin() + (size_t)u * (cap + 1) + nseg[u]);
+    }
+    return 0;
+}
+
+void read_ctrl(detail::SlotPool &pool, int slot, int32_t *ctrl) {
+    if (pk_slot_read(pool.dec, slot, nullptr, nullptr, nullptr, ctrl) != 0)
+        throw std::runtime_error(std::string("parakeet: slot read failed: ") + pk_last_error());
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ loading
+
+int load_from_gguf(const std::string &gguf_path, ParakeetCtcModel &out, int, int, bool verbose) {
+    auto impl = std::make_shared<ParakeetCtcModel::Impl>();
+    std::string err;
+    if (impl->file.open(gguf_path, err)) {
+        std::fprintf(stderr, "gguf: %s\n", err.c_str());
+        return 1;
+    }
+    const gguf::File &g = impl->file;
+    if (g.get_str("general.architecture", "") != "parakeet-ctc") {
+        std::fprintf(stderr, "gguf: expected arch=parakeet-ctc\n");
+        return 2;
+    }
+    out = ParakeetCtcModel{};
+    out.encoder_cfg.d_model = (int)g.get_u32("parakeet.encoder.d_model", 1024);
+    const std::string mt = g.get_str("parakeet.model.type", "ctc");
+    out.model_type = mt == "tdt" ? ParakeetModelType::TDT
+                   : mt == "eou" ? ParakeetModelType::EOU
+                   : mt == "sortformer" ? ParakeetModelType::SORTFORMER : ParakeetModelType::CTC;
+    EncoderConfig &c = out.encoder_cfg;
+    if (out.model_type == ParakeetModelType::TDT) {
+        c.tdt_pred_hidden = (int)g.get_u32("parakeet.tdt.pred_hidden", 640);
+        c.tdt_pred_rnn_layers = (int)g.get_u32("parakeet.tdt.pred_rnn_layers", 2);
+        c.tdt_joint_hidden = (int)g.get_u32("parakeet.tdt.joint_hidden", 640);
+        c.tdt_num_durations = (int)g.get_u32("parakeet.tdt.num_durations", 5);
+        out.vocab_size = (int32_t)g.get_u32("parakeet.tdt.vocab_size", 8192);
+        out.blank_id = (int32_t)g.get_u32("parakeet.tdt.blank_id", (uint32_t)out.vocab_size);
+        if (const gguf::Value *v = g.find("parakeet.tdt.durations"))
+            out.tdt_durations.assign(v->arr_i.begin(), v->arr_i.end());
+        else
+            out.tdt_durations = {0, 1, 2, 3, 4};
+    } else if (out.model_type == ParakeetModelType::EOU) {
+        c.eou_pred_hidden = (int)g.get_u32("parakeet.eou.pred_hidden", 640);
+        c.eou_pred_rnn_layers = (int)g.get_u32("parakeet.eou.pred_rnn_layers", 1);
+        c.eou_joint_hidden = (int)g.get_u32("parakeet.eou.joint_hidden", 640);
+        c.eou_max_symbols_per_step = (int)g.get_u32("parakeet.eou.max_symbols_per_step", 5);
+        out.vocab_size = (int32_t)g.get_u32("parakeet.eou.vocab_size", 1026);
+        out.blank_id = (int32_t)g.get_u32("parakeet.eou.blank_id", (uint32_t)out.vocab_size);
+        out.eou_id = g.find("parakeet.eou.eou_id") ? g.get_i32("parakeet.eou.eou_id", -1) : -1;
+        out.eob_id = g.find("parakeet.eou.eob_id") ? g.get_i32("parakeet.eou.eob_id", -1) : -1;
+    }
+    out.vocab.blank_id = out.blank_id;
+    if (const gguf::Value *v = g.find("tokenizer.ggml.tokens")) out.vocab.pieces = v->arr_s;
+    out.vocab.unk_id = (int32_t)g.get_u32("tokenizer.ggml.unk_token_id", (uint32_t)-1);
+    out.vocab.bos_id = (int32_t)g.get_u32("tokenizer.ggml.bos_token_id", (uint32_t)-1);
+    out.vocab.eos_id = (int32_t)g.get_u32("tokenizer.ggml.eos_token_id", (uint32_t)-1);
+    out.vocab.pad_id = (int32_t)g.get_u32("tokenizer.ggml.pad_token_id", (uint32_t)-1);
+    out.impl = impl;
+    if (out.model_type == ParakeetModelType::TDT || out.model_type == ParakeetModelType::EOU) {
+        const std::string p = prefix(out.model_type);
+        const int L = out.model_type == ParakeetModelType::TDT ? c.tdt_pred_rnn_layers : c.eou_pred_rnn_layers;
+        std::vector<std::string> need = {p + "predict.embed.weight", p + "joint.enc.weight", p + "joint.enc.bias",
+                                         p + "joint.pred.weight", p + "joint.pred.bias", p + "joint.out.weight",
+                                         p + "joint.out.bias"};
+        for (int l = 0; l < L; ++l)
+            for (const char *n : {"w_ih", "w_hh", "b_ih", "b_hh"})
+                need.push_back(p + "predict.lstm." + std::to_string(l) + "." + n);
+        for (const auto &n : need)
+            if (!g.tensor(n)) {
+                std::fprintf(stderr, "gguf: missing tensor %s\n", n.c_str());
+                return 2;
+            }
+    }
+    if (verbose)
+        std::fprintf(stderr, "gguf: %s type=%s vocab=%d blank=%d\n", gguf_path.c_str(), mt.c_str(), out.vocab_size,
+                     out.blank_id);
+    return 0;
+}
+
+std::string detokenize(const BpeVocab &vocab, const std::vector<int32_t> &ids) {
+    std::string out;
+    out.reserve(ids.size() * 3);
+    for (int32_t id : ids) {
+        if (id < 0 || id >= (int32_t)vocab.pieces.size()) continue;
+        if (id == vocab.blank_id || id == vocab.bos_id || id == vocab.eos_id || id == vocab.pad_id) continue;
+        const std::string &piece = vocab.pieces[id];
+        for (size_t i = 0; i < piece.size();) {
+            if ((unsigned char)piece[i] == 0xE2 && i + 2 < piece.size() && (unsigned char)piece[i + 1] == 0x96 &&
+                (unsigned char)piece[i + 2] == 0x81) {
+                out.push_back(' ');
+                i += 3;
+            } else {
+                out.push_back(piece[i++]);
+            }
+        }
+    }
+    size_t start = 0;
+    while (start < out.size() && out[start] == ' ') ++start;
+    out.erase(0, start);
+    return out;
+}
+
+// ------------------------------------------------------------------ TDT
+
+int tdt_prepare_runtime(const ParakeetCtcModel &model, TdtRuntimeWeights &W, int n_slots) {
+    W = TdtRuntimeWeights{};
+    if (model.model_type != ParakeetModelType::TDT || !model.impl) return 2;
+    const EncoderConfig &c = model.encoder_cfg;
+    W.H_pred = c.tdt_pred_hidden;
+    W.H_joint = c.tdt_joint_hidden;
+    W.D_enc = c.d_model;
+    W.L = c.tdt_pred_rnn_layers;
+    W.num_durations = c.tdt_num_durations;
+    W.V_plus_1 = model.vocab_size + 1;
+    W.V_out = W.V_plus_1 + W.num_durations;
+    W.weights_model = &model;
+    return make_pool(model, n_slots, W.pool);
+}
+
+void tdt_init_state(TdtRuntimeWeights &W, int, TdtDecodeState &state) {
+    if (!state.slot) state.slot = lease(W.pool);
+    if (pk_slot_init(W.pool->dec, state.slot->slot) != 0)
+        throw std::runtime_error(std::string("tdt_init_state: ") + pk_last_error());
+    state.symbols_this_step = 0;
+    state.carry_frames = 0;
+    state.h_state.clear();
+    state.c_state.clear();
+    state.pred_out.clear();
+    state.initialized = true;
+}
+
+int tdt_decode_batch(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const std::vector<const float *> &enc,
+                     const std::vector<int> &n_frames, int D_enc, const TdtDecodeOptions &opts,
+                     const std::vector<TdtDecodeState *> &states, std::vector<std::vector<int32_t>> &out_tokens,
+                     std::vector<int> &out_steps) {
+    const int n = (int)enc.size();
+    out_steps.assign(n, 0);
+    out_tokens.assign(n, {});
+    if (D_enc != W.D_enc) {
+        std::fprintf(stderr, "tdt_decode_window: encoder d_model mismatch (%d vs %d)\n", D_enc, W.D_enc);
+        return 1;
+    }
+    if ((int)n_frames.size() != n || (int)states.size() != n) return 3;
+    std::vector<int> idx, slots, T;
+    std::vector<const float *> e;
+    for (int u = 0; u < n; ++u) {
+        if (n_frames[u] <= 0) continue;   // src/parakeet_tdt.cpp:879
+        if (!states[u]->initialized) tdt_init_state(W, model.blank_id, *states[u]);
+        idx.push_back(u);
+        slots.push_back(states[u]->slot->slot);
+        T.push_back(n_frames[u]);
+        e.push_back(enc[u]);
+    }
+    for (size_t i = 0; i < idx.size(); i += PK_MAX_BATCH) {
+        const size_t j = std::min(idx.size(), i + PK_MAX_BATCH);
+        std::vector<const float *> ee(e.begin() + i, e.begin() + j);
+        std::vector<int> tt(T.begin() + i, T.begin() + j), ss(slots.begin() + i, slots.begin() + j);
+        std::vector<std::vector<int32_t>> toks;
+        std::vector<int> steps;
+        if (int rc = run_batch(*W.pool, D_enc, opts.max_symbols_per_step, ee, tt, ss, {}, toks, nullptr, steps))
+            return rc;
+        for (size_t k = i; k < j; ++k) {
+            const int u = idx[k];
+            out_tokens[u] = std::move(toks[k - i]);
+            out_steps[u] = steps[k - i];
+            int32_t ctrl[PK_CTRL_N];
+            read_ctrl(*W.pool, slots[k], ctrl);
+            states[u]->symbols_this_step = ctrl[PK_CTRL_SYM];
+            states[u]->carry_frames = ctrl[PK_CTRL_CARRY];
+        }
+    }
+    return 0;
+}
+
+int tdt_decode_window(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const float *encoder_out_window,
+                      int n_frames, int D_enc, const TdtDecodeOptions &opts, TdtDecodeState &state,
+                      std::vector<int32_t> &out_tokens, int &out_steps) {
+    std::vector<std::vector<int32_t>> toks;
+    std::vector<int> steps;
+    const int rc = tdt_decode_batch(model, W, {encoder_out_window}, {n_frames}, D_enc, opts, {&state}, toks, steps);
+    out_steps = steps.empty() ? 0 : steps[0];
+    if (rc == 0) out_tokens.insert(out_tokens.end(), toks[0].begin(), toks[0].end());
+    return rc;
+}
+
+int tdt_greedy_decode(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const float *encoder_out, int T_enc,
+                      int D_enc, const TdtDecodeOptions &opts, TdtDecodeResult &result) {
+    const auto t0 = std::chrono::steady_clock::now();
+    TdtDecodeState state;
+    result.token_ids.clear();
+    result.token_ids.reserve(T_enc);
+    if (int rc = tdt_decode_window(model, W, encoder_out, T_enc, D_enc, opts, state, result.token_ids, result.steps))
+        return rc;
+    result.text = detokenize(model.vocab, result.token_ids);
+    result.decode_ms =
+        std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::steady_clock::now() - t0).count() / 1000.0;
+    return 0;
+}
+
+// ------------------------------------------------------------------ EOU
+
+int eou_prepare_runtime(const ParakeetCtcModel &model, EouRuntimeWeights &W, int n_slots) {
+    if (model.model_type != ParakeetModelType::EOU) return 1;   // src/parakeet_eou.cpp:173-175
+    const EncoderConfig &c = model.encoder_cfg;
+    W = EouRuntimeWeights{};
+    W.H_pred = c.eou_pred_hidden;
+    W.H_joint = c.eou_joint_hidden;
+    W.D_enc = c.d_model;
+    W.L = c.eou_pred_rnn_layers;
+    W.V_plus_1 = model.vocab_size + 1;
+    W.blank_id = model.blank_id;
+    W.eou_id = model.eou_id >= 0 ? model.eou_id : model.vocab_size - 2;
+    W.eob_id = model.eob_id >= 0 ? model.eob_id : model.vocab_size - 1;
+    return make_pool(model, n_slots, W.pool);
+}
+
+void eou_init_state(const EouRuntimeWeights &W, EouDecodeState &state) {
+    if (!state.slot) state.slot = lease(W.pool);
+    if (pk_slot_init(W.pool->dec, state.slot->slot) != 0)
+        throw std::runtime_error(std::string("eou_init_state: ") + pk_last_error());
+    state.h_state.clear();
+    state.c_state.clear();
+    state.pred_out.clear();
+    state.last_token = -1;
+    state.symbols_this_step = 0;
+    state.segment_start_token = 0;
+    state.initialized = true;
+}
+
+int eou_decode_batch(const ParakeetCtcModel &, const EouRuntimeWeights &W, const std::vector<const float *> &enc,
+                     const std::vector<int> &n_frames, int D_enc, const EouDecodeOptions &opts,
+                     const std::vector<EouDecodeState *> &states, std::vector<std::vector<int32_t>> &out_tokens,
+                     std::vector<std::vector<EouSegmentBoundary>> &out_segments, std::vector<int> &out_steps) {
+    const int n = (int)enc.size();
+    out_tokens.assign(n, {});
+    out_segments.assign(n, {});
+    out_steps.assign(n, 0);
+    if (D_enc != W.D_enc) {
+        std::fprintf(stderr, "eou_decode_window: encoder d_model mismatch (%d vs %d)\n", D_enc, W.D_enc);
+        return 1;
+    }
+    if ((int)n_frames.size() != n || (int)states.size() != n) return 3;
+    std::vector<int> slots(n), base(n, 0);
+    for (int u = 0; u < n; ++u) {
+        if (!states[u]->initialized) eou_init_state(W, *states[u]);
+        slots[u] = states[u]->slot->slot;
+    }
+    for (int i = 0; i < n; i += PK_MAX_BATCH) {
+        const int j = std::min(n, i + PK_MAX_BATCH);
+        std::vector<const float *> ee(enc.begin() + i, enc.begin() + j);
+        std::vector<int> tt(n_frames.begin() + i, n_frames.begin() + j), ss(slots.begin() + i, slots.begin() + j);
+        std::vector<int> bb(base.begin() + i, base.begin() + j);
+        std::vector<std::vector<int32_t>> toks, segs;
+        std::vector<int> steps;
+        if (int rc = run_batch(*W.pool, D_enc, opts.max_symbols_per_step, ee, tt, ss, bb, toks, &segs, steps))
+            return rc;
+        for (int u = i; u < j; ++u) {
+            out_tokens[u] = std::move(toks[u - i]);
+            out_steps[u] = steps[u - i];
+            for (int32_t s : segs[u - i]) out_segments[u].push_back(EouSegmentBoundary{s, true});
+            int32_t ctrl[PK_CTRL_N];
+            read_ctrl(*W.pool, slots[u], ctrl);
+            states[u]->symbols_this_step = ctrl[PK_CTRL_SYM];
+            states[u]->last_token = ctrl[PK_CTRL_LAST];
+            states[u]->segment_start_token = ctrl[PK_CTRL_SEGSTART];
+        }
+    }
+    return 0;
+}
+
+int eou_decode_window(const ParakeetCtcModel &model, const EouRuntimeWeights &W, const float *encoder_out_window,
+                      int n_frames, int D_enc, const EouDecodeOptions &opts, EouDecodeState &state,
+                      std::vector<int32_t> &out_tokens, std::vector<EouSegmentBoundary> &out_segments,
+                      int &out_steps) {
+    if (D_enc != W.D_enc) {
+        std::fprintf(stderr, "eou_decode_window: encoder d_model mismatch (%d vs %d)\n", D_enc, W.D_enc);
+        return 1;
+    }
+    if (!state.initialized) eou_init_state(W, state);
+    // segment indices count from the caller's token vector (src/parakeet_eou.cpp:293-298)
+    const int base = (int)out_tokens.size();
+    const int n = std::max(0, n_frames);
+    std::vector<int32_t> toks;
+    std::vector<int> steps;
+    std::vector<std::vector<int32_t>> tv, sv;
+    if (int rc = run_batch(*W.pool, D_enc, opts.max_symbols_per_step, {encoder_out_window}, {n},
+                           {state.slot->slot}, {base}, tv, &sv, steps))
+        return rc;
+    out_steps = steps[0];
+    out_tokens.insert(out_tokens.end(), tv[0].begin(), tv[0].end());
+    for (int32_t s : sv[0]) out_segments.push_back(EouSegmentBoundary{s, true});
+    int32_t ctrl[PK_CTRL_N];
+    read_ctrl(*W.pool, state.slot->slot, ctrl);
+    state.symbols_this_step = ctrl[PK_CTRL_SYM];
+    state.last_token = ctrl[PK_CTRL_LAST];
+    state.segment_start_token = ctrl[PK_CTRL_SEGSTART];
+    return 0;
+}
+
+namespace {
+std::string trim_spaces(const std::string &s) {
+    const size_t a = s.find_first_not_of(" \t\r\n");
+    if (a == std::string::npos) return std::string();
+    const size_t b = s.find_last_not_of(" \t\r\n");
+    return s.substr(a, b - a + 1);
+}
+}  // namespace
+
+int eou_greedy_decode(const ParakeetCtcModel &model, const EouRuntimeWeights &W, const float *encoder_out, int T_enc,
+                      int D_enc, const EouDecodeOptions &opts, EouDecodeResult &result) {
+    const auto t0 = std::chrono::steady_clock::now();
+    EouDecodeState state;
+    result.token_ids.clear();
+    result.segments.clear();
+    if (int rc = eou_decode_window(model, W, encoder_out, T_enc, D_enc, opts, state, result.token_ids,
+                                   result.segments, result.steps))
+        return rc;
+    result.eou_count = (int)result.segments.size();
+    // segments joined with '\n' (src/parakeet_eou.cpp:359-382)
+    int seg_start = 0;
+    std::string text;
+    for (size_t i = 0; i <= result.segments.size(); ++i) {
+        const int seg_end = i < result.segments.size() ? result.segments[i].token_index : (int)result.token_ids.size();
+        if (seg_end <= seg_start) { seg_start = seg_end; continue; }
+        std::vector<int32_t> seg(result.token_ids.begin() + seg_start, result.token_ids.begin() + seg_end);
+        std::string s = trim_spaces(detokenize(model.vocab, seg));
+        if (!s.empty()) {
+            if (!text.empty()) text += "\n";
+            text += s;
+        }
+        seg_start = seg_end;
+    }
+    result.text = std::move(text);
+    result.decode_ms =
+        std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::steady_clock::now() - t0).count() / 1000.0;
+    return 0;
+}
+
+// ------------------------------------------------------------------ Engine
+
+struct Engine::Impl {
+    EngineOptions opts;
+    ParakeetCtcModel model;
+    TdtRuntimeWeights tdt;
+    EouRuntimeWeights eou;
+};
+
+Engine::Engine(const EngineOptions &opts) : pimpl_(std::make_unique<Impl>()) {
+    pimpl_->opts = opts;
+    if (int rc = load_from_gguf(opts.model_gguf_path, pimpl_->model))
+        throw std::runtime_error("parakeet::Engine: failed to load GGUF '" + opts.model_gguf_path +
+                                 "' (rc=" + std::to_string(rc) + ")");
+    if (pimpl_->model.model_type == ParakeetModelType::TDT) {
+        if (tdt_prepare_runtime(pimpl_->model, pimpl_->tdt, opts.n_slots) != 0)
+            throw std::runtime_error("Engine: tdt_prepare_runtime failed");
+    } else if (pimpl_->model.model_type == ParakeetModelType::EOU) {
+        if (eou_prepare_runtime(pimpl_->model, pimpl_->eou, opts.n_slots) != 0)
+            throw std::runtime_error("Engine: eou_prepare_runtime failed");
+    } else {
+        throw std::runtime_error("parakeet::Engine: loaded GGUF has no transducer decoder");
+    }
+}
+
+Engine::~Engine() = default;
+
+const ParakeetCtcModel &Engine::model() const { return pimpl_->model; }
+
+EngineResult Engine::transcribe_features(const float *enc, int T_enc, int D_enc) {
+    return transcribe_features_batch({enc}, {T_enc}, D_enc)[0];
+}
+
+std::vector<EngineResult> Engine::transcribe_features_batch(const std::vector<const float *> &enc,
+                                                            const std::vector<int> &T_enc, int D_enc) {
+    const auto t0 = std::chrono::steady_clock::now();
+    const int n = (int)enc.size();
+    std::vector<EngineResult> out(n);
+    const ParakeetCtcModel &m = pimpl_->model;
+    if (m.model_type == ParakeetModelType::TDT) {
+        std::vector<TdtDecodeState> states(n);
+        std::vector<TdtDecodeState *> sp(n);
+        for (int u = 0; u < n; ++u) sp[u] = &states[u];
+        std::vector<std::vector<int32_t>> toks;
+        std::vector<int> steps;
+        if (int rc = tdt_decode_batch(m, pimpl_->tdt, enc, T_enc, D_enc, TdtDecodeOptions{}, sp, toks, steps))
+            throw std::runtime_error("parakeet::Engine: tdt decode failed (rc=" + std::to_string(rc) + ")");
+        for (int u = 0; u < n; ++u) {
+            out[u].token_ids = std::move(toks[u]);
+            out[u].text = detokenize(m.vocab, out[u].token_ids);
+            out[u].steps = steps[u];
+        }
+    } else {
+        EouDecodeOptions o;
+        o.max_symbols_per_step = m.encoder_cfg.eou_max_symbols_per_step;
+        std::vector<EouDecodeState> states(n);
+        std::vector<EouDecodeState *> sp(n);
+        for (int u = 0; u < n; ++u) sp[u] = &states[u];
+        std::vector<std::vector<int32_t>> toks;
+        std::vector<std::vector<EouSegmentBoundary>> segs;
+        std::vector<int> steps;
+        if (int rc = eou_decode_batch(m, pimpl_->eou, enc, T_enc, D_enc, o, sp, toks, segs, steps))
+            throw std::runtime_error("parakeet::Engine: eou decode failed (rc=" + std::to_string(rc) + ")");
+        for (int u = 0; u < n; ++u) {
+            out[u].token_ids = std::move(toks[u]);
+            out[u].steps = steps[u];
+            int s0 = 0;
+            std::string text;
+            for (size_t i = 0; i <= segs[u].size(); ++i) {
+                const int e = i < segs[u].size() ? segs[u][i].token_index : (int)out[u].token_ids.size();
+                if (e > s0) {
+                    std::vector<int32_t> seg(out[u].token_ids.begin() + s0, out[u].token_ids.begin() + e);
+                    std::string s = trim_spaces(detokenize(m.vocab, seg));
+                    if (!s.empty()) text += (text.empty() ? "" : "\n") + s;
+                }
+                s0 = e;
+            }
+            out[u].text = std::move(text);
+        }
+    }
+    const double ms =
+        std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::steady_clock::now() - t0).count() / 1000.0;
+    for (int u = 0; u < n; ++u) {
+        out[u].decode_ms = ms;
+        out[u].encoder_frames = T_enc[u];
+    }
+    return out;
+}
+
+}  // namespace parakeet
