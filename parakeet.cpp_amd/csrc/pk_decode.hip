@@ -35,624 +35,29 @@
 // reference's sequential row sums, so logits differ by f32 rounding only.
 
 #include <hip/hip_runtime.h>
-#include <hip/hip_fp16.h>
 
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
-#include <mutex>
 #include <string>
 #include <vector>
 
 #include "parakeet_hip.h"
+#include "pk_device.h"
 
 namespace {
 
-constexpr int kWave = 64;
-constexpr int kBlock = 256;
-constexpr int kWavesPerBlock = kBlock / kWave;
-constexpr int kMaxBatch = PK_MAX_BATCH;
-constexpr int kUC = 8;               // utterances per register tile
-constexpr int kIdxBits = 14;         // argmax key: index field
-constexpr int kStampShift = 46;      // argmax key: 14 index + 32 value bits below the stamp
-constexpr unsigned kMaxStamp = (1u << 18) - 1;
-
-// Flags in the per-utterance control word.
-constexpr int kFlagZeroHC = 1;       // LSTM input state is zero (init / EOU reset)
-constexpr int kFlagTokOverflow = 2;
-constexpr int kFlagSegOverflow = 4;
-constexpr int kFlagTraceOverflow = 8;
-
-struct DMat {
-    const void *w;       // int8 / f16 / f32 plane [rows][cols]
-    const float *d;      // q8_0 block scales [rows][cols/32], else null
-    int type;
-    int rows, cols;
-};
-
-struct KParams {
-    int kind, H, L, J, V1, Dn, Vo, blank, eou, eob, max_sym, n_dur;
-    int durations[PK_MAX_DURATIONS];
-    DMat embed;
-    DMat w_ih[PK_MAX_LAYERS], w_hh[PK_MAX_LAYERS];
-    const float *b_ih[PK_MAX_LAYERS], *b_hh[PK_MAX_LAYERS];
-    DMat w_pred, w_out;
-    const float *b_pred, *b_out;
-    const unsigned char *special;
-    int n_special;
-    // slot state
-    float *slot_h;       // [slots][2][L][H] ping-pong
-    float *slot_c;       // [slots][L][H]
-    float *slot_pp;      // [slots][J]  b_p + W_p . h[L-1]
-    int *slot_ctrl;      // [slots][PK_CTRL_N]
-    // batch
-    int n_utts;
-    const float *encp;           // [rows][J]
-    const long long *encp_row;   // [n_utts]
-    const int *T;
-    const int *slot;
-    const float *blank_bias;     // nullable
-    const int *tokens_base;      // nullable
-    int *tokens; int token_cap;
-    int *n_tokens; int *steps;
-    int *segs; int seg_cap; int *n_segs;
-    int *trace; int trace_cap;
-    // sync
-    unsigned *barrier;
-    unsigned long long *keys;    // [2][n_utts][2]
-    int *status;                 // [0] error code, [1] iterations
-    int max_iter;
-};
-
-// ---------------------------------------------------------------- helpers
-
-__device__ __forceinline__ float4 load_w4(const DMat &m, int r, int k) {
-    if (m.type == PK_TYPE_Q8_0) {
-        const int packed = *reinterpret_cast<const int *>(
-            static_cast<const signed char *>(m.w) + (size_t)r * m.cols + k);
-        const float d = m.d[(size_t)r * (m.cols >> 5) + (k >> 5)];
-        return make_float4(d * (float)(signed char)(packed), d * (float)(signed char)(packed >> 8),
-                           d * (float)(signed char)(packed >> 16), d * (float)(signed char)(packed >> 24));
-    } else if (m.type == PK_TYPE_F16) {
-        const uint2 raw = *reinterpret_cast<const uint2 *>(
-            static_cast<const __half *>(m.w) + (size_t)r * m.cols + k);
-        const __half2 a = *reinterpret_cast<const __half2 *>(&raw.x);
-        const __half2 b = *reinterpret_cast<const __half2 *>(&raw.y);
-        const float2 fa = __half22float2(a), fb = __half22float2(b);
-        return make_float4(fa.x, fa.y, fb.x, fb.y);
-    }
-    return *reinterpret_cast<const float4 *>(static_cast<const float *>(m.w) + (size_t)r * m.cols + k);
-}
-
-__device__ __forceinline__ float load_w1(const DMat &m, int r, int k) {
-    if (m.type == PK_TYPE_Q8_0) {
-        const signed char q = static_cast<const signed char *>(m.w)[(size_t)r * m.cols + k];
-        return m.d[(size_t)r * (m.cols >> 5) + (k >> 5)] * (float)q;
-    } else if (m.type == PK_TYPE_F16) {
-        return __half2float(static_cast<const __half *>(m.w)[(size_t)r * m.cols + k]);
-    }
-    return static_cast<const float *>(m.w)[(size_t)r * m.cols + k];
-}
-
-// Butterfly reduction of N per-lane partial sums over the 64 lanes of a wave:
-// each exchange halves the values a lane carries.  On return lane l holds the
-// total of value index (l >> (6 - log2 N)).  Partners add the same two
-// operands, so every lane holding an index holds the same bits.
-template <int N, int M>
-struct Bfly {
-    static __device__ __forceinline__ void run(float *v, int lane) {
-        if constexpr (M == 0) {
-            return;
-        } else if constexpr (N > 1) {
-            const bool up = (lane & M) != 0;
-#pragma unroll
-            for (int i = 0; i < N / 2; ++i) {
-                const float send = up ? v[i] : v[i + N / 2];
-                const float keep = up ? v[i + N / 2] : v[i];
-                v[i] = keep + __shfl_xor(send, M, kWave);
-            }
-            Bfly<N / 2, M / 2>::run(v, lane);
-        } else {
-            v[0] = v[0] + __shfl_xor(v[0], M, kWave);
-            Bfly<1, M / 2>::run(v, lane);
-        }
-    }
-};
-
-template <int N>
-__device__ __forceinline__ float wave_reduce_n(float (&v)[N], int lane) {
-    Bfly<N, 32>::run(v, lane);
-    return v[0];
-}
-
-template <int N>
-constexpr int ilog2() { return N <= 1 ? 0 : 1 + ilog2<N / 2>(); }
-
-// Accumulate acc[r*UC+u] += W[r0+r, :] . xs[u*xstride + :] for R rows, nu <= UC utterances.
-template <int R, int UC>
-__device__ __forceinline__ void dot_rows(const DMat &m, int r0, int nrows, const float *xs, int xstride,
-                                         int nu, float *acc, int lane) {
-    for (int k = lane * 4; k < m.cols; k += 4 * kWave) {
-        float4 w[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) w[r] = (r < nrows) ? load_w4(m, r0 + r, k) : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int u = 0; u < UC; ++u) {
-            if (u < nu) {
-                const float4 x = *reinterpret_cast<const float4 *>(xs + u * xstride + k);
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    float a = acc[r * UC + u];
-                    a = fmaf(w[r].x, x.x, a);
-                    a = fmaf(w[r].y, x.y, a);
-                    a = fmaf(w[r].z, x.z, a);
-                    a = fmaf(w[r].w, x.w, a);
-                    acc[r * UC + u] = a;
-                }
-            }
-        }
-    }
-}
-
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
-
-// Order-preserving map of an f32 onto u32 (-0 folded onto +0).
-__device__ __forceinline__ unsigned ordered_bits(float v) {
-    if (v == 0.0f) v = 0.0f;
-    const unsigned b = __float_as_uint(v);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
-__device__ __forceinline__ unsigned long long make_key(float v, int idx) {
-    return ((unsigned long long)ordered_bits(v) << kIdxBits) |
-           (unsigned long long)((1 << kIdxBits) - 1 - idx);
-}
-
-__device__ __forceinline__ int key_index(unsigned long long key) {
-    return (1 << kIdxBits) - 1 - (int)(key & ((1u << kIdxBits) - 1));
-}
-
-__device__ __forceinline__ unsigned key_stamp(unsigned long long key) {
-    return (unsigned)(key >> kStampShift);
-}
-
-// Grid barrier on a monotonically increasing counter (reset to 0 before
-// launch).  Returns false if the device error word is set or the wait
-// exceeds ~2 s of wall clock, so a broken launch ends instead of spinning.
-__device__ __forceinline__ bool grid_sync(unsigned *ctr, unsigned &target, unsigned nwg, int *status) {
-    __syncthreads();
-    __shared__ int s_ok;
-    if (threadIdx.x == 0) {
-        target += nwg;
-        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        int ok = 1;
-        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-        while (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            __builtin_amdgcn_s_sleep(1);
-            if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) { ok = 0; break; }
-            if (__builtin_amdgcn_s_memrealtime() - t0 > 200000000ull) {   // 100 MHz clock
-                __hip_atomic_store(status, PK_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ok = 0;
-                break;
-            }
-        }
-        s_ok = ok;
-    }
-    __syncthreads();
-    return s_ok != 0;
-}
-
-__device__ __forceinline__ int split_begin(int i, int total, int parts) {
-    return (int)(((long long)i * total) / parts);
-}
-
-// ---------------------------------------------------------------- enc_proj
-
-// encp[rows of utterance u] = b_e + W_e . enc[row]  (f32), 64x64 tiles, K step 32.
-__global__ void __launch_bounds__(256) enc_proj_kernel(DMat w, const float *__restrict bias,
-                                                       const float *__restrict enc, int d_enc,
-                                                       const long long *__restrict src_row,
-                                                       const long long *__restrict dst_row,
-                                                       const int *__restrict T, float *__restrict out) {
-    const int u = blockIdx.y;
-    const int Tu = T[u];
-    const int m0 = blockIdx.x * 64;
-    if (m0 >= Tu) return;
-    const int n0 = blockIdx.z * 64;
-    const int J = w.rows;
-    __shared__ float xs[32][65];
-    __shared__ float ws[32][65];
-    const int tid = threadIdx.x;
-    const int tr = tid / 16, tc = tid % 16;     // 16x16 threads, 4x4 outputs each
-    float acc[4][4] = {};
-    const float *src = enc + (size_t)src_row[u] * d_enc;
-    for (int k0 = 0; k0 < d_enc; k0 += 32) {
-        for (int i = tid; i < 64 * 32; i += 256) {
-            const int r = i / 32, k = i % 32;
-            const int m = m0 + r, n = n0 + r;
-            xs[k][r] = (m < Tu && k0 + k < d_enc) ? src[(size_t)m * d_enc + k0 + k] : 0.0f;
-            ws[k][r] = (n < J && k0 + k < d_enc) ? load_w1(w, n, k0 + k) : 0.0f;
-        }
-        __syncthreads();
-#pragma unroll 8
-        for (int k = 0; k < 32; ++k) {
-            float a[4], b[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { a[i] = xs[k][tr * 4 + i]; b[i] = ws[k][tc * 4 + i]; }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
-        }
-        __syncthreads();
-    }
-    float *dst = out + (size_t)dst_row[u] * J;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = m0 + tr * 4 + i;
-        if (m >= Tu) continue;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = n0 + tc * 4 + j;
-            if (n < J) dst[(size_t)m * J + n] = bias[n] + acc[i][j];
-        }
-    }
-}
-
-// ---------------------------------------------------------------- decode loop
-
-struct Ctl {                      // per-workgroup copy of the control state
-    int t[kMaxBatch], T[kMaxBatch], sym[kMaxBatch], pend[kMaxBatch], flags[kMaxBatch];
-    int ntok[kMaxBatch], steps[kMaxBatch], nseg[kMaxBatch], segst[kMaxBatch], last[kMaxBatch];
-    int cur[kMaxBatch], slot[kMaxBatch];
-    int lst[kMaxBatch], jst[kMaxBatch];
-    int cnt_l[kMaxBatch / kWave], cnt_j[kMaxBatch / kWave];
-    int nl, nj;
-    unsigned long long wgkey[kUC][2];
-};
-
-__device__ void build_lists(Ctl &s, int n) {
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int nblk = (n + kWave - 1) / kWave;
-    for (int b = wave; b < nblk; b += kWavesPerBlock) {
-        const int u = b * kWave + lane;
-        const bool fl = u < n && s.pend[u] >= 0;
-        const bool fj = u < n && s.t[u] < s.T[u];
-        const unsigned long long bl = __ballot(fl), bj = __ballot(fj);
-        if (lane == 0) { s.cnt_l[b] = __popcll(bl); s.cnt_j[b] = __popcll(bj); }
-    }
-    __syncthreads();
-    for (int b = wave; b < nblk; b += kWavesPerBlock) {
-        int base_l = 0, base_j = 0;
-        for (int i = 0; i < b; ++i) { base_l += s.cnt_l[i]; base_j += s.cnt_j[i]; }
-        const int u = b * kWave + lane;
-        const bool fl = u < n && s.pend[u] >= 0;
-        const bool fj = u < n && s.t[u] < s.T[u];
-        const unsigned long long bl = __ballot(fl), bj = __ballot(fj);
-        const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-        if (fl) s.lst[base_l + __popcll(bl & below)] = u;
-        if (fj) s.jst[base_j + __popcll(bj & below)] = u;
-    }
-    if (threadIdx.x == 0) {
-        int nl = 0, nj = 0;
-        for (int i = 0; i < nblk; ++i) { nl += s.cnt_l[i]; nj += s.cnt_j[i]; }
-        s.nl = nl;
-        s.nj = nj;
-    }
-    __syncthreads();
-}
-
-__device__ __forceinline__ size_t h_index(const KParams &p, int slot, int buf, int layer) {
-    return (((size_t)slot * 2 + buf) * p.L + layer) * p.H;
-}
-
-// One LSTM layer for every utterance in the LSTM list: rows 4j..4j+3 of this
-// workgroup's units, gates = W_ih x + W_hh h + b_ih + b_hh, then the cell
-// update of src/parakeet_tdt.cpp:130-138.
-__device__ void lstm_layer(const KParams &p, Ctl &s, float *stage, int layer, int wg, int nwg) {
-    const int H = p.H, lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int j0 = split_begin(wg, H, nwg), j1 = split_begin(wg + 1, H, nwg);
-    const int xstride = 2 * H;
-    for (int c0 = 0; c0 < s.nl; c0 += kUC) {
-        const int nu = min(kUC, s.nl - c0);
-        // stage x (embedding row or previous layer's new h) and h (this layer's old h)
-        for (int i = threadIdx.x; i < nu * H; i += kBlock) {
-            const int uu = i / H, k = i - uu * H;
-            const int b = s.lst[c0 + uu];
-            const int slot = s.slot[b];
-            float x;
-            if (layer == 0) x = load_w1(p.embed, s.pend[b], k);
-            else x = p.slot_h[h_index(p, slot, s.cur[b] ^ 1, layer - 1) + k];
-            const float h = (s.flags[b] & kFlagZeroHC) ? 0.0f : p.slot_h[h_index(p, slot, s.cur[b], layer) + k];
-            stage[uu * xstride + k] = x;
-            stage[uu * xstride + H + k] = h;
-        }
-        __syncthreads();
-        for (int j = j0 + wave; j < j1; j += kWavesPerBlock) {
-            float acc[4 * kUC];
-#pragma unroll
-            for (int i = 0; i < 4 * kUC; ++i) acc[i] = 0.0f;
-            dot_rows<4, kUC>(p.w_ih[layer], 4 * j, 4, stage, xstride, nu, acc, lane);
-            dot_rows<4, kUC>(p.w_hh[layer], 4 * j, 4, stage + H, xstride, nu, acc, lane);
-            wave_reduce_n<4 * kUC>(acc, lane);
-            constexpr int kShift = 6 - ilog2<4 * kUC>();
-            // gate g of utterance uu sits on lane ((g * kUC + uu) << kShift)
-            float g[4];
-#pragma unroll
-            for (int gi = 0; gi < 4; ++gi) g[gi] = __shfl(acc[0], ((gi * kUC + (lane % kUC)) << kShift), kWave);
-            if (lane < nu) {
-                const int b = s.lst[c0 + lane];
-                const int slot = s.slot[b];
-                const float *bi = p.b_ih[layer], *bh = p.b_hh[layer];
-                const float gi_ = g[0] + (bi[4 * j + 0] + bh[4 * j + 0]);
-                const float gf_ = g[1] + (bi[4 * j + 1] + bh[4 * j + 1]);
-                const float gg_ = g[2] + (bi[4 * j + 2] + bh[4 * j + 2]);
-                const float go_ = g[3] + (bi[4 * j + 3] + bh[4 * j + 3]);
-                const size_t ci = ((size_t)slot * p.L + layer) * H + j;
-                const float c_prev = (s.flags[b] & kFlagZeroHC) ? 0.0f : p.slot_c[ci];
-                const float c_new = sigmoidf_(gf_) * c_prev + sigmoidf_(gi_) * tanhf(gg_);
-                p.slot_c[ci] = c_new;
-                p.slot_h[h_index(p, slot, s.cur[b] ^ 1, layer) + j] = sigmoidf_(go_) * tanhf(c_new);
-            }
-        }
-        __syncthreads();
-    }
-}
-
-// pp = b_p + W_p . h[L-1] for every utterance in the LSTM list (cur already flipped).
-__device__ void pred_proj(const KParams &p, Ctl &s, float *stage, int wg, int nwg) {
-    const int H = p.H, J = p.J, lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int r0 = split_begin(wg, J, nwg), r1 = split_begin(wg + 1, J, nwg);
-    constexpr int R = 2;
-    for (int c0 = 0; c0 < s.nl; c0 += kUC) {
-        const int nu = min(kUC, s.nl - c0);
-        for (int i = threadIdx.x; i < nu * H; i += kBlock) {
-            const int uu = i / H, k = i - uu * H;
-            const int b = s.lst[c0 + uu];
-            stage[uu * H + k] = p.slot_h[h_index(p, s.slot[b], s.cur[b], p.L - 1) + k];
-        }
-        __syncthreads();
-        for (int r = r0 + wave * R; r < r1; r += kWavesPerBlock * R) {
-            float acc[R * kUC];
-#pragma unroll
-            for (int i = 0; i < R * kUC; ++i) acc[i] = 0.0f;
-            dot_rows<R, kUC>(p.w_pred, r, min(R, r1 - r), stage, H, nu, acc, lane);
-            wave_reduce_n<R * kUC>(acc, lane);
-            constexpr int kShift = 6 - ilog2<R * kUC>();
-            const int idx = lane >> kShift;
-            const int rr = idx / kUC, uu = idx % kUC;
-            if ((lane & ((1 << kShift) - 1)) == 0 && uu < nu && r + rr < r1) {
-                const int b = s.lst[c0 + uu];
-                p.slot_pp[(size_t)s.slot[b] * J + r + rr] = p.b_pred[r + rr] + acc[0];
-            }
-        }
-        __syncthreads();
-    }
-}
-
-// logits rows of this workgroup for every utterance in the joint list, local
-// argmax, then one global atomic max per (utterance, head) per workgroup.
-__device__ void joint_argmax(const KParams &p, Ctl &s, float *stage, unsigned stamp, int wg, int nwg) {
-    const int J = p.J, lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int r0 = split_begin(wg, p.Vo, nwg), r1 = split_begin(wg + 1, p.Vo, nwg);
-    constexpr int R = 2;
-    unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * 2;
-    for (int c0 = 0; c0 < s.nj; c0 += kUC) {
-        const int nu = min(kUC, s.nj - c0);
-        for (int i = threadIdx.x; i < nu * J; i += kBlock) {
-            const int uu = i / J, k = i - uu * J;
-            const int b = s.jst[c0 + uu];
-            const float v = p.encp[(size_t)(p.encp_row[b] + s.t[b]) * J + k] + p.slot_pp[(size_t)s.slot[b] * J + k];
-            stage[uu * J + k] = (0.0f < v) ? v : 0.0f;
-        }
-        if (threadIdx.x < 2 * kUC) s.wgkey[threadIdx.x / 2][threadIdx.x % 2] = 0ull;
-        __syncthreads();
-        for (int r = r0 + wave * R; r < r1; r += kWavesPerBlock * R) {
-            float acc[R * kUC];
-#pragma unroll
-            for (int i = 0; i < R * kUC; ++i) acc[i] = 0.0f;
-            dot_rows<R, kUC>(p.w_out, r, min(R, r1 - r), stage, J, nu, acc, lane);
-            wave_reduce_n<R * kUC>(acc, lane);
-            constexpr int kShift = 6 - ilog2<R * kUC>();
-            const int idx = lane >> kShift;
-            const int rr = idx / kUC, uu = idx % kUC;
-            const int row = r + rr;
-            if ((lane & ((1 << kShift) - 1)) == 0 && uu < nu && row < r1) {
-                float v = acc[0] + p.b_out[row];
-                const int b = s.jst[c0 + uu];
-                if (row == p.blank && p.blank_bias) v += p.blank_bias[b];
-                const int head = row < p.V1 ? 0 : 1;
-                const int li = head ? row - p.V1 : row;
-                atomicMax(&s.wgkey[uu][head], make_key(v, li));
-            }
-        }
-        __syncthreads();
-        if (threadIdx.x < 2 * nu) {
-            const int uu = threadIdx.x / 2, head = threadIdx.x % 2;
-            const unsigned long long k = s.wgkey[uu][head];
-            if (k != 0ull)
-                __hip_atomic_fetch_max(&keys[(size_t)s.jst[c0 + uu] * 2 + head],
-                                       ((unsigned long long)stamp << kStampShift) | k,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-    }
-}
-
-// Apply the argmax results of iteration `stamp` to every utterance of the joint
-// list: src/parakeet_tdt.cpp:936-967 (TDT) and src/parakeet_eou.cpp:275-332 (EOU).
-__device__ void decide(const KParams &p, Ctl &s, unsigned stamp, int wg, int nwg) {
-    const unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * 2;
-    for (int i = threadIdx.x; i < s.nj; i += kBlock) {
-        const int b = s.jst[i];
-        const unsigned long long kt = __hip_atomic_load(&keys[(size_t)b * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned long long kd = __hip_atomic_load(&keys[(size_t)b * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (key_stamp(kt) != stamp || (p.Dn > 0 && key_stamp(kd) != stamp)) {
-            __hip_atomic_store(p.status, PK_ERR_DEVICE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            s.t[b] = s.T[b];
-            continue;
-        }
-        const int tok = key_index(kt);
-        const int di = p.Dn > 0 ? key_index(kd) : -1;
-        const bool writer = (b % nwg) == wg;
-        const int step = s.steps[b]++;
-        if (writer && p.trace) {
-            if (step < p.trace_cap) {
-                p.trace[((size_t)b * p.trace_cap + step) * 2] = tok;
-                p.trace[((size_t)b * p.trace_cap + step) * 2 + 1] = di;
-            } else {
-                s.flags[b] |= kFlagTraceOverflow;
-            }
-        }
-        if (p.kind == PK_KIND_TDT) {
-            const int dur = p.n_dur > 0 ? p.durations[di] : di;
-            const int adv = dur > 1 ? dur : 1;
-            if (tok == p.blank) {
-                s.t[b] += adv;
-                s.sym[b] = 0;
-                continue;
-            }
-            const int n = s.ntok[b]++;
-            if (writer) {
-                if (n < p.token_cap) p.tokens[(size_t)b * p.token_cap + n] = tok;
-                else s.flags[b] |= kFlagTokOverflow;
-            }
-            s.pend[b] = tok;
-            s.sym[b] += 1;
-            if (dur > 0 || s.sym[b] >= p.max_sym) {
-                s.t[b] += adv;
-                s.sym[b] = 0;
-            }
-        } else {
-            const int max_syms = p.max_sym > 1 ? p.max_sym : 1;
-            bool frame_done = false;
-            if (tok == p.blank || tok == p.eob) {
-                frame_done = true;
-            } else if (tok == p.eou) {
-                const int total = (p.tokens_base ? p.tokens_base[b] : 0) + s.ntok[b];
-                if (total > s.segst[b]) {
-                    const int ns = s.nseg[b]++;
-                    if (writer) {
-                        if (p.segs && ns < p.seg_cap) p.segs[(size_t)b * p.seg_cap + ns] = total;
-                        else s.flags[b] |= kFlagSegOverflow;
-                    }
-                    s.segst[b] = total;
-                }
-                s.flags[b] |= kFlagZeroHC;
-                s.pend[b] = p.blank;
-                s.last[b] = p.blank;
-                frame_done = true;
-            } else if (tok >= 0 && tok < p.n_special && p.special[tok]) {
-                frame_done = true;
-            } else {
-                const int n = s.ntok[b]++;
-                if (writer) {
-                    if (n < p.token_cap) p.tokens[(size_t)b * p.token_cap + n] = tok;
-                    else s.flags[b] |= kFlagTokOverflow;
-                }
-                s.pend[b] = tok;
-                s.last[b] = tok;
-                s.sym[b] += 1;
-                if (s.sym[b] >= max_syms) frame_done = true;
-            }
-            if (frame_done) {          // the next frame starts with sym = 0 (src/parakeet_eou.cpp:269)
-                s.t[b] += 1;
-                if (s.t[b] < s.T[b]) s.sym[b] = 0;
-            }
-        }
-    }
-}
-
-__global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
-    extern __shared__ float stage[];
-    __shared__ Ctl s;
-    const int wg = blockIdx.x, nwg = gridDim.x;
-    const int n = p.n_utts;
-    unsigned target = 0;
-
-    for (int b = threadIdx.x; b < n; b += kBlock) {
-        const int slot = p.slot[b];
-        const int *ctrl = p.slot_ctrl + (size_t)slot * PK_CTRL_N;
-        const bool init = ctrl[PK_CTRL_INIT] != 0;
-        s.slot[b] = slot;
-        s.T[b] = p.T[b];
-        s.ntok[b] = 0;
-        s.steps[b] = 0;
-        s.nseg[b] = 0;
-        s.cur[b] = init ? ctrl[PK_CTRL_CUR] : 0;
-        s.sym[b] = init ? ctrl[PK_CTRL_SYM] : 0;
-        if (p.kind == PK_KIND_EOU && s.T[b] > 0) s.sym[b] = 0;   // reset per frame (src/parakeet_eou.cpp:269)
-        s.last[b] = init ? ctrl[PK_CTRL_LAST] : -1;
-        s.segst[b] = init ? ctrl[PK_CTRL_SEGSTART] : 0;
-        const int carry = init ? ctrl[PK_CTRL_CARRY] : 0;
-        s.pend[b] = init ? -1 : p.blank;
-        s.flags[b] = init ? 0 : kFlagZeroHC;
-        if (p.kind == PK_KIND_TDT) s.t[b] = carry > 0 ? min(carry, s.T[b]) : 0;
-        else s.t[b] = 0;
-    }
-    __syncthreads();
-    build_lists(s, n);
-
-    unsigned iter = 0;
-    bool ok = true;
-    while (ok) {
-        if (s.nl == 0 && s.nj == 0) break;
-        if ((int)iter >= p.max_iter) {
-            if (wg == 0 && threadIdx.x == 0)
-                __hip_atomic_store(p.status, PK_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            ok = false;
-            break;
-        }
-        ++iter;
-        if (s.nl > 0) {
-            for (int l = 0; l < p.L && ok; ++l) {
-                lstm_layer(p, s, stage, l, wg, nwg);
-                ok = grid_sync(p.barrier, target, nwg, p.status);
-            }
-            if (!ok) break;
-            for (int i = threadIdx.x; i < s.nl; i += kBlock) {
-                const int b = s.lst[i];
-                s.cur[b] ^= 1;
-                s.pend[b] = -1;
-                s.flags[b] &= ~kFlagZeroHC;
-            }
-            __syncthreads();
-            pred_proj(p, s, stage, wg, nwg);
-            ok = grid_sync(p.barrier, target, nwg, p.status);
-            if (!ok) break;
-        }
-        if (s.nj > 0) {
-            joint_argmax(p, s, stage, iter, wg, nwg);
-            ok = grid_sync(p.barrier, target, nwg, p.status);
-            if (!ok) break;
-            decide(p, s, iter, wg, nwg);
-        }
-        __syncthreads();
-        build_lists(s, n);
-    }
-    if (!ok) return;
-
-    for (int b = threadIdx.x; b < n; b += kBlock) {
-        if (b % nwg != wg) continue;
-        int *ctrl = p.slot_ctrl + (size_t)s.slot[b] * PK_CTRL_N;
-        ctrl[PK_CTRL_INIT] = 1;
-        ctrl[PK_CTRL_SYM] = s.sym[b];
-        ctrl[PK_CTRL_CARRY] = (p.kind == PK_KIND_TDT) ? max(0, s.t[b] - s.T[b]) : 0;
-        ctrl[PK_CTRL_LAST] = s.last[b];
-        ctrl[PK_CTRL_SEGSTART] = s.segst[b];
-        ctrl[PK_CTRL_CUR] = s.cur[b];
-        p.n_tokens[b] = s.ntok[b];
-        p.steps[b] = s.steps[b];
-        if (p.n_segs) p.n_segs[b] = s.nseg[b];
-        if (s.flags[b] & (kFlagTokOverflow | kFlagSegOverflow))
-            __hip_atomic_store(p.status + 2, PK_ERR_OVERFLOW, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (s.flags[b] & kFlagTraceOverflow)
-            __hip_atomic_store(p.status + 3, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (wg == 0 && threadIdx.x == 0) p.status[1] = (int)iter;
-}
+using pkdev::DMat;
+using pkdev::KParams;
+using pkdev::kBlock;
+using pkdev::kMaxBatch;
+using pkdev::kIdxBits;
+using pkdev::kMaxStamp;
+using pkdev::kUC;
+using pkdev::kSmallB;
+using pkdev::kFlagStride;
 
 // ---------------------------------------------------------------- host side
 
@@ -782,10 +187,11 @@ struct pk_decoder {
     hipStream_t stream = nullptr;
     hipEvent_t ev[3] = {};
     DevBuf arena;              // weights
+    DevBuf eproj;              // [V1][4H] layer-0 input projection of every token
     DevBuf slots_h, slots_c, slots_pp, slots_ctrl;
     DevBuf special;
     // per-call scratch
-    DevBuf d_desc, d_encp, d_keys, d_sync, d_enc, d_out;
+    DevBuf d_desc, d_encp, d_keys, d_sync, d_enc, d_out, d_xchg, d_flags;
     std::vector<uint8_t> h_desc;
     int last_iters = 0;
 };
@@ -902,12 +308,25 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
         vec_dst.push_back(dst);
         return vec_f32(t, n, map, vecs.back(), name);
     };
-    if ((rc = add_mat(d->embed, V1, H, nullptr, &kp.embed, "predict.embed.weight"))) return cleanup(rc);
+    DMat embed{};
+    const float *b_ih0 = nullptr, *b_hh0 = nullptr;
+    if ((rc = add_mat(d->embed, V1, H, nullptr, &embed, "predict.embed.weight"))) return cleanup(rc);
     for (int l = 0; l < L; ++l) {
         if ((rc = add_mat(d->w_ih[l], 4 * H, H, &gmap, &kp.w_ih[l], "predict.lstm.w_ih"))) return cleanup(rc);
         if ((rc = add_mat(d->w_hh[l], 4 * H, H, &gmap, &kp.w_hh[l], "predict.lstm.w_hh"))) return cleanup(rc);
-        if ((rc = add_vec(d->b_ih[l], 4 * H, &gmap, &kp.b_ih[l], "predict.lstm.b_ih"))) return cleanup(rc);
-        if ((rc = add_vec(d->b_hh[l], 4 * H, &gmap, &kp.b_hh[l], "predict.lstm.b_hh"))) return cleanup(rc);
+        std::vector<float> bi, bh;
+        if ((rc = vec_f32(d->b_ih[l], 4 * H, &gmap, bi, "predict.lstm.b_ih"))) return cleanup(rc);
+        if ((rc = vec_f32(d->b_hh[l], 4 * H, &gmap, bh, "predict.lstm.b_hh"))) return cleanup(rc);
+        if (l == 0) {
+            vecs.push_back(bi);
+            vec_dst.push_back(&b_ih0);
+            vecs.push_back(bh);
+            vec_dst.push_back(&b_hh0);
+        } else {
+            for (int i = 0; i < 4 * H; ++i) bi[i] += bh[i];
+            vecs.push_back(bi);
+            vec_dst.push_back(&kp.b_lstm[l]);
+        }
     }
     if ((rc = add_mat(d->joint_enc_w, J, D, nullptr, &dec->w_enc, "joint.enc.weight"))) return cleanup(rc);
     if ((rc = add_vec(d->joint_enc_b, J, nullptr, &dec->b_enc, "joint.enc.bias"))) return cleanup(rc);
@@ -915,7 +334,17 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     if ((rc = add_vec(d->joint_pred_b, J, nullptr, &kp.b_pred, "joint.pred.bias"))) return cleanup(rc);
     if ((rc = add_mat(d->joint_out_w, Vo, J, nullptr, &kp.w_out, "joint.out.weight"))) return cleanup(rc);
     if ((rc = add_vec(d->joint_out_b, Vo, nullptr, &kp.b_out, "joint.out.bias"))) return cleanup(rc);
+    if (H % 4 || J % 4) return cleanup(fail(PK_ERR_UNSUPPORTED, "pred_hidden and joint_hidden must be multiples of 4"));
     if ((rc = upload_weights(dec, mats, vecs, mat_dst, vec_dst))) return cleanup(rc);
+    // layer-0 input projection of every token: E'[v] = W_ih0 . embed[v] + b_ih0 + b_hh0
+    if ((rc = dec->eproj.ensure((size_t)V1 * 4 * H * 4))) return cleanup(rc);
+    {
+        dim3 grid((V1 + 15) / 16, (4 * H + 63) / 64);
+        pkdev::embed_proj_kernel<<<grid, 256>>>(kp.w_ih[0], embed, b_ih0, b_hh0, dec->eproj.as<float>());
+        if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+            return cleanup(fail(PK_ERR_DEVICE, "embedding projection kernel failed"));
+    }
+    kp.eproj = dec->eproj.as<float>();
     dec->desc.special = nullptr;
     dec->kp.special = nullptr;
     dec->kp.n_special = 0;
@@ -928,7 +357,7 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     }
 
     // slots
-    if ((rc = dec->slots_h.ensure((size_t)n_slots * 2 * L * H * 4))) return cleanup(rc);
+    if ((rc = dec->slots_h.ensure((size_t)n_slots * L * H * 4))) return cleanup(rc);
     if ((rc = dec->slots_c.ensure((size_t)n_slots * L * H * 4))) return cleanup(rc);
     if ((rc = dec->slots_pp.ensure((size_t)n_slots * J * 4))) return cleanup(rc);
     if ((rc = dec->slots_ctrl.ensure((size_t)n_slots * PK_CTRL_N * 4))) return cleanup(rc);
@@ -943,18 +372,19 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     kp.slot_ctrl = dec->slots_ctrl.as<int>();
 
     // decode-loop launch shape: one workgroup per CU, LDS stage for kUC utterances
-    const size_t need = (size_t)kUC * std::max(2 * H, J) * 4;
-    if (need + sizeof(Ctl) > (size_t)dec->lds_block)
-        return cleanup(fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed, %d available", need + sizeof(Ctl), dec->lds_block));
+    const size_t need = std::max((size_t)kUC * (J + L * H), (size_t)kSmallB * H) * 4;
+    if (need + sizeof(pkdev::Ctl) > (size_t)dec->lds_block)
+        return cleanup(fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed, %d available", need + sizeof(pkdev::Ctl),
+                            dec->lds_block));
     dec->stage_bytes = need;
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(decode_loop_kernel),
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(pkdev::decode_loop_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)need) != hipSuccess)
         return cleanup(fail(PK_ERR_DEVICE, "hipFuncSetAttribute"));
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(decode_loop_kernel),
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(pkdev::decode_loop_kernel),
                                                      kBlock, need) != hipSuccess || per_cu < 1)
         return cleanup(fail(PK_ERR_DEVICE, "decode kernel does not fit on a CU"));
-    dec->nwg = dec->n_cu;
+    dec->nwg = std::min(dec->n_cu, kBlock);
     if (hipStreamCreateWithFlags(&dec->stream, hipStreamNonBlocking) != hipSuccess)
         return cleanup(fail(PK_ERR_DEVICE, "stream"));
     for (auto &e : dec->ev)
@@ -1012,11 +442,10 @@ PK_API int pk_slot_read(pk_decoder *dec, int32_t slot, float *h, float *c, float
     const KParams &kp = dec->kp;
     int32_t cw[PK_CTRL_N];
     HIP_TRY(hipMemcpy(cw, kp.slot_ctrl + (size_t)slot * PK_CTRL_N, sizeof cw, hipMemcpyDeviceToHost));
-    const int cur = cw[PK_CTRL_CUR] & 1;
     const size_t hn = (size_t)kp.L * kp.H;
-    if (h) HIP_TRY(hipMemcpy(h, kp.slot_h + ((size_t)slot * 2 + cur) * hn, hn * 4, hipMemcpyDeviceToHost));
+    if (h) HIP_TRY(hipMemcpy(h, kp.slot_h + (size_t)slot * hn, hn * 4, hipMemcpyDeviceToHost));
     if (c) HIP_TRY(hipMemcpy(c, kp.slot_c + (size_t)slot * hn, hn * 4, hipMemcpyDeviceToHost));
-    if (pred) HIP_TRY(hipMemcpy(pred, kp.slot_h + ((size_t)slot * 2 + cur) * hn + (size_t)(kp.L - 1) * kp.H,
+    if (pred) HIP_TRY(hipMemcpy(pred, kp.slot_h + (size_t)slot * hn + (size_t)(kp.L - 1) * kp.H,
                                 (size_t)kp.H * 4, hipMemcpyDeviceToHost));
     if (ctrl) memcpy(ctrl, cw, sizeof cw);
     return 0;
@@ -1118,7 +547,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     if (rows > 0) {
         if ((rc = dec->d_encp.ensure((size_t)rows * J * 4))) return rc;
         dim3 grid((max_T + 63) / 64, m, (J + 63) / 64);
-        enc_proj_kernel<<<grid, 256, 0, dec->stream>>>(dec->w_enc, dec->b_enc, enc, D,
+        pkdev::enc_proj_kernel<<<grid, 256, 0, dec->stream>>>(dec->w_enc, dec->b_enc, enc, D,
                                                        d_src, d_dst, d_T, dec->d_encp.as<float>());
         HIP_TRY(hipGetLastError());
     }
@@ -1165,14 +594,24 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         if ((unsigned)p.max_iter >= kMaxStamp) return fail(PK_ERR_UNSUPPORTED, "window too long for the iteration stamp");
         if ((rc = dec->d_keys.ensure((size_t)2 * std::max(m, 1) * 2 * 8))) return rc;
         if ((rc = dec->d_sync.ensure(64))) return rc;
+        if ((rc = dec->d_flags.ensure((size_t)dec->nwg * kFlagStride * 4))) return rc;
+        const int L = kp.L, H = kp.H;
+        const size_t mm = std::max(m, 1);
+        const size_t xh = 2 * (size_t)L * mm * H, xp = mm * J, xr = (size_t)L * mm * 4 * H;
+        if ((rc = dec->d_xchg.ensure((2 * xh + xp + xr) * 4))) return rc;
+        p.hx = dec->d_xchg.as<float>();
+        p.cx = p.hx + xh;
+        p.ppx = p.cx + xh;
+        p.rx = p.ppx + xp;
         p.keys = dec->d_keys.as<unsigned long long>();
-        p.barrier = dec->d_sync.as<unsigned>();
+        p.flags = dec->d_flags.as<unsigned>();
         p.status = dec->d_sync.as<int>() + 4;
         HIP_TRY(hipMemsetAsync(dec->d_keys.p, 0, (size_t)2 * std::max(m, 1) * 2 * 8, dec->stream));
         HIP_TRY(hipMemsetAsync(dec->d_sync.p, 0, 64, dec->stream));
+        HIP_TRY(hipMemsetAsync(dec->d_flags.p, 0, (size_t)dec->nwg * kFlagStride * 4, dec->stream));
         void *args[] = {&p};
         if (m > 0) {
-            HIP_TRY(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(decode_loop_kernel), dim3(dec->nwg),
+            HIP_TRY(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(pkdev::decode_loop_kernel), dim3(dec->nwg),
                                                dim3(kBlock), args, dec->stage_bytes, dec->stream));
         }
     }
