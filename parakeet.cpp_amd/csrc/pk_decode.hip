@@ -1,38 +1,33 @@
-// pk_decode.hip -- MI355X (gfx950) transducer greedy decode: kernels + C ABI.
+// pk_decode.hip -- MI355X (gfx950) transducer greedy decode: host side + C ABI.
 //
 // Replaces the decode loop of parakeet.cpp (tdt_decode_window,
 // src/parakeet_tdt.cpp:865-981; eou_decode_window, src/parakeet_eou.cpp:232-336)
-// with one persistent, batch-over-utterances kernel:
+// with one persistent, batch-over-utterances kernel (pk_device.h):
 //
 //   enc_proj_kernel     b_e + W_e . enc[t] for every frame of every utterance,
 //                       once per window (src/parakeet_tdt.cpp:433-483 computes
 //                       the same projection as a ggml graph; the CPU path
 //                       recomputes it per step at :167-168).
 //   decode_loop_kernel  all lockstep iterations of all utterances in one
-//                       cooperative launch.  One iteration is
-//                         LSTM layer 0..L-1   (utterances that emitted a token)
+//                       cooperative launch.  The batch is split into
+//                       independent domains (16 or 32 utterances, each on
+//                       nwg/C workgroups with its own barrier); one iteration
+//                       of a domain is
+//                         LSTM layer 0        gates = E'[token] + W_hh0 . h0
+//                         LSTM layers >= 1    MFMA tiles, cell update in the epilogue
 //                         pred projection     pp = b_p + W_p . h[L-1]
-//                         joint + argmax      logits = b_o + W_o . relu(encp[t] + pp)
+//                         joint + argmax      logits = b_o + W_o . relu(encp[t] + pp),
+//                                             and W_hh_l . h_l for the next step
 //                         decisions           token / duration / frame advance,
 //                                             symbol cap, EOU reset, compaction
-//                       separated by grid barriers.  The token and duration
-//                       argmaxes are reduced with 64-bit atomic max on a key
-//                       (iteration stamp | order-preserving value | inverted
-//                       index), which reproduces the reference's first-index
-//                       tie rule (src/parakeet_tdt.cpp:25-32) independently of
-//                       reduction order.  Every workgroup applies the same
-//                       decisions to its own copy of the control state, so no
-//                       state is broadcast and no host round trip happens
-//                       inside the loop.
+//                       with a barrier after each dependent phase.
 //
-// Weights stay at their stored precision: q8_0 is re-laid out as an int8
-// plane [rows][cols] plus an f32 plane of block scales [rows][cols/32]
-// (d converted exactly from f16); value = d * q as ggml's to_float.  LSTM
-// gate rows are reordered unit-major (row 4j+g = gate g of unit j) so a wave
-// owning unit j holds its four gates for the cell update.
-//
-// Arithmetic is f32 FMA throughout; summation order differs from the
-// reference's sequential row sums, so logits differ by f32 rounding only.
+// Weights stay at their stored precision.  Matrices used per step are tiled
+// as MFMA A fragments (16 rows x 32 columns per fragment); q8_0 integers go
+// through the matrix cores exactly as f16 and the block scale d is applied in
+// f32 per 32-column block; activations enter as f16 pairs (hi + lo = x to
+// about 2^-22 relative).  The layer-0 input projection of every token,
+// E'[v] = W_ih0 . embed[v] + b_ih0 + b_hh0, is computed once at load in f32.
 
 #include <hip/hip_runtime.h>
 
@@ -41,6 +36,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <numeric>
 #include <string>
 #include <vector>
 
@@ -49,17 +45,20 @@
 
 namespace {
 
-using pkdev::DMat;
 using pkdev::KParams;
+using pkdev::TMat;
 using pkdev::kBlock;
-using pkdev::kMaxBatch;
-using pkdev::kIdxBits;
-using pkdev::kMaxStamp;
-using pkdev::kUC;
-using pkdev::kSmallB;
+using pkdev::kDomCap;
 using pkdev::kFlagStride;
+using pkdev::kIdxBits;
+using pkdev::kKPad;
+using pkdev::kMaxStamp;
+using pkdev::kSmallB;
+using pkdev::kTile;
+using pkdev::kWave;
+using pkdev::kWaves;
 
-// ---------------------------------------------------------------- host side
+constexpr int kMaxBatch = PK_MAX_BATCH;
 
 thread_local std::string g_err;
 
@@ -100,6 +99,9 @@ float f16_to_f32(uint16_t h) {
 struct DevBuf {
     void *p = nullptr;
     size_t n = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf &) = delete;
+    DevBuf &operator=(const DevBuf &) = delete;
     ~DevBuf() { if (p) (void)hipFree(p); }
     int ensure(size_t bytes) {
         if (bytes <= n) return 0;
@@ -113,62 +115,116 @@ struct DevBuf {
     template <class T> T *as() const { return static_cast<T *>(p); }
 };
 
-// Host copy of a repacked matrix, uploaded into one arena.
-struct HostMat {
-    int type, rows, cols;
-    std::vector<uint8_t> w;       // plane bytes
-    std::vector<float> d;         // q8 scales
-};
-
-int bytes_per_elem(int type) { return type == PK_TYPE_F32 ? 4 : type == PK_TYPE_F16 ? 2 : 1; }
-
-// Repack a stored GGUF matrix [rows][cols]; row_map[r] = stored row placed at r (nullable).
-int repack(const pk_tensor &t, int rows, int cols, const std::vector<int> *row_map, HostMat &out, const char *name) {
+int check_tensor(const pk_tensor &t, int rows, int cols, const char *name) {
     if (!t.data) return fail(PK_ERR_TENSOR, "missing tensor %s", name);
     if (t.ne0 != cols || t.ne1 != rows)
-        return fail(PK_ERR_TENSOR, "%s: ne=[%lld,%lld], expected [%d,%d]", name, (long long)t.ne0,
-                    (long long)t.ne1, cols, rows);
+        return fail(PK_ERR_TENSOR, "%s: ne=[%lld,%lld], expected [%d,%d]", name, (long long)t.ne0, (long long)t.ne1,
+                    cols, rows);
     if (t.type != PK_TYPE_F32 && t.type != PK_TYPE_F16 && t.type != PK_TYPE_Q8_0)
         return fail(PK_ERR_UNSUPPORTED, "%s: ggml type %d not supported", name, t.type);
-    if (cols % 4) return fail(PK_ERR_UNSUPPORTED, "%s: row length %d not a multiple of 4", name, cols);
     if (t.type == PK_TYPE_Q8_0 && cols % 32) return fail(PK_ERR_TENSOR, "%s: q8_0 row length %d", name, cols);
-    out.type = t.type;
-    out.rows = rows;
-    out.cols = cols;
-    const int bpe = bytes_per_elem(t.type);
-    out.w.resize((size_t)rows * cols * bpe);
-    if (t.type == PK_TYPE_Q8_0) out.d.resize((size_t)rows * (cols / 32));
+    return 0;
+}
+
+// Stored row sr of a tensor as f32 (ggml to_float: q8_0 -> d*q, f16 -> f32).
+void row_f32(const pk_tensor &t, int cols, int sr, float *out) {
     const uint8_t *src = static_cast<const uint8_t *>(t.data);
-    const size_t row_bytes = t.type == PK_TYPE_Q8_0 ? (size_t)(cols / 32) * 34 : (size_t)cols * bpe;
-    for (int r = 0; r < rows; ++r) {
-        const int sr = row_map ? (*row_map)[r] : r;
-        const uint8_t *row = src + (size_t)sr * row_bytes;
-        if (t.type == PK_TYPE_Q8_0) {
-            for (int b = 0; b < cols / 32; ++b) {
-                uint16_t dh;
-                memcpy(&dh, row + 34 * b, 2);
-                out.d[(size_t)r * (cols / 32) + b] = f16_to_f32(dh);
-                memcpy(&out.w[(size_t)r * cols + 32 * b], row + 34 * b + 2, 32);
-            }
-        } else {
-            memcpy(&out.w[(size_t)r * cols * bpe], row, row_bytes);
+    if (t.type == PK_TYPE_Q8_0) {
+        const uint8_t *row = src + (size_t)sr * (cols / 32) * 34;
+        for (int b = 0; b < cols / 32; ++b) {
+            uint16_t dh;
+            memcpy(&dh, row + 34 * b, 2);
+            const float d = f16_to_f32(dh);
+            const int8_t *q = reinterpret_cast<const int8_t *>(row + 34 * b + 2);
+            for (int j = 0; j < 32; ++j) out[32 * b + j] = (float)q[j] * d;
         }
+    } else if (t.type == PK_TYPE_F16) {
+        const uint16_t *row = reinterpret_cast<const uint16_t *>(src) + (size_t)sr * cols;
+        for (int j = 0; j < cols; ++j) out[j] = f16_to_f32(row[j]);
+    } else {
+        memcpy(out, reinterpret_cast<const float *>(src) + (size_t)sr * cols, 4 * (size_t)cols);
     }
+}
+
+// Dense f32 copy [rows][cols] of a stored matrix; map[r] = stored row placed at r.
+int dense_f32(const pk_tensor &t, int rows, int cols, const std::vector<int> *map, std::vector<float> &out,
+              const char *name) {
+    if (int rc = check_tensor(t, rows, cols, name)) return rc;
+    out.resize((size_t)rows * cols);
+    for (int r = 0; r < rows; ++r) row_f32(t, cols, map ? (*map)[r] : r, out.data() + (size_t)r * cols);
     return 0;
 }
 
 int vec_f32(const pk_tensor &t, int n, const std::vector<int> *map, std::vector<float> &out, const char *name) {
     if (!t.data) return fail(PK_ERR_TENSOR, "missing tensor %s", name);
-    if (t.ne0 * t.ne1 != n) return fail(PK_ERR_TENSOR, "%s: %lld elements, expected %d", name,
-                                        (long long)(t.ne0 * t.ne1), n);
+    if (t.ne0 * t.ne1 != n)
+        return fail(PK_ERR_TENSOR, "%s: %lld elements, expected %d", name, (long long)(t.ne0 * t.ne1), n);
+    if (t.type != PK_TYPE_F32 && t.type != PK_TYPE_F16) return fail(PK_ERR_UNSUPPORTED, "%s: bias type %d", name, t.type);
     std::vector<float> tmp(n);
-    if (t.type == PK_TYPE_F32) memcpy(tmp.data(), t.data, 4 * (size_t)n);
-    else if (t.type == PK_TYPE_F16) {
-        const uint16_t *s = static_cast<const uint16_t *>(t.data);
-        for (int i = 0; i < n; ++i) tmp[i] = f16_to_f32(s[i]);
-    } else return fail(PK_ERR_UNSUPPORTED, "%s: bias type %d", name, t.type);
+    row_f32(t, n, 0, tmp.data());
     out.resize(n);
     for (int i = 0; i < n; ++i) out[i] = tmp[map ? (*map)[i] : i];
+    return 0;
+}
+
+// A matrix tiled as MFMA A fragments (see TMat in pk_device.h), host side.
+struct HostTiled {
+    int type = 0, rows = 0, tiles = 0, KB = 0;
+    std::vector<uint8_t> a, a_lo;
+    std::vector<float> scale;
+};
+
+int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *map, HostTiled &out, const char *name) {
+    if (int rc = check_tensor(t, rows, cols, name)) return rc;
+    if (cols % 32) return fail(PK_ERR_UNSUPPORTED, "%s: row length %d not a multiple of 32", name, cols);
+    out.type = t.type;
+    out.rows = rows;
+    out.tiles = (rows + kTile - 1) / kTile;
+    out.KB = cols / 32;
+    const size_t frags = (size_t)out.tiles * out.KB;
+    const uint8_t *src = static_cast<const uint8_t *>(t.data);
+    if (t.type == PK_TYPE_Q8_0) {
+        out.a.assign(frags * kWave * 8, 0);
+        out.scale.assign(frags * kTile, 0.0f);
+        for (int tile = 0; tile < out.tiles; ++tile)
+            for (int r = 0; r < kTile; ++r) {
+                const int row = tile * kTile + r;
+                if (row >= rows) continue;
+                const uint8_t *srow = src + (size_t)(map ? (*map)[row] : row) * out.KB * 34;
+                for (int kb = 0; kb < out.KB; ++kb) {
+                    const size_t f = (size_t)tile * out.KB + kb;
+                    uint16_t dh;
+                    memcpy(&dh, srow + 34 * kb, 2);
+                    out.scale[f * kTile + r] = f16_to_f32(dh);
+                    for (int g = 0; g < 4; ++g)   // lane r + 16 g holds q[8g .. 8g+8)
+                        memcpy(&out.a[(f * kWave + r + 16 * g) * 8], srow + 34 * kb + 2 + 8 * g, 8);
+                }
+            }
+    } else {
+        std::vector<float> row(cols);
+        out.a.assign(frags * kWave * 16, 0);
+        if (t.type == PK_TYPE_F32) out.a_lo.assign(frags * kWave * 16, 0);
+        for (int tile = 0; tile < out.tiles; ++tile)
+            for (int r = 0; r < kTile; ++r) {
+                const int rr = tile * kTile + r;
+                if (rr >= rows) continue;
+                row_f32(t, cols, map ? (*map)[rr] : rr, row.data());
+                for (int kb = 0; kb < out.KB; ++kb) {
+                    const size_t f = (size_t)tile * out.KB + kb;
+                    for (int g = 0; g < 4; ++g)
+                        for (int i = 0; i < 8; ++i) {
+                            const float w = row[32 * kb + 8 * g + i];
+                            const _Float16 hi = (_Float16)w;
+                            const size_t at = ((f * kWave + r + 16 * g) * 8 + i) * 2;
+                            memcpy(&out.a[at], &hi, 2);
+                            if (t.type == PK_TYPE_F32) {
+                                const _Float16 lo = (_Float16)(w - (float)hi);
+                                memcpy(&out.a_lo[at], &lo, 2);
+                            }
+                        }
+                }
+            }
+    }
     return 0;
 }
 
@@ -177,13 +233,12 @@ int vec_f32(const pk_tensor &t, int n, const std::vector<int> *map, std::vector<
 struct pk_decoder {
     KParams kp{};              // weights + dims (batch fields filled per call)
     pk_decoder_desc desc{};    // host copy of the description (tensor pointers not kept)
-    DMat w_enc{};              // joint.enc.weight on the device
-    const float *b_enc = nullptr;
+    const float *w_enc = nullptr, *b_enc = nullptr;   // joint.enc dense f32 [J][D], bias
     int n_slots = 0;
     int device = 0;
     int n_cu = 0, lds_block = 0;
     int nwg = 0;               // decode-loop workgroups
-    size_t stage_bytes = 0;
+    size_t lds_bytes = 0;      // dynamic LDS of the decode loop
     hipStream_t stream = nullptr;
     hipEvent_t ev[3] = {};
     DevBuf arena;              // weights
@@ -198,36 +253,89 @@ struct pk_decoder {
 
 namespace {
 
-int upload_weights(pk_decoder *dec, std::vector<HostMat> &mats, std::vector<std::vector<float>> &vecs,
-                   std::vector<DMat *> &mat_dst, std::vector<const float **> &vec_dst) {
-    size_t total = 0;
-    auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    for (auto &m : mats) total += align(m.w.size()) + align(m.d.size() * 4);
-    for (auto &v : vecs) total += align(v.size() * 4);
-    if (int rc = dec->arena.ensure(total)) return rc;
-    uint8_t *base = dec->arena.as<uint8_t>();
-    size_t off = 0;
-    for (size_t i = 0; i < mats.size(); ++i) {
-        DMat &dm = *mat_dst[i];
-        dm.type = mats[i].type;
-        dm.rows = mats[i].rows;
-        dm.cols = mats[i].cols;
-        HIP_TRY(hipMemcpy(base + off, mats[i].w.data(), mats[i].w.size(), hipMemcpyHostToDevice));
-        dm.w = base + off;
-        off += align(mats[i].w.size());
-        dm.d = nullptr;
-        if (!mats[i].d.empty()) {
-            HIP_TRY(hipMemcpy(base + off, mats[i].d.data(), mats[i].d.size() * 4, hipMemcpyHostToDevice));
-            dm.d = reinterpret_cast<const float *>(base + off);
-            off += align(mats[i].d.size() * 4);
+// One device arena for every weight plane and bias.
+struct Arena {
+    std::vector<std::pair<const void *, size_t>> parts;
+    std::vector<const void **> dst;
+    void add(const void *host, size_t bytes, const void **where) {
+        parts.emplace_back(host, bytes);
+        dst.push_back(where);
+    }
+    int upload(DevBuf &buf) {
+        auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+        size_t total = 0;
+        for (auto &p : parts) total += align(p.second);
+        if (int rc = buf.ensure(std::max<size_t>(total, 256))) return rc;
+        size_t off = 0;
+        for (size_t i = 0; i < parts.size(); ++i) {
+            uint8_t *d = buf.as<uint8_t>() + off;
+            if (parts[i].second) HIP_TRY(hipMemcpy(d, parts[i].first, parts[i].second, hipMemcpyHostToDevice));
+            *dst[i] = parts[i].second ? d : nullptr;
+            off += align(parts[i].second);
         }
+        return 0;
     }
-    for (size_t i = 0; i < vecs.size(); ++i) {
-        HIP_TRY(hipMemcpy(base + off, vecs[i].data(), vecs[i].size() * 4, hipMemcpyHostToDevice));
-        *vec_dst[i] = reinterpret_cast<const float *>(base + off);
-        off += align(vecs[i].size() * 4);
+};
+
+void arena_tiled(Arena &ar, HostTiled &h, TMat &m) {
+    m.type = h.type;
+    m.rows = h.rows;
+    m.tiles = h.tiles;
+    m.KB = h.KB;
+    ar.add(h.a.data(), h.a.size(), &m.a);
+    ar.add(h.a_lo.data(), h.a_lo.size(), &m.a_lo);
+    ar.add(h.scale.data(), h.scale.size() * 4, reinterpret_cast<const void **>(&m.scale));
+}
+
+// Domain plan for m utterances over nwg workgroups (see KParams::n_dom).
+struct Plan {
+    int n_dom = 1, P = 0, nt = 1;
+    std::vector<int> dom_n, dom_list, wg_dom, wg_rank, dom_wg;
+};
+
+Plan plan_domains(int m, int nwg, const std::vector<int32_t> &T) {
+    Plan pl;
+    int C, nt;
+    if (m <= kTile) { C = 1; nt = 1; }
+    else if (m <= 8 * kTile) { nt = 1; C = 1; while (C * kTile < m) C *= 2; }
+    else { nt = 2; C = 1; while (C * 2 * kTile < m) C *= 2; }
+    while (C > 1 && nwg / C < 8) C /= 2;      // at least 8 workgroups per domain
+    pl.n_dom = C;
+    pl.nt = nt;
+    pl.P = nwg / C;
+    // utterances dealt longest-first round robin, so every domain sees a similar length mix
+    std::vector<int> order(m);
+    std::iota(order.begin(), order.end(), 0);
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return T[a] > T[b]; });
+    pl.dom_n.assign(C, 0);
+    pl.dom_list.assign((size_t)C * kDomCap, 0);
+    for (int i = 0; i < m; ++i) {
+        const int d = i % C;
+        if (pl.dom_n[d] < kDomCap) pl.dom_list[(size_t)d * kDomCap + pl.dom_n[d]] = order[i];
+        ++pl.dom_n[d];
     }
-    return 0;
+    // workgroup -> (domain, rank); with 8 XCDs dispatched round robin, rank r
+    // of every domain sits on XCD r % 8, so the weight tiles of rank r share
+    // one L2 across domains
+    pl.wg_dom.assign(nwg, 0);
+    pl.wg_rank.assign(nwg, 0);
+    pl.dom_wg.assign((size_t)C * pl.P, 0);
+    const bool xcd = nwg % (8 * C) == 0;
+    for (int wg = 0; wg < C * pl.P; ++wg) {
+        int d, r;
+        if (xcd) {
+            const int x = wg % 8, j = wg / 8;
+            d = j % C;
+            r = x + 8 * (j / C);
+        } else {
+            d = wg / pl.P;
+            r = wg % pl.P;
+        }
+        pl.wg_dom[wg] = d;
+        pl.wg_rank[wg] = r;
+        pl.dom_wg[(size_t)d * pl.P + r] = wg;
+    }
+    return pl;
 }
 
 int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty);
@@ -260,16 +368,19 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     if (d->kind != PK_KIND_TDT && d->kind != PK_KIND_EOU) return fail(PK_ERR_ARG, "unknown decoder kind %d", d->kind);
     if (H <= 0 || J <= 0 || D <= 0 || L <= 0 || L > PK_MAX_LAYERS || d->vocab_size <= 0)
         return fail(PK_ERR_ARG, "bad dims H=%d L=%d J=%d D=%d V=%d", H, L, J, D, d->vocab_size);
+    if (H % 32 || J % 32 || D % 4)
+        return fail(PK_ERR_UNSUPPORTED, "pred_hidden and joint_hidden must be multiples of 32, d_enc of 4");
     if (d->kind == PK_KIND_TDT && (Dn <= 0 || Dn > PK_MAX_DURATIONS))
         return fail(PK_ERR_UNSUPPORTED, "TDT num_durations %d", Dn);
     if (d->kind == PK_KIND_TDT && d->n_duration_values > 0 && d->n_duration_values < Dn)
         return fail(PK_ERR_ARG, "durations table (%d) shorter than num_durations (%d)", d->n_duration_values, Dn);
-    if (V1 > (1 << kIdxBits) - 1 || Dn > (1 << kIdxBits) - 1)
-        return fail(PK_ERR_UNSUPPORTED, "vocab %d exceeds the argmax key index field", V1);
+    if (V1 > (1 << kIdxBits) - 1) return fail(PK_ERR_UNSUPPORTED, "vocab %d exceeds the argmax key index field", V1);
     if (d->blank_id < 0 || d->blank_id >= V1) return fail(PK_ERR_ARG, "blank_id %d outside [0,%d)", d->blank_id, V1);
 
     auto *dec = new pk_decoder();
+    auto cleanup = [&](int rc) { delete dec; return rc; };
     dec->desc = *d;
+    dec->desc.special = nullptr;
     dec->n_slots = n_slots;
     KParams &kp = dec->kp;
     kp.kind = d->kind; kp.H = H; kp.L = L; kp.J = J; kp.V1 = V1; kp.Dn = Dn; kp.Vo = Vo;
@@ -279,7 +390,6 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     kp.n_dur = d->kind == PK_KIND_TDT ? d->n_duration_values : 0;
     for (int i = 0; i < PK_MAX_DURATIONS; ++i) kp.durations[i] = d->durations[i];
 
-    auto cleanup = [&](int rc) { delete dec; return rc; };
     if (hipGetDevice(&dec->device) != hipSuccess) return cleanup(fail(PK_ERR_DEVICE, "no HIP device"));
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, dec->device) != hipSuccess) return cleanup(fail(PK_ERR_DEVICE, "device props"));
@@ -291,63 +401,64 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     for (int j = 0; j < H; ++j)
         for (int g = 0; g < 4; ++g) gmap[4 * j + g] = g * H + j;
 
-    std::vector<HostMat> mats;
-    std::vector<DMat *> mat_dst;
-    std::vector<std::vector<float>> vecs;
-    std::vector<const float **> vec_dst;
-    mats.reserve(4 + 2 * L);
     int rc;
-    auto add_mat = [&](const pk_tensor &t, int rows, int cols, const std::vector<int> *map, DMat *dst,
-                       const char *name) {
-        mats.emplace_back();
-        mat_dst.push_back(dst);
-        return repack(t, rows, cols, map, mats.back(), name);
-    };
-    auto add_vec = [&](const pk_tensor &t, int n, const std::vector<int> *map, const float **dst, const char *name) {
-        vecs.emplace_back();
-        vec_dst.push_back(dst);
-        return vec_f32(t, n, map, vecs.back(), name);
-    };
-    DMat embed{};
-    const float *b_ih0 = nullptr, *b_hh0 = nullptr;
-    if ((rc = add_mat(d->embed, V1, H, nullptr, &embed, "predict.embed.weight"))) return cleanup(rc);
+    Arena ar;
+    std::vector<HostTiled> tiled(2 * L + 2);
+    std::vector<std::vector<float>> vecs(L + 2);
     for (int l = 0; l < L; ++l) {
-        if ((rc = add_mat(d->w_ih[l], 4 * H, H, &gmap, &kp.w_ih[l], "predict.lstm.w_ih"))) return cleanup(rc);
-        if ((rc = add_mat(d->w_hh[l], 4 * H, H, &gmap, &kp.w_hh[l], "predict.lstm.w_hh"))) return cleanup(rc);
-        std::vector<float> bi, bh;
-        if ((rc = vec_f32(d->b_ih[l], 4 * H, &gmap, bi, "predict.lstm.b_ih"))) return cleanup(rc);
-        if ((rc = vec_f32(d->b_hh[l], 4 * H, &gmap, bh, "predict.lstm.b_hh"))) return cleanup(rc);
-        if (l == 0) {
-            vecs.push_back(bi);
-            vec_dst.push_back(&b_ih0);
-            vecs.push_back(bh);
-            vec_dst.push_back(&b_hh0);
-        } else {
-            for (int i = 0; i < 4 * H; ++i) bi[i] += bh[i];
-            vecs.push_back(bi);
-            vec_dst.push_back(&kp.b_lstm[l]);
+        if (l > 0) {
+            if ((rc = tile_matrix(d->w_ih[l], 4 * H, H, &gmap, tiled[2 * l], "predict.lstm.w_ih"))) return cleanup(rc);
+            arena_tiled(ar, tiled[2 * l], kp.w_ih[l]);
+            std::vector<float> bh;
+            if ((rc = vec_f32(d->b_ih[l], 4 * H, &gmap, vecs[l], "predict.lstm.b_ih"))) return cleanup(rc);
+            if ((rc = vec_f32(d->b_hh[l], 4 * H, &gmap, bh, "predict.lstm.b_hh"))) return cleanup(rc);
+            for (int i = 0; i < 4 * H; ++i) vecs[l][i] += bh[i];
+            ar.add(vecs[l].data(), vecs[l].size() * 4, reinterpret_cast<const void **>(&kp.b_lstm[l]));
         }
+        if ((rc = tile_matrix(d->w_hh[l], 4 * H, H, &gmap, tiled[2 * l + 1], "predict.lstm.w_hh"))) return cleanup(rc);
+        arena_tiled(ar, tiled[2 * l + 1], kp.w_hh[l]);
     }
-    if ((rc = add_mat(d->joint_enc_w, J, D, nullptr, &dec->w_enc, "joint.enc.weight"))) return cleanup(rc);
-    if ((rc = add_vec(d->joint_enc_b, J, nullptr, &dec->b_enc, "joint.enc.bias"))) return cleanup(rc);
-    if ((rc = add_mat(d->joint_pred_w, J, H, nullptr, &kp.w_pred, "joint.pred.weight"))) return cleanup(rc);
-    if ((rc = add_vec(d->joint_pred_b, J, nullptr, &kp.b_pred, "joint.pred.bias"))) return cleanup(rc);
-    if ((rc = add_mat(d->joint_out_w, Vo, J, nullptr, &kp.w_out, "joint.out.weight"))) return cleanup(rc);
-    if ((rc = add_vec(d->joint_out_b, Vo, nullptr, &kp.b_out, "joint.out.bias"))) return cleanup(rc);
-    if (H % 4 || J % 4) return cleanup(fail(PK_ERR_UNSUPPORTED, "pred_hidden and joint_hidden must be multiples of 4"));
-    if ((rc = upload_weights(dec, mats, vecs, mat_dst, vec_dst))) return cleanup(rc);
-    // layer-0 input projection of every token: E'[v] = W_ih0 . embed[v] + b_ih0 + b_hh0
-    if ((rc = dec->eproj.ensure((size_t)V1 * 4 * H * 4))) return cleanup(rc);
+    if ((rc = tile_matrix(d->joint_pred_w, J, H, nullptr, tiled[2 * L], "joint.pred.weight"))) return cleanup(rc);
+    arena_tiled(ar, tiled[2 * L], kp.w_pred);
+    if ((rc = tile_matrix(d->joint_out_w, Vo, J, nullptr, tiled[2 * L + 1], "joint.out.weight"))) return cleanup(rc);
+    arena_tiled(ar, tiled[2 * L + 1], kp.w_out);
+    std::vector<float> b_pred, b_out, b_enc, w_enc;
+    if ((rc = vec_f32(d->joint_pred_b, J, nullptr, b_pred, "joint.pred.bias"))) return cleanup(rc);
+    if ((rc = vec_f32(d->joint_out_b, Vo, nullptr, b_out, "joint.out.bias"))) return cleanup(rc);
+    if ((rc = vec_f32(d->joint_enc_b, J, nullptr, b_enc, "joint.enc.bias"))) return cleanup(rc);
+    if ((rc = dense_f32(d->joint_enc_w, J, D, nullptr, w_enc, "joint.enc.weight"))) return cleanup(rc);
+    ar.add(b_pred.data(), b_pred.size() * 4, reinterpret_cast<const void **>(&kp.b_pred));
+    ar.add(b_out.data(), b_out.size() * 4, reinterpret_cast<const void **>(&kp.b_out));
+    ar.add(b_enc.data(), b_enc.size() * 4, reinterpret_cast<const void **>(&dec->b_enc));
+    ar.add(w_enc.data(), w_enc.size() * 4, reinterpret_cast<const void **>(&dec->w_enc));
+    if ((rc = ar.upload(dec->arena))) return cleanup(rc);
+
+    // layer-0 input projection of every token: E'[v] = W_ih0 . embed[v] + b_ih0 + b_hh0 (f32)
     {
+        std::vector<float> w0, emb, bi, bh;
+        if ((rc = dense_f32(d->w_ih[0], 4 * H, H, &gmap, w0, "predict.lstm.0.w_ih"))) return cleanup(rc);
+        if ((rc = dense_f32(d->embed, V1, H, nullptr, emb, "predict.embed.weight"))) return cleanup(rc);
+        if ((rc = vec_f32(d->b_ih[0], 4 * H, &gmap, bi, "predict.lstm.0.b_ih"))) return cleanup(rc);
+        if ((rc = vec_f32(d->b_hh[0], 4 * H, &gmap, bh, "predict.lstm.0.b_hh"))) return cleanup(rc);
+        DevBuf tmp;
+        const size_t nw = w0.size(), ne = emb.size();
+        if ((rc = tmp.ensure((nw + ne + 8 * (size_t)H) * 4))) return cleanup(rc);
+        float *dw = tmp.as<float>(), *de = dw + nw, *dbi = de + ne, *dbh = dbi + 4 * H;
+        if (hipMemcpy(dw, w0.data(), nw * 4, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(de, emb.data(), ne * 4, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(dbi, bi.data(), 16 * (size_t)H, hipMemcpyHostToDevice) != hipSuccess ||
+            hipMemcpy(dbh, bh.data(), 16 * (size_t)H, hipMemcpyHostToDevice) != hipSuccess)
+            return cleanup(fail(PK_ERR_DEVICE, "embedding projection upload"));
+        if ((rc = dec->eproj.ensure((size_t)V1 * 4 * H * 4))) return cleanup(rc);
         dim3 grid((V1 + 15) / 16, (4 * H + 63) / 64);
-        pkdev::embed_proj_kernel<<<grid, 256>>>(kp.w_ih[0], embed, b_ih0, b_hh0, dec->eproj.as<float>());
+        pkdev::embed_proj_kernel<<<grid, 256>>>(dw, de, 4 * H, V1, H, dbi, dbh, dec->eproj.as<float>());
         if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess)
             return cleanup(fail(PK_ERR_DEVICE, "embedding projection kernel failed"));
+        kp.eproj = dec->eproj.as<float>();
     }
-    kp.eproj = dec->eproj.as<float>();
-    dec->desc.special = nullptr;
-    dec->kp.special = nullptr;
-    dec->kp.n_special = 0;
+
+    kp.special = nullptr;
+    kp.n_special = 0;
     if (d->special && d->n_special > 0) {
         if ((rc = dec->special.ensure(d->n_special))) return cleanup(rc);
         if (hipMemcpy(dec->special.p, d->special, d->n_special, hipMemcpyHostToDevice) != hipSuccess)
@@ -371,12 +482,15 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     kp.slot_pp = dec->slots_pp.as<float>();
     kp.slot_ctrl = dec->slots_ctrl.as<int>();
 
-    // decode-loop launch shape: one workgroup per CU, LDS stage for kUC utterances
-    const size_t need = std::max((size_t)kUC * (J + L * H), (size_t)kSmallB * H) * 4;
-    if (need + sizeof(pkdev::Ctl) > (size_t)dec->lds_block)
+    // decode-loop launch shape: one workgroup per CU; LDS = activation blocks
+    // [hidden | h_0 .. h_{L-1}] of one 16-utterance tile + K-split partials +
+    // the redundant layer-0 output
+    const size_t act = (size_t)kTile * ((J + kKPad) + (size_t)L * (H + kKPad)) * 2 * 2;
+    const size_t need = act + (size_t)kWaves * kWave * 16 + (size_t)kSmallB * H * 4;
+    if (need + sizeof(pkdev::Ctl) + 256 > (size_t)dec->lds_block)
         return cleanup(fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed, %d available", need + sizeof(pkdev::Ctl),
                             dec->lds_block));
-    dec->stage_bytes = need;
+    dec->lds_bytes = need;
     if (hipFuncSetAttribute(reinterpret_cast<const void *>(pkdev::decode_loop_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)need) != hipSuccess)
         return cleanup(fail(PK_ERR_DEVICE, "hipFuncSetAttribute"));
@@ -440,14 +554,12 @@ PK_API int pk_slot_read(pk_decoder *dec, int32_t slot, float *h, float *c, float
     if (!dec || slot < 0 || slot >= dec->n_slots) return fail(PK_ERR_ARG, "pk_slot_read: bad slot");
     HIP_TRY(hipSetDevice(dec->device));
     const KParams &kp = dec->kp;
-    int32_t cw[PK_CTRL_N];
-    HIP_TRY(hipMemcpy(cw, kp.slot_ctrl + (size_t)slot * PK_CTRL_N, sizeof cw, hipMemcpyDeviceToHost));
     const size_t hn = (size_t)kp.L * kp.H;
+    if (ctrl) HIP_TRY(hipMemcpy(ctrl, kp.slot_ctrl + (size_t)slot * PK_CTRL_N, PK_CTRL_N * 4, hipMemcpyDeviceToHost));
     if (h) HIP_TRY(hipMemcpy(h, kp.slot_h + (size_t)slot * hn, hn * 4, hipMemcpyDeviceToHost));
     if (c) HIP_TRY(hipMemcpy(c, kp.slot_c + (size_t)slot * hn, hn * 4, hipMemcpyDeviceToHost));
     if (pred) HIP_TRY(hipMemcpy(pred, kp.slot_h + (size_t)slot * hn + (size_t)(kp.L - 1) * kp.H,
                                 (size_t)kp.H * 4, hipMemcpyDeviceToHost));
-    if (ctrl) memcpy(ctrl, cw, sizeof cw);
     return 0;
 }
 
@@ -473,8 +585,9 @@ namespace {
 
 int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     if (!dec || !bt) return fail(PK_ERR_ARG, "pk_decode: null argument");
-    const KParams &kp = dec->kp;
-    if (bt->d_enc != dec->desc.d_enc) return fail(PK_ERR_D_ENC, "encoder d_model mismatch (%d vs %d)", bt->d_enc, dec->desc.d_enc);
+    KParams &p = dec->kp;
+    if (bt->d_enc != dec->desc.d_enc)
+        return fail(PK_ERR_D_ENC, "encoder d_model mismatch (%d vs %d)", bt->d_enc, dec->desc.d_enc);
     const int n = bt->n_utts;
     if (n < 0 || n > kMaxBatch) return fail(PK_ERR_ARG, "n_utts %d outside [0,%d]", n, kMaxBatch);
     if (n == 0) return 0;
@@ -492,8 +605,17 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     // TDT windows with no frames return before initialising (src/parakeet_tdt.cpp:879).
     std::vector<int> map;
     for (int u = 0; u < n; ++u)
-        if (keep_empty || kp.kind == PK_KIND_EOU || bt->n_frames[u] > 0) map.push_back(u);
+        if (keep_empty || p.kind == PK_KIND_EOU || bt->n_frames[u] > 0) map.push_back(u);
     const int m = (int)map.size();
+    const bool host = bt->mem == PK_MEM_HOST;
+    if (!host && m != n) return fail(PK_ERR_ARG, "device-memory batches must not contain empty TDT windows");
+    if (host)
+        for (int u = 0; u < n; ++u) {   // outputs of utterances that do not run
+            bt->n_tokens[u] = 0;
+            bt->steps[u] = 0;
+            if (bt->n_segments) bt->n_segments[u] = 0;
+        }
+    if (m == 0) return 0;
     long long rows = 0;
     int max_T = 0;
     std::vector<long long> src_row(m), dst_row(m);
@@ -510,8 +632,9 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         bias[i] = bt->blank_bias ? bt->blank_bias[u] : 0.0f;
         base[i] = bt->tokens_base ? bt->tokens_base[u] : 0;
     }
-    const bool host = bt->mem == PK_MEM_HOST;
-    const int D = dec->desc.d_enc, J = kp.J;
+    const int max_iter = max_T * (std::max(bt->max_symbols, 1) + 1) + 4;
+    if ((unsigned)max_iter >= kMaxStamp) return fail(PK_ERR_UNSUPPORTED, "window too long for the iteration stamp");
+    const int D = dec->desc.d_enc, J = p.J, L = p.L, H = p.H;
     int rc;
     // encoder frames: device pointer as given, or packed host rows uploaded
     const float *enc = bt->enc;
@@ -523,98 +646,105 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         enc = dec->d_enc.as<float>();
         src_row = dst_row;
     }
-    // descriptor block: src_row, dst_row (int64), T, slot, base (int32), bias (f32)
-    const size_t desc_bytes = (size_t)m * (8 + 8 + 4 + 4 + 4 + 4);
-    if ((rc = dec->d_desc.ensure(std::max<size_t>(desc_bytes, 64)))) return rc;
+    const Plan pl = plan_domains(m, dec->nwg, T);
+    const int nwg = pl.n_dom * pl.P;
+    for (int d = 0; d < pl.n_dom; ++d)
+        if (pl.dom_n[d] > kDomCap) return fail(PK_ERR_UNSUPPORTED, "batch of %d too large for %d compute units", m, dec->nwg);
+    // descriptor block (device): int64 src_row, dst_row; int32 T, slot, base; f32 bias;
+    // int32 dom_n, dom_list, wg_dom, wg_rank, dom_wg
+    const size_t n64 = 2 * (size_t)m, n32 = 4 * (size_t)m + pl.dom_n.size() + pl.dom_list.size() +
+                                              pl.wg_dom.size() + pl.wg_rank.size() + pl.dom_wg.size();
+    const size_t desc_bytes = n64 * 8 + n32 * 4;
+    if ((rc = dec->d_desc.ensure(desc_bytes))) return rc;
     dec->h_desc.resize(desc_bytes);
     uint8_t *hd = dec->h_desc.data();
-    memcpy(hd, src_row.data(), 8 * (size_t)m);
-    memcpy(hd + 8 * (size_t)m, dst_row.data(), 8 * (size_t)m);
-    memcpy(hd + 16 * (size_t)m, T.data(), 4 * (size_t)m);
-    memcpy(hd + 20 * (size_t)m, slots.data(), 4 * (size_t)m);
-    memcpy(hd + 24 * (size_t)m, base.data(), 4 * (size_t)m);
-    memcpy(hd + 28 * (size_t)m, bias.data(), 4 * (size_t)m);
-    if (m > 0) HIP_TRY(hipMemcpyAsync(dec->d_desc.p, hd, desc_bytes, hipMemcpyHostToDevice, dec->stream));
-    uint8_t *dd = dec->d_desc.as<uint8_t>();
-    const long long *d_src = reinterpret_cast<const long long *>(dd);
-    const long long *d_dst = reinterpret_cast<const long long *>(dd + 8 * (size_t)m);
-    const int *d_T = reinterpret_cast<const int *>(dd + 16 * (size_t)m);
-    const int *d_slot = reinterpret_cast<const int *>(dd + 20 * (size_t)m);
-    const int *d_base = reinterpret_cast<const int *>(dd + 24 * (size_t)m);
-    const float *d_bias = reinterpret_cast<const float *>(dd + 28 * (size_t)m);
+    size_t off = 0;
+    auto put = [&](const void *src, size_t bytes) {
+        memcpy(hd + off, src, bytes);
+        const size_t at = off;
+        off += bytes;
+        return dec->d_desc.as<uint8_t>() + at;
+    };
+    const long long *d_src = reinterpret_cast<const long long *>(put(src_row.data(), 8 * (size_t)m));
+    const long long *d_dst = reinterpret_cast<const long long *>(put(dst_row.data(), 8 * (size_t)m));
+    const int *d_T = reinterpret_cast<const int *>(put(T.data(), 4 * (size_t)m));
+    const int *d_slot = reinterpret_cast<const int *>(put(slots.data(), 4 * (size_t)m));
+    const int *d_base = reinterpret_cast<const int *>(put(base.data(), 4 * (size_t)m));
+    const float *d_bias = reinterpret_cast<const float *>(put(bias.data(), 4 * (size_t)m));
+    const int *d_dom_n = reinterpret_cast<const int *>(put(pl.dom_n.data(), 4 * pl.dom_n.size()));
+    const int *d_dom_list = reinterpret_cast<const int *>(put(pl.dom_list.data(), 4 * pl.dom_list.size()));
+    const int *d_wg_dom = reinterpret_cast<const int *>(put(pl.wg_dom.data(), 4 * pl.wg_dom.size()));
+    const int *d_wg_rank = reinterpret_cast<const int *>(put(pl.wg_rank.data(), 4 * pl.wg_rank.size()));
+    const int *d_dom_wg = reinterpret_cast<const int *>(put(pl.dom_wg.data(), 4 * pl.dom_wg.size()));
+    HIP_TRY(hipMemcpyAsync(dec->d_desc.p, hd, desc_bytes, hipMemcpyHostToDevice, dec->stream));
 
     HIP_TRY(hipEventRecord(dec->ev[0], dec->stream));
     if (rows > 0) {
         if ((rc = dec->d_encp.ensure((size_t)rows * J * 4))) return rc;
         dim3 grid((max_T + 63) / 64, m, (J + 63) / 64);
-        pkdev::enc_proj_kernel<<<grid, 256, 0, dec->stream>>>(dec->w_enc, dec->b_enc, enc, D,
-                                                       d_src, d_dst, d_T, dec->d_encp.as<float>());
+        pkdev::enc_proj_kernel<<<grid, 256, 0, dec->stream>>>(dec->w_enc, J, dec->b_enc, enc, D, d_src, d_dst, d_T,
+                                                              dec->d_encp.as<float>());
         HIP_TRY(hipGetLastError());
     }
     HIP_TRY(hipEventRecord(dec->ev[1], dec->stream));
 
     // outputs: device arrays as given, or a device staging area copied back
-    const int tcap = bt->token_cap, scap = bt->seg_cap, trcap = bt->trace ? bt->trace_cap : 0;
+    const int tcap = bt->token_cap, scap = std::max(bt->seg_cap, 0), trcap = bt->trace ? bt->trace_cap : 0;
     int *o_tok, *o_ntok, *o_steps, *o_seg = nullptr, *o_nseg = nullptr, *o_trace = nullptr;
-    std::vector<int> idx_map = map;
     if (host) {
-        const size_t need = ((size_t)m * tcap + 3 * (size_t)m + (size_t)m * std::max(scap, 0) +
-                             (size_t)m * trcap * 2) * 4 + 64;
+        const size_t need = ((size_t)m * tcap + 3 * (size_t)m + (size_t)m * scap + (size_t)m * trcap * 2) * 4 + 64;
         if ((rc = dec->d_out.ensure(need))) return rc;
         int *o = dec->d_out.as<int>();
         o_tok = o; o += (size_t)m * tcap;
         o_ntok = o; o += m;
         o_steps = o; o += m;
         o_nseg = o; o += m;
-        o_seg = scap > 0 ? o : nullptr; o += (size_t)m * std::max(scap, 0);
+        o_seg = scap > 0 ? o : nullptr; o += (size_t)m * scap;
         o_trace = trcap > 0 ? o : nullptr;
     } else {
-        if (m != n) return fail(PK_ERR_ARG, "device-memory batches must not contain empty TDT windows");
         o_tok = bt->tokens; o_ntok = bt->n_tokens; o_steps = bt->steps;
         o_seg = bt->segments; o_nseg = bt->n_segments; o_trace = bt->trace;
     }
-    // launch with the device descriptor arrays
-    KParams &p = dec->kp;
-    (void)d_base;
-    rc = 0;
-    {
-        p.n_utts = m;
-        p.encp = dec->d_encp.as<float>();
-        p.encp_row = d_dst;
-        p.T = d_T;
-        p.slot = d_slot;
-        p.blank_bias = bt->blank_bias ? d_bias : nullptr;
-        p.tokens_base = bt->tokens_base ? d_base : nullptr;
-        p.tokens = o_tok; p.token_cap = tcap;
-        p.n_tokens = o_ntok; p.steps = o_steps;
-        p.segs = o_seg; p.seg_cap = scap; p.n_segs = o_nseg;
-        p.trace = o_trace; p.trace_cap = trcap;
-        p.max_sym = bt->max_symbols;
-        p.max_iter = max_T * (std::max(bt->max_symbols, 1) + 1) + 4;
-        if ((unsigned)p.max_iter >= kMaxStamp) return fail(PK_ERR_UNSUPPORTED, "window too long for the iteration stamp");
-        if ((rc = dec->d_keys.ensure((size_t)2 * std::max(m, 1) * 2 * 8))) return rc;
-        if ((rc = dec->d_sync.ensure(64))) return rc;
-        if ((rc = dec->d_flags.ensure((size_t)dec->nwg * kFlagStride * 4))) return rc;
-        const int L = kp.L, H = kp.H;
-        const size_t mm = std::max(m, 1);
-        const size_t xh = 2 * (size_t)L * mm * H, xp = mm * J, xr = (size_t)L * mm * 4 * H;
-        if ((rc = dec->d_xchg.ensure((2 * xh + xp + xr) * 4))) return rc;
-        p.hx = dec->d_xchg.as<float>();
-        p.cx = p.hx + xh;
-        p.ppx = p.cx + xh;
-        p.rx = p.ppx + xp;
-        p.keys = dec->d_keys.as<unsigned long long>();
-        p.flags = dec->d_flags.as<unsigned>();
-        p.status = dec->d_sync.as<int>() + 4;
-        HIP_TRY(hipMemsetAsync(dec->d_keys.p, 0, (size_t)2 * std::max(m, 1) * 2 * 8, dec->stream));
-        HIP_TRY(hipMemsetAsync(dec->d_sync.p, 0, 64, dec->stream));
-        HIP_TRY(hipMemsetAsync(dec->d_flags.p, 0, (size_t)dec->nwg * kFlagStride * 4, dec->stream));
-        void *args[] = {&p};
-        if (m > 0) {
-            HIP_TRY(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(pkdev::decode_loop_kernel), dim3(dec->nwg),
-                                               dim3(kBlock), args, dec->stage_bytes, dec->stream));
-        }
-    }
+    p.n_utts = m;
+    p.encp = dec->d_encp.as<float>();
+    p.encp_row = d_dst;
+    p.T = d_T;
+    p.slot = d_slot;
+    p.blank_bias = bt->blank_bias ? d_bias : nullptr;
+    p.tokens_base = bt->tokens_base ? d_base : nullptr;
+    p.tokens = o_tok; p.token_cap = tcap;
+    p.n_tokens = o_ntok; p.steps = o_steps;
+    p.segs = o_seg; p.seg_cap = scap; p.n_segs = o_nseg;
+    p.trace = o_trace; p.trace_cap = trcap;
+    p.max_sym = bt->max_symbols;
+    p.max_iter = max_iter;
+    p.n_dom = pl.n_dom;
+    p.dom_size = pl.P;
+    p.nt = pl.nt;
+    p.dom_n = d_dom_n;
+    p.dom_list = d_dom_list;
+    p.wg_dom = d_wg_dom;
+    p.wg_rank = d_wg_rank;
+    p.dom_wg = d_dom_wg;
+    const size_t keys_bytes = (size_t)2 * m * 2 * 8;
+    if ((rc = dec->d_keys.ensure(keys_bytes))) return rc;
+    if ((rc = dec->d_sync.ensure(64))) return rc;
+    if ((rc = dec->d_flags.ensure((size_t)nwg * kFlagStride * 4))) return rc;
+    const size_t xh = 2 * (size_t)L * m * H, xp = (size_t)m * J, xr = (size_t)L * m * 4 * H;
+    if ((rc = dec->d_xchg.ensure((2 * xh + xp + xr) * 4))) return rc;
+    p.hx = dec->d_xchg.as<float>();
+    p.cx = p.hx + xh;
+    p.ppx = p.cx + xh;
+    p.rx = p.ppx + xp;
+    p.keys = dec->d_keys.as<unsigned long long>();
+    p.flags = dec->d_flags.as<unsigned>();
+    p.status = dec->d_sync.as<int>() + 4;
+    HIP_TRY(hipMemsetAsync(dec->d_keys.p, 0, keys_bytes, dec->stream));
+    HIP_TRY(hipMemsetAsync(dec->d_sync.p, 0, 64, dec->stream));
+    HIP_TRY(hipMemsetAsync(dec->d_flags.p, 0, (size_t)nwg * kFlagStride * 4, dec->stream));
+    void *args[] = {&p};
+    HIP_TRY(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(pkdev::decode_loop_kernel), dim3(nwg),
+                                       dim3(kBlock), args, dec->lds_bytes, dec->stream));
     HIP_TRY(hipEventRecord(dec->ev[2], dec->stream));
     int status[4] = {0, 0, 0, 0};
     HIP_TRY(hipMemcpyAsync(status, p.status, sizeof status, hipMemcpyDeviceToHost, dec->stream));
@@ -624,24 +754,26 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         HIP_TRY(hipMemcpyAsync(tmp_steps.data(), o_steps, 4 * (size_t)m, hipMemcpyDeviceToHost, dec->stream));
         HIP_TRY(hipMemcpyAsync(tmp_nseg.data(), o_nseg, 4 * (size_t)m, hipMemcpyDeviceToHost, dec->stream));
         HIP_TRY(hipStreamSynchronize(dec->stream));
-        for (int u = 0; u < n; ++u) { bt->n_tokens[u] = 0; bt->steps[u] = 0; if (bt->n_segments) bt->n_segments[u] = 0; }
         for (int i = 0; i < m; ++i) {
             const int u = map[i];
             bt->n_tokens[u] = tmp_ntok[i];
             bt->steps[u] = tmp_steps[i];
             const int nt = std::min(tmp_ntok[i], tcap);
             if (nt > 0)
-                HIP_TRY(hipMemcpy(bt->tokens + (size_t)u * tcap, o_tok + (size_t)i * tcap, 4 * (size_t)nt, hipMemcpyDeviceToHost));
+                HIP_TRY(hipMemcpy(bt->tokens + (size_t)u * tcap, o_tok + (size_t)i * tcap, 4 * (size_t)nt,
+                                  hipMemcpyDeviceToHost));
             if (bt->n_segments) bt->n_segments[u] = tmp_nseg[i];
             if (bt->segments && scap > 0) {
                 const int ns = std::min(tmp_nseg[i], scap);
                 if (ns > 0)
-                    HIP_TRY(hipMemcpy(bt->segments + (size_t)u * scap, o_seg + (size_t)i * scap, 4 * (size_t)ns, hipMemcpyDeviceToHost));
+                    HIP_TRY(hipMemcpy(bt->segments + (size_t)u * scap, o_seg + (size_t)i * scap, 4 * (size_t)ns,
+                                      hipMemcpyDeviceToHost));
             }
             if (o_trace) {
                 const int ns = std::min(tmp_steps[i], trcap);
                 if (ns > 0)
-                    HIP_TRY(hipMemcpy(bt->trace + (size_t)u * trcap * 2, o_trace + (size_t)i * trcap * 2, 8 * (size_t)ns, hipMemcpyDeviceToHost));
+                    HIP_TRY(hipMemcpy(bt->trace + (size_t)u * trcap * 2, o_trace + (size_t)i * trcap * 2,
+                                      8 * (size_t)ns, hipMemcpyDeviceToHost));
             }
         }
     } else {

@@ -2,8 +2,8 @@
 //
 // Included once, by pk_decode.hip.  See that file for the host side and the
 // overall structure; this file holds the data layout, the building blocks
-// (weight loads, wave reductions, argmax keys, grid barrier, coherent loads
-// and stores) and the kernels.
+// (MFMA tiles over q8_0 / f16 weights, argmax keys, domain barrier, coherent
+// loads and stores) and the kernels.
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -16,13 +16,15 @@ namespace pkdev {
 constexpr int kWave = 64;
 constexpr int kBlock = 512;                 // 8 waves per workgroup, one workgroup per CU
 constexpr int kWaves = kBlock / kWave;
-constexpr int kMaxBatch = PK_MAX_BATCH;
-constexpr int kUC = 8;                      // utterances per register tile
+constexpr int kTile = 16;                   // MFMA tile edge (rows = outputs, columns = utterances)
+constexpr int kMaxNT = 2;                   // utterance tiles per domain
+constexpr int kDomCap = kTile * kMaxNT;     // utterances per domain
 constexpr int kSmallB = 4;                  // LSTM batch at or below which layer 0 runs redundantly
 constexpr int kIdxBits = 14;                // argmax key: index field
 constexpr int kStampShift = 46;             // argmax key: 14 index + 32 value bits below the stamp
 constexpr unsigned kMaxStamp = (1u << 18) - 1;
 constexpr int kFlagStride = 64;             // words between barrier flags (256 B)
+constexpr int kKPad = 8;                    // halves of padding per staged row (bank spread)
 
 // Flags in the per-utterance control word.
 constexpr int kFlagZeroHC = 1;              // LSTM input state is zero (init / EOU reset)
@@ -30,20 +32,31 @@ constexpr int kFlagTokOverflow = 2;
 constexpr int kFlagSegOverflow = 4;
 constexpr int kFlagTraceOverflow = 8;
 
-struct DMat {
-    const void *w;       // int8 / f16 / f32 plane [rows][cols]
-    const float *d;      // q8_0 block scales [rows][cols/32], else null
-    int type;
-    int rows, cols;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// A weight matrix [rows][K] laid out as MFMA A fragments: for row tile t and
+// K block kb (32 columns), lane l holds the 8 consecutive weights of row
+// 16t + l%16 starting at column 32kb + 8(l/16).  q8_0: 8 int8 per lane plus
+// the block scales d[16t + r][kb] at scale[(t*KB + kb)*16 + r]; f16: 8 halves
+// per lane; f32: the same two f16 planes holding hi = f16(w), lo = f16(w - hi).
+struct TMat {
+    const void *a;        // fragment plane
+    const void *a_lo;     // f32 weights: low halves
+    const float *scale;   // q8_0 block scales
+    int type;             // PK_TYPE_Q8_0, PK_TYPE_F16, PK_TYPE_F32
+    int rows, tiles, KB;
 };
 
 struct KParams {
     int kind, H, L, J, V1, Dn, Vo, blank, eou, eob, max_sym, n_dur;
     int durations[PK_MAX_DURATIONS];
     const float *eproj;                      // [V1][4H] W_ih0 . embed[v] + b_ih0 + b_hh0, unit-major
-    DMat w_ih[PK_MAX_LAYERS], w_hh[PK_MAX_LAYERS];   // unit-major gate rows
+    TMat w_ih[PK_MAX_LAYERS], w_hh[PK_MAX_LAYERS];   // unit-major gate rows (w_ih[0] unused)
     const float *b_lstm[PK_MAX_LAYERS];      // b_ih + b_hh (unit-major), layers >= 1
-    DMat w_pred, w_out;
+    TMat w_pred, w_out;
     const float *b_pred, *b_out;
     const unsigned char *special;
     int n_special;
@@ -69,6 +82,13 @@ struct KParams {
     float *cx;           // [2][L][n][H]
     float *ppx;          // [n][J]
     float *rx;           // [L][n][4H]  W_hh . h (no bias), unit-major rows
+    // domains: independent utterance groups, each on dom_size workgroups
+    int n_dom, dom_size, nt;
+    const int *dom_n;            // [n_dom] utterances per domain
+    const int *dom_list;         // [n_dom][kDomCap] batch indices
+    const int *wg_dom;           // [nwg] domain of a workgroup
+    const int *wg_rank;          // [nwg] rank inside its domain
+    const int *dom_wg;           // [n_dom][dom_size] workgroup of each rank
     // sync
     unsigned *flags;             // [nwg * kFlagStride]
     unsigned long long *keys;    // [2][n_utts][2]
@@ -84,12 +104,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, unsigne
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// Agent-coherent (SC1) 16-byte load / store: used for every buffer written by
-// one workgroup and read by another inside a launch.  Plain loads elsewhere
-// keep weights cached in L2 (no cache-wide invalidation anywhere in the loop).
+// Agent-coherent (SC1) loads / stores: used for every buffer written by one
+// workgroup and read by another inside a launch.  Plain loads elsewhere keep
+// weights cached in L2 (nothing in the loop invalidates the L2).
 constexpr int kSC1 = 16;
 __device__ __forceinline__ float4 ld4_coh(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kSC1));
+}
+__device__ __forceinline__ void st4_coh(__amdgpu_buffer_rsrc_t r, unsigned byte_off, float4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), r,
+                                           byte_off, 0, kSC1);
 }
 __device__ __forceinline__ float ld_coh(const float *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -98,94 +122,87 @@ __device__ __forceinline__ void st_coh(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ float4 load_w4(const DMat &m, int r, int k) {
-    if (m.type == PK_TYPE_Q8_0) {
-        const int packed = *reinterpret_cast<const int *>(static_cast<const signed char *>(m.w) + (size_t)r * m.cols + k);
-        const float d = m.d[(size_t)r * (m.cols >> 5) + (k >> 5)];
-        return make_float4(d * (float)(signed char)(packed), d * (float)(signed char)(packed >> 8),
-                           d * (float)(signed char)(packed >> 16), d * (float)(signed char)(packed >> 24));
-    } else if (m.type == PK_TYPE_F16) {
-        const uint2 raw = *reinterpret_cast<const uint2 *>(static_cast<const __half *>(m.w) + (size_t)r * m.cols + k);
-        const float2 fa = __half22float2(*reinterpret_cast<const __half2 *>(&raw.x));
-        const float2 fb = __half22float2(*reinterpret_cast<const __half2 *>(&raw.y));
-        return make_float4(fa.x, fa.y, fb.x, fb.y);
-    }
-    return *reinterpret_cast<const float4 *>(static_cast<const float *>(m.w) + (size_t)r * m.cols + k);
+// ---------------------------------------------------------------- MFMA tiles
+
+// 8 int8 (two dwords) -> 8 exact f16: byte q ^ 0x80 = q + 128 becomes the low
+// mantissa byte of 1024.0 (0x64xx), then 1152 is subtracted.
+__device__ __forceinline__ half8 q8_to_half8(uint2 q) {
+    const unsigned x0 = q.x ^ 0x80808080u, x1 = q.y ^ 0x80808080u;
+    const half2v off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    half2v p0 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u)) - off;
+    half2v p1 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u)) - off;
+    half2v p2 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u)) - off;
+    half2v p3 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)) - off;
+    return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
-__device__ __forceinline__ float load_w1(const DMat &m, int r, int k) {
+// Partial product of one 16-row weight tile with one 16-utterance activation
+// tile over K blocks [kb0, kb1).  Activations are staged in LDS as f16 pairs
+// (hi, lo) with x = hi + lo, row stride kp halves; lane l of the result holds
+// rows 4(l/16)..4(l/16)+3 of utterance column l%16.  q8_0 blocks are
+// multiplied exactly (integers in f16) and scaled by d in f32 per block.
+__device__ __forceinline__ f32x4 tile_dot(const TMat &m, int tile, const _Float16 *xhi, const _Float16 *xlo, int kp,
+                                          int col0, int kb0, int kb1, int lane) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const int xo = (col0 + (lane & 15)) * kp + (lane >> 4) * 8;
+    const size_t frag = (size_t)tile * m.KB;
     if (m.type == PK_TYPE_Q8_0) {
-        const signed char q = static_cast<const signed char *>(m.w)[(size_t)r * m.cols + k];
-        return m.d[(size_t)r * (m.cols >> 5) + (k >> 5)] * (float)q;
-    } else if (m.type == PK_TYPE_F16) {
-        return __half2float(static_cast<const __half *>(m.w)[(size_t)r * m.cols + k]);
-    }
-    return static_cast<const float *>(m.w)[(size_t)r * m.cols + k];
-}
-
-// ---------------------------------------------------------------- wave reductions
-
-// Butterfly reduction of N per-lane partial sums over the 64 lanes of a wave:
-// each exchange halves the values a lane carries.  On return lane l holds the
-// total of value index (l >> (6 - log2 N)).  Partners add the same two
-// operands, so every lane holding an index holds the same bits.
-template <int N, int M>
-struct Bfly {
-    static __device__ __forceinline__ void run(float *v, int lane) {
-        if constexpr (M == 0) {
-            return;
-        } else if constexpr (N > 1) {
-            const bool up = (lane & M) != 0;
-#pragma unroll
-            for (int i = 0; i < N / 2; ++i) {
-                const float send = up ? v[i] : v[i + N / 2];
-                const float keep = up ? v[i + N / 2] : v[i];
-                v[i] = keep + __shfl_xor(send, M, kWave);
+        const uint2 *a = static_cast<const uint2 *>(m.a);
+        const float4 *sc = reinterpret_cast<const float4 *>(m.scale);
+#pragma unroll 4
+        for (int kb = kb0; kb < kb1; ++kb) {
+            const half8 bh = *reinterpret_cast<const half8 *>(xhi + xo + kb * 32);
+            const half8 bl = *reinterpret_cast<const half8 *>(xlo + xo + kb * 32);
+            const half8 w = q8_to_half8(a[(frag + kb) * kWave + lane]);
+            const float4 d = sc[(frag + kb) * 4 + (lane >> 4)];
+            f32x4 p = {0.f, 0.f, 0.f, 0.f};
+            p = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bh, p, 0, 0, 0);
+            p = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bl, p, 0, 0, 0);
+            acc[0] = fmaf(d.x, p[0], acc[0]);
+            acc[1] = fmaf(d.y, p[1], acc[1]);
+            acc[2] = fmaf(d.z, p[2], acc[2]);
+            acc[3] = fmaf(d.w, p[3], acc[3]);
+        }
+    } else {
+        const half8 *a = static_cast<const half8 *>(m.a);
+        const half8 *al = static_cast<const half8 *>(m.a_lo);
+        const bool two = m.type == PK_TYPE_F32;
+#pragma unroll 4
+        for (int kb = kb0; kb < kb1; ++kb) {
+            const half8 bh = *reinterpret_cast<const half8 *>(xhi + xo + kb * 32);
+            const half8 bl = *reinterpret_cast<const half8 *>(xlo + xo + kb * 32);
+            const half8 w = a[(frag + kb) * kWave + lane];
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bl, acc, 0, 0, 0);
+            if (two) {
+                const half8 wl = al[(frag + kb) * kWave + lane];
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wl, bh, acc, 0, 0, 0);
             }
-            Bfly<N / 2, M / 2>::run(v, lane);
-        } else {
-            v[0] = v[0] + __shfl_xor(v[0], M, kWave);
-            Bfly<1, M / 2>::run(v, lane);
         }
     }
+    return acc;
+}
+
+__device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+// Staged activation block: NT*16 utterance rows of K values as f16 (hi, lo).
+struct Act {
+    _Float16 *hi, *lo;
+    int kp;     // row stride in halves (K + kKPad)
 };
 
-template <int N>
-constexpr int ilog2() { return N <= 1 ? 0 : 1 + ilog2<N / 2>(); }
-
-template <int N>
-__device__ __forceinline__ float wave_reduce_n(float (&v)[N], int lane) {
-    Bfly<N, 32>::run(v, lane);
-    return v[0];
+__device__ __forceinline__ void put4(const Act &x, int row, int k, float4 v) {
+    _Float16 h0, h1, h2, h3, l0, l1, l2, l3;
+    split_f16(v.x, h0, l0);
+    split_f16(v.y, h1, l1);
+    split_f16(v.z, h2, l2);
+    split_f16(v.w, h3, l3);
+    *reinterpret_cast<half4 *>(x.hi + row * x.kp + k) = half4{h0, h1, h2, h3};
+    *reinterpret_cast<half4 *>(x.lo + row * x.kp + k) = half4{l0, l1, l2, l3};
 }
-
-// acc[r*UC+u] += W[r0+r, :] . xs[u*xstride + :] for R rows (nrows valid), nu <= UC utterances.
-template <int R, int UC>
-__device__ __forceinline__ void dot_rows(const DMat &m, int r0, int nrows, const float *xs, int xstride, int nu,
-                                         float *acc, int lane) {
-    for (int k = lane * 4; k < m.cols; k += 4 * kWave) {
-        float4 w[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) w[r] = (r < nrows) ? load_w4(m, r0 + r, k) : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int u = 0; u < UC; ++u) {
-            if (u < nu) {
-                const float4 x = *reinterpret_cast<const float4 *>(xs + u * xstride + k);
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    float a = acc[r * UC + u];
-                    a = fmaf(w[r].x, x.x, a);
-                    a = fmaf(w[r].y, x.y, a);
-                    a = fmaf(w[r].z, x.z, a);
-                    a = fmaf(w[r].w, x.w, a);
-                    acc[r * UC + u] = a;
-                }
-            }
-        }
-    }
-}
-
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // ---------------------------------------------------------------- argmax keys
 
@@ -204,66 +221,35 @@ __device__ __forceinline__ int key_index(unsigned long long key) {
 }
 __device__ __forceinline__ unsigned key_stamp(unsigned long long key) { return (unsigned)(key >> kStampShift); }
 
-// ---------------------------------------------------------------- grid barrier
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Every workgroup publishes its epoch in its own flag word and every workgroup
-// polls all flags (thread t polls flag t).  No cache-wide fences: data that
-// crosses workgroups is stored and loaded agent-coherently (SC1), and each
-// thread waits for its own stores (s_waitcnt 0) before arriving.  Returns
-// false if the error word is set or the wait exceeds ~2 s of wall clock.
-__device__ __forceinline__ bool grid_sync(const KParams &p, unsigned &epoch) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    __shared__ int s_ok;
-    ++epoch;
-    if (threadIdx.x == 0) {
-        s_ok = 1;
-        __hip_atomic_store(p.flags + (size_t)blockIdx.x * kFlagStride, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (threadIdx.x < gridDim.x) {
-        unsigned *f = p.flags + (size_t)threadIdx.x * kFlagStride;
-        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-        while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < epoch) {
-            __builtin_amdgcn_s_sleep(1);
-            if (__hip_atomic_load(p.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) { s_ok = 0; break; }
-            if (__builtin_amdgcn_s_memrealtime() - t0 > 200000000ull) {   // 100 MHz clock: 2 s
-                __hip_atomic_store(p.status, PK_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                s_ok = 0;
-                break;
-            }
-        }
-    }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __syncthreads();
-    return s_ok != 0;
-}
-
-__device__ __forceinline__ int split_begin(int i, int total, int parts) {
-    return (int)(((long long)i * total) / parts);
+__device__ __forceinline__ void cell(float gi, float gf, float gg, float go, float c_prev, float &c_new, float &h_new) {
+    c_new = sigmoidf_(gf) * c_prev + sigmoidf_(gi) * tanhf(gg);
+    h_new = sigmoidf_(go) * tanhf(c_new);
 }
 
 // ---------------------------------------------------------------- prepare-time kernels
 
-// out[v][r] = bias0[r] + bias1[r] + W[r, :] . E[v, :]: the layer-0 input
-// projection of every vocabulary row (W_ih0 . embed[v] + b_ih0 + b_hh0).
-__global__ void __launch_bounds__(256) embed_proj_kernel(DMat w, DMat e, const float *__restrict b0,
+// out[v][r] = bias0[r] + bias1[r] + W[r, :] . E[v, :] in f32: the layer-0
+// input projection of every vocabulary row (W_ih0 . embed[v] + b_ih0 + b_hh0).
+// Operands are dense f32 here (dequantised on the host from the stored bytes).
+__global__ void __launch_bounds__(256) embed_proj_kernel(const float *__restrict w, const float *__restrict e,
+                                                         int rows, int V, int K, const float *__restrict b0,
                                                          const float *__restrict b1, float *__restrict out) {
     const int v0 = blockIdx.x * 16, r0 = blockIdx.y * 64;
-    const int K = w.cols;
     __shared__ float es[16][65];
     __shared__ float ws[64][65];
     const int tid = threadIdx.x;
-    const int tv = tid / 16, tr = tid % 16;       // 16 vocab rows x 16 thread columns (4 outputs each)
+    const int tv = tid / 16, tr = tid % 16;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     for (int k0 = 0; k0 < K; k0 += 64) {
         for (int i = tid; i < 16 * 64; i += 256) {
             const int vv = i / 64, k = i % 64;
-            es[vv][k] = (v0 + vv < e.rows && k0 + k < K) ? load_w1(e, v0 + vv, k0 + k) : 0.0f;
+            es[vv][k] = (v0 + vv < V && k0 + k < K) ? e[(size_t)(v0 + vv) * K + k0 + k] : 0.0f;
         }
         for (int i = tid; i < 64 * 64; i += 256) {
             const int rr = i / 64, k = i % 64;
-            ws[rr][k] = (r0 + rr < w.rows && k0 + k < K) ? load_w1(w, r0 + rr, k0 + k) : 0.0f;
+            ws[rr][k] = (r0 + rr < rows && k0 + k < K) ? w[(size_t)(r0 + rr) * K + k0 + k] : 0.0f;
         }
         __syncthreads();
         for (int k = 0; k < 64; ++k) {
@@ -274,18 +260,19 @@ __global__ void __launch_bounds__(256) embed_proj_kernel(DMat w, DMat e, const f
         __syncthreads();
     }
     const int v = v0 + tv;
-    if (v >= e.rows) return;
+    if (v >= V) return;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int r = r0 + tr * 4 + j;
-        if (r < w.rows) out[(size_t)v * w.rows + r] = acc[j] + (b0[r] + b1[r]);
+        if (r < rows) out[(size_t)v * rows + r] = acc[j] + (b0[r] + b1[r]);
     }
 }
 
 // ---------------------------------------------------------------- enc_proj
 
 // encp[rows of utterance u] = b_e + W_e . enc[row]  (f32), 64x64 tiles, K step 32.
-__global__ void __launch_bounds__(256) enc_proj_kernel(DMat w, const float *__restrict bias,
+// W is dense f32 [J][D] (dequantised at load from the stored bytes).
+__global__ void __launch_bounds__(256) enc_proj_kernel(const float *__restrict w, int J, const float *__restrict bias,
                                                        const float *__restrict enc, int d_enc,
                                                        const long long *__restrict src_row,
                                                        const long long *__restrict dst_row,
@@ -295,7 +282,6 @@ __global__ void __launch_bounds__(256) enc_proj_kernel(DMat w, const float *__re
     const int m0 = blockIdx.x * 64;
     if (m0 >= Tu) return;
     const int n0 = blockIdx.z * 64;
-    const int J = w.rows;
     __shared__ float xs[32][65];
     __shared__ float ws[32][65];
     const int tid = threadIdx.x;
@@ -307,7 +293,7 @@ __global__ void __launch_bounds__(256) enc_proj_kernel(DMat w, const float *__re
             const int r = i / 32, k = i % 32;
             const int m = m0 + r, n = n0 + r;
             xs[k][r] = (m < Tu && k0 + k < d_enc) ? src[(size_t)m * d_enc + k0 + k] : 0.0f;
-            ws[k][r] = (n < J && k0 + k < d_enc) ? load_w1(w, n, k0 + k) : 0.0f;
+            ws[k][r] = (n < J && k0 + k < d_enc) ? w[(size_t)n * d_enc + k0 + k] : 0.0f;
         }
         __syncthreads();
 #pragma unroll 8
@@ -337,45 +323,65 @@ __global__ void __launch_bounds__(256) enc_proj_kernel(DMat w, const float *__re
 
 // ---------------------------------------------------------------- decode loop
 
-struct Ctl {                      // per-workgroup copy of the control state
-    int t[kMaxBatch], T[kMaxBatch], sym[kMaxBatch], pend[kMaxBatch], flags[kMaxBatch];
-    int ntok[kMaxBatch], steps[kMaxBatch], nseg[kMaxBatch], segst[kMaxBatch], last[kMaxBatch];
-    int cur[kMaxBatch];
-    int lst[kMaxBatch], jst[kMaxBatch];
-    int cnt_l[kMaxBatch / kWave], cnt_j[kMaxBatch / kWave];
-    int nl, nj;
-    unsigned long long wgkey[kUC][2];
+struct Ctl {                      // per-workgroup copy of its domain's control state
+    int b[kDomCap];               // batch index of each domain utterance
+    int t[kDomCap], T[kDomCap], sym[kDomCap], pend[kDomCap], flags[kDomCap];
+    int ntok[kDomCap], steps[kDomCap], nseg[kDomCap], segst[kDomCap], last[kDomCap], cur[kDomCap];
+    int lst[kDomCap], jst[kDomCap];
+    int n, nl, nj;
+    int dom, rank, P;
+    unsigned long long wgkey[kDomCap][2];
 };
 
-__device__ void build_lists(Ctl &s, int n) {
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int nblk = (n + kWave - 1) / kWave;
-    for (int b = wave; b < nblk; b += kWaves) {
-        const int u = b * kWave + lane;
-        const bool fl = u < n && s.pend[u] >= 0;
-        const bool fj = u < n && s.t[u] < s.T[u];
-        const unsigned long long bl = __ballot(fl), bj = __ballot(fj);
-        if (lane == 0) { s.cnt_l[b] = __popcll(bl); s.cnt_j[b] = __popcll(bj); }
-    }
-    __syncthreads();
-    for (int b = wave; b < nblk; b += kWaves) {
-        int base_l = 0, base_j = 0;
-        for (int i = 0; i < b; ++i) { base_l += s.cnt_l[i]; base_j += s.cnt_j[i]; }
-        const int u = b * kWave + lane;
-        const bool fl = u < n && s.pend[u] >= 0;
-        const bool fj = u < n && s.t[u] < s.T[u];
+// Compact the LSTM list (pending token) and the joint list (frames left).
+__device__ void build_lists(Ctl &s) {
+    if (threadIdx.x < kWave) {
+        const int lane = threadIdx.x;
+        const bool fl = lane < s.n && s.pend[lane] >= 0;
+        const bool fj = lane < s.n && s.t[lane] < s.T[lane];
         const unsigned long long bl = __ballot(fl), bj = __ballot(fj);
         const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-        if (fl) s.lst[base_l + __popcll(bl & below)] = u;
-        if (fj) s.jst[base_j + __popcll(bj & below)] = u;
-    }
-    if (threadIdx.x == 0) {
-        int nl = 0, nj = 0;
-        for (int i = 0; i < nblk; ++i) { nl += s.cnt_l[i]; nj += s.cnt_j[i]; }
-        s.nl = nl;
-        s.nj = nj;
+        if (fl) s.lst[__popcll(bl & below)] = lane;
+        if (fj) s.jst[__popcll(bj & below)] = lane;
+        if (lane == 0) {
+            s.nl = __popcll(bl);
+            s.nj = __popcll(bj);
+        }
     }
     __syncthreads();
+}
+
+// Domain barrier: every member publishes its epoch in its own flag word and
+// every member polls all members' flags (thread t polls rank t).  No
+// cache-wide fences: cross-workgroup data is stored and loaded coherently
+// (SC1), and each thread waits for its own stores (s_waitcnt 0) before
+// arriving.  Returns false if the error word is set or the wait exceeds ~2 s.
+__device__ __forceinline__ bool dom_sync(const KParams &p, const Ctl &s, unsigned &epoch) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ int s_ok;
+    ++epoch;
+    if (threadIdx.x == 0) {
+        s_ok = 1;
+        __hip_atomic_store(p.flags + (size_t)blockIdx.x * kFlagStride, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (threadIdx.x < s.P) {
+        unsigned *f = p.flags + (size_t)p.dom_wg[s.dom * s.P + threadIdx.x] * kFlagStride;
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < epoch) {
+            __builtin_amdgcn_s_sleep(1);
+            if (__hip_atomic_load(p.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) { s_ok = 0; break; }
+            if (__builtin_amdgcn_s_memrealtime() - t0 > 200000000ull) {   // 100 MHz clock: 2 s
+                __hip_atomic_store(p.status, PK_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                s_ok = 0;
+                break;
+            }
+        }
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    return s_ok != 0;
 }
 
 // Exchange-buffer offsets (floats).
@@ -386,78 +392,165 @@ __device__ __forceinline__ size_t rx_off(const KParams &p, int layer, int b) {
     return ((size_t)layer * p.n_utts + b) * 4 * p.H;
 }
 
-struct Bufs {                       // buffer resources of the exchange buffers
+struct Bufs {
     __amdgpu_buffer_rsrc_t hx, cx, ppx, rx;
 };
 
-// Stage nu utterances' vectors of length len (multiple of 4) from an exchange
-// buffer into LDS: dst[u*dstride + k] = src[off(u) + k], coherent loads.
+// Stage vectors of length K for n <= 16 utterances into an activation block:
+// row u <- src(off(u)) via coherent loads; rows n .. 15 are zero.
 template <class OffFn>
-__device__ __forceinline__ void stage_coh(float *dst, int dstride, int nu, int len, __amdgpu_buffer_rsrc_t r,
-                                          OffFn off) {
-    const int per = len / 4;
-    for (int i = threadIdx.x; i < nu * per; i += kBlock) {
+__device__ __forceinline__ void stage_act(const Act &x, int K, int n, __amdgpu_buffer_rsrc_t r, OffFn off) {
+    const int per = K / 4;
+    for (int i = threadIdx.x; i < kTile * per; i += kBlock) {
         const int u = i / per, k = (i - u * per) * 4;
-        *reinterpret_cast<float4 *>(dst + u * dstride + k) = ld4_coh(r, (unsigned)((off(u) + k) * 4));
+        const float4 v = u < n ? ld4_coh(r, (unsigned)((off(u) + k) * 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
+        put4(x, u, k, v);
     }
 }
 
-__device__ __forceinline__ void cell(float gi, float gf, float gg, float go, float c_prev, float &c_new, float &h_new) {
-    c_new = sigmoidf_(gf) * c_prev + sigmoidf_(gi) * tanhf(gg);
-    h_new = sigmoidf_(go) * tanhf(c_new);
+// Work split of a set of (tile, utterance-tile) items over the 8 waves:
+// with few items, K is split S ways and the partials are summed in LDS in a
+// fixed order (deterministic).  fn(item, kb0, kb1) returns the partial;
+// epi(item, acc) consumes the total.
+template <class DotFn, class EpiFn>
+__device__ __forceinline__ void run_items(int n_items, int KB, f32x4 *red, DotFn dot, EpiFn epi) {
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    if (n_items <= 0) return;
+    int S = kWaves / n_items;
+    if (S < 1) S = 1;
+    if (S > KB) S = KB;
+    if (S == 1) {
+        for (int it = wave; it < n_items; it += kWaves) epi(it, dot(it, 0, KB));
+        return;
+    }
+    const int units = n_items * S;          // <= kWaves
+    if (wave < units) {
+        const int it = wave / S, s = wave % S;
+        const int kb0 = s * KB / S, kb1 = (s + 1) * KB / S;
+        red[wave * kWave + lane] = dot(it, kb0, kb1);
+    }
+    __syncthreads();
+    for (int it = wave; it < n_items; it += kWaves) {
+        f32x4 acc = red[(it * S) * kWave + lane];
+        for (int s = 1; s < S; ++s) acc += red[(it * S + s) * kWave + lane];
+        epi(it, acc);
+    }
+    __syncthreads();
 }
 
-// LSTM layers >= 1 for this workgroup's units: gates = W_ih . x (staged) +
-// R (rx, computed in the joint phase) + b_ih + b_hh, cell update, coherent
-// stores of h', c' into the other ping-pong buffer.  xs holds the layer input
-// for nu utterances (stride xstride).
-__device__ void lstm_upper_layer(const KParams &p, Ctl &s, const Bufs &B, const float *xs, int xstride, int layer,
-                                 int c0, int nu, int wg, int nwg) {
-    const int H = p.H, lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int j0 = split_begin(wg, H, nwg), j1 = split_begin(wg + 1, H, nwg);
-    for (int j = j0 + wave; j < j1; j += kWaves) {
-        float acc[4 * kUC];
-#pragma unroll
-        for (int i = 0; i < 4 * kUC; ++i) acc[i] = 0.0f;
-        dot_rows<4, kUC>(p.w_ih[layer], 4 * j, 4, xs, xstride, nu, acc, lane);
-        wave_reduce_n<4 * kUC>(acc, lane);
-        constexpr int kShift = 6 - ilog2<4 * kUC>();
-        float g[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) g[q] = __shfl(acc[0], ((q * kUC + (lane % kUC)) << kShift), kWave);
-        if (lane < nu) {
-            const int b = s.lst[c0 + lane];
-            const bool zero = s.flags[b] & kFlagZeroHC;
-            const int cur = s.cur[b];
-            const float *bl = p.b_lstm[layer];
-            float gate[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float r = zero ? 0.0f : ld_coh(p.rx + rx_off(p, layer, b) + 4 * j + q);
-                gate[q] = (g[q] + r) + bl[4 * j + q];
+// Tiles of a matrix with `tiles` row tiles owned by rank r of P: t = r, r+P, ...
+__device__ __forceinline__ int owned(int tiles, int r, int P) { return tiles > r ? (tiles - r + P - 1) / P : 0; }
+
+struct Lds {
+    Act act[1 + PK_MAX_LAYERS];   // staged activation blocks
+    f32x4 *red;                   // [kWaves][kWave] K-split partials
+    float *h0s;                   // [kSmallB][H] layer-0 output in redundant mode
+};
+
+// Joint + argmax for this workgroup's output tiles, plus the recurrent
+// products R_l = W_hh_l . h_l of its LSTM unit tiles (for the next step).
+// Utterances are processed 16 at a time (one MFMA column tile).
+__device__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned stamp) {
+    const int J = p.J, H = p.H, L = p.L, lane = threadIdx.x & (kWave - 1);
+    unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * 2;
+    if (threadIdx.x < 2 * kDomCap) s.wgkey[threadIdx.x / 2][threadIdx.x % 2] = 0ull;
+    const int n_out = owned(p.w_out.tiles, s.rank, s.P);
+    const int n_hh = owned(p.w_hh[0].tiles, s.rank, s.P);
+    const int KBo = p.w_out.KB;
+    for (int c0 = 0; c0 < s.nj; c0 += kTile) {
+        const int nc = min(kTile, s.nj - c0);
+        // stage hidden = relu(encp[t] + pp) and h_l for this column tile
+        {
+            const Act &x = S.act[0];
+            const int per = J / 4;
+            for (int i = threadIdx.x; i < kTile * per; i += kBlock) {
+                const int u = i / per, k = (i - u * per) * 4;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (u < nc) {
+                    const int ul = s.jst[c0 + u], b = s.b[ul];
+                    const float4 e = *reinterpret_cast<const float4 *>(p.encp + (size_t)(p.encp_row[b] + s.t[ul]) * J + k);
+                    const float4 q = ld4_coh(B.ppx, (unsigned)(((size_t)b * J + k) * 4));
+                    v = make_float4(e.x + q.x, e.y + q.y, e.z + q.z, e.w + q.w);
+                    v.x = (0.0f < v.x) ? v.x : 0.0f;
+                    v.y = (0.0f < v.y) ? v.y : 0.0f;
+                    v.z = (0.0f < v.z) ? v.z : 0.0f;
+                    v.w = (0.0f < v.w) ? v.w : 0.0f;
+                }
+                put4(x, u, k, v);
             }
-            const float c_prev = zero ? 0.0f : ld_coh(p.cx + hx_off(p, cur, layer, b) + j);
-            float c_new, h_new;
-            cell(gate[0], gate[1], gate[2], gate[3], c_prev, c_new, h_new);
-            st_coh(p.cx + hx_off(p, cur ^ 1, layer, b) + j, c_new);
-            st_coh(p.hx + hx_off(p, cur ^ 1, layer, b) + j, h_new);
         }
+        for (int l = 0; l < L; ++l)
+            stage_act(S.act[1 + l], H, nc, B.hx, [&](int u) {
+                const int ul = s.jst[c0 + u];
+                return hx_off(p, s.cur[ul], l, s.b[ul]);
+            });
+        __syncthreads();
+        run_items(n_out + L * n_hh, KBo, S.red,
+                  [&](int k, int kb0, int kb1) {
+                      if (k < n_out)
+                          return tile_dot(p.w_out, s.rank + k * s.P, S.act[0].hi, S.act[0].lo, S.act[0].kp, 0, kb0,
+                                          kb1, lane);
+                      const int l = (k - n_out) / n_hh, tile = s.rank + ((k - n_out) % n_hh) * s.P;
+                      const Act &x = S.act[1 + l];
+                      const int kbh = p.w_hh[l].KB;
+                      return tile_dot(p.w_hh[l], tile, x.hi, x.lo, x.kp, 0, kb0 * kbh / KBo, kb1 * kbh / KBo, lane);
+                  },
+                  [&](int k, f32x4 acc) {
+                      const int u = lane & 15;
+                      if (u >= nc) return;
+                      const int ul = s.jst[c0 + u], b = s.b[ul];
+                      if (k < n_out) {
+                          const int tile = s.rank + k * s.P;
+                          unsigned long long best[2] = {0ull, 0ull};
+#pragma unroll
+                          for (int i = 0; i < 4; ++i) {
+                              const int row = tile * kTile + (lane >> 4) * 4 + i;
+                              if (row >= p.Vo) continue;
+                              float v = acc[i] + p.b_out[row];
+                              if (row == p.blank && p.blank_bias) v += p.blank_bias[b];
+                              const int head = row < p.V1 ? 0 : 1;
+                              const unsigned long long key = make_key(v, head ? row - p.V1 : row);
+                              best[head] = key > best[head] ? key : best[head];
+                          }
+                          if (best[0]) atomicMax(&s.wgkey[c0 + u][0], best[0]);
+                          if (best[1]) atomicMax(&s.wgkey[c0 + u][1], best[1]);
+                      } else {
+                          const int l = (k - n_out) / n_hh, tile = s.rank + ((k - n_out) % n_hh) * s.P;
+                          const int row0 = tile * kTile + (lane >> 4) * 4;    // unit-major: gates of one unit
+                          if (row0 < 4 * H)
+                              st4_coh(B.rx, (unsigned)((rx_off(p, l, b) + row0) * 4),
+                                      make_float4(acc[0], acc[1], acc[2], acc[3]));
+                      }
+                  });
+        __syncthreads();
+    }
+    if (threadIdx.x < 2 * s.nj) {
+        const int u = threadIdx.x / 2, head = threadIdx.x % 2;
+        const unsigned long long k = s.wgkey[u][head];
+        if (k != 0ull)
+            __hip_atomic_fetch_max(&keys[(size_t)s.b[s.jst[u]] * 2 + head],
+                                   ((unsigned long long)stamp << kStampShift) | k, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-// Layer 0 from the precomputed input projection: gates = E'[token] + R0.
-// redundant == true: every workgroup computes every unit (into h0s, LDS,
-// stride H) and the unit owners store h', c'; otherwise only own units.
-__device__ void lstm_layer0(const KParams &p, Ctl &s, float *h0s, int c0, int nu, bool redundant, int wg, int nwg) {
+// Layer 0 from the precomputed input projection: gates = E'[token] + R0,
+// elementwise per unit.  redundant: every unit for every listed utterance,
+// h' kept in LDS (h0s) as well; otherwise only this workgroup's unit tiles.
+// Owners store h', c' coherently.
+__device__ void lstm_layer0(const KParams &p, Ctl &s, const Lds &S, bool redundant) {
     const int H = p.H;
-    const int j0 = split_begin(wg, H, nwg), j1 = split_begin(wg + 1, H, nwg);
-    const int ja = redundant ? 0 : j0, jn = redundant ? H : j1 - j0;
-    for (int i = threadIdx.x; i < nu * jn; i += kBlock) {
-        const int uu = i / jn, j = ja + (i - uu * jn);
-        const int b = s.lst[c0 + uu];
-        const bool zero = s.flags[b] & kFlagZeroHC;
-        const int cur = s.cur[b];
-        const float4 e = *reinterpret_cast<const float4 *>(p.eproj + (size_t)s.pend[b] * 4 * H + 4 * j);
+    const int groups = p.w_hh[0].tiles;                 // unit groups of 4
+    const int n_own = owned(groups, s.rank, s.P);
+    const int nunits = redundant ? H : 4 * n_own;
+    for (int i = threadIdx.x; i < s.nl * nunits; i += kBlock) {
+        const int u = i / nunits, jj = i - u * nunits;
+        const int j = redundant ? jj : 4 * (s.rank + (jj / 4) * s.P) + (jj & 3);
+        if (j >= H) continue;
+        const int ul = s.lst[u], b = s.b[ul];
+        const bool zero = s.flags[ul] & kFlagZeroHC;
+        const int cur = s.cur[ul];
+        const float4 e = *reinterpret_cast<const float4 *>(p.eproj + (size_t)s.pend[ul] * 4 * H + 4 * j);
         float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
         float c_prev = 0.0f;
         if (!zero) {
@@ -467,154 +560,183 @@ __device__ void lstm_layer0(const KParams &p, Ctl &s, float *h0s, int c0, int nu
         }
         float c_new, h_new;
         cell(e.x + r.x, e.y + r.y, e.z + r.z, e.w + r.w, c_prev, c_new, h_new);
-        if (redundant) h0s[uu * H + j] = h_new;
-        if (j >= j0 && j < j1) {
+        if (redundant) S.h0s[u * H + j] = h_new;
+        const bool mine = ((j >> 2) % s.P) == s.rank;
+        if (mine) {
             st_coh(p.cx + hx_off(p, cur ^ 1, 0, b) + j, c_new);
             st_coh(p.hx + hx_off(p, cur ^ 1, 0, b) + j, h_new);
         }
     }
 }
 
-// pp = b_p + W_p . h[L-1]' for this workgroup's rows; hs holds h[L-1]' (stride H).
-__device__ void pred_rows(const KParams &p, Ctl &s, const float *hs, int c0, int nu, int wg, int nwg) {
-    const int H = p.H, J = p.J, lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int r0 = split_begin(wg, J, nwg), r1 = split_begin(wg + 1, J, nwg);
-    constexpr int R = 2;
-    for (int r = r0 + wave * R; r < r1; r += kWaves * R) {
-        float acc[R * kUC];
+// Layer l >= 1 for this workgroup's unit tiles: gates = W_ih_l . x + R_l +
+// b_ih + b_hh; the four rows a lane holds are the four gates of one unit, so
+// the cell update happens in the epilogue.
+__device__ void lstm_upper(const KParams &p, Ctl &s, const Lds &S, const Act &x, int layer, int c0, int nc) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const TMat &w = p.w_ih[layer];
+    const int n_own = owned(w.tiles, s.rank, s.P);
+    run_items(n_own, w.KB, S.red,
+              [&](int it, int kb0, int kb1) {
+                  return tile_dot(w, s.rank + it * s.P, x.hi, x.lo, x.kp, 0, kb0, kb1, lane);
+              },
+              [&](int it, f32x4 acc) {
+                  const int tile = s.rank + it * s.P;
+                  const int u = lane & 15;
+                  if (u >= nc) return;
+                  const int j = tile * 4 + (lane >> 4);
+                  if (j >= p.H) return;
+                  const int ul = s.lst[c0 + u], b = s.b[ul];
+                  const bool zero = s.flags[ul] & kFlagZeroHC;
+                  const int cur = s.cur[ul];
+                  const float *bl = p.b_lstm[layer];
+                  float g[4];
 #pragma unroll
-        for (int i = 0; i < R * kUC; ++i) acc[i] = 0.0f;
-        dot_rows<R, kUC>(p.w_pred, r, min(R, r1 - r), hs, H, nu, acc, lane);
-        wave_reduce_n<R * kUC>(acc, lane);
-        constexpr int kShift = 6 - ilog2<R * kUC>();
-        const int idx = lane >> kShift;
-        const int rr = idx / kUC, uu = idx % kUC;
-        if ((lane & ((1 << kShift) - 1)) == 0 && uu < nu && r + rr < r1) {
-            const int b = s.lst[c0 + uu];
-            st_coh(p.ppx + (size_t)b * J + r + rr, p.b_pred[r + rr] + acc[0]);
-        }
-    }
+                  for (int q = 0; q < 4; ++q) {
+                      const float r = zero ? 0.0f : ld_coh(p.rx + rx_off(p, layer, b) + 4 * j + q);
+                      g[q] = (acc[q] + r) + bl[4 * j + q];
+                  }
+                  const float c_prev = zero ? 0.0f : ld_coh(p.cx + hx_off(p, cur, layer, b) + j);
+                  float c_new, h_new;
+                  cell(g[0], g[1], g[2], g[3], c_prev, c_new, h_new);
+                  st_coh(p.cx + hx_off(p, cur ^ 1, layer, b) + j, c_new);
+                  st_coh(p.hx + hx_off(p, cur ^ 1, layer, b) + j, h_new);
+              });
 }
 
-// Joint + argmax for this workgroup's output rows, plus the recurrent products
-// R_l = W_hh_l . h_l of its LSTM units for the next step (off the critical path).
-__device__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, float *stage, unsigned stamp, int wg, int nwg) {
-    const int J = p.J, H = p.H, L = p.L, lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int r0 = split_begin(wg, p.Vo, nwg), r1 = split_begin(wg + 1, p.Vo, nwg);
-    const int j0 = split_begin(wg, H, nwg), j1 = split_begin(wg + 1, H, nwg);
-    const int xstride = J + L * H;
-    constexpr int R = 2;
-    unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * 2;
-    for (int c0 = 0; c0 < s.nj; c0 += kUC) {
-        const int nu = min(kUC, s.nj - c0);
-        // stage: hidden = relu(encp[t] + pp) and h_l for every layer
-        const int per = J / 4;
-        for (int i = threadIdx.x; i < nu * per; i += kBlock) {
-            const int uu = i / per, k = (i - uu * per) * 4;
-            const int b = s.jst[c0 + uu];
-            const float4 e = *reinterpret_cast<const float4 *>(p.encp + (size_t)(p.encp_row[b] + s.t[b]) * J + k);
-            const float4 q = ld4_coh(B.ppx, (unsigned)(((size_t)b * J + k) * 4));
-            float4 v = make_float4(e.x + q.x, e.y + q.y, e.z + q.z, e.w + q.w);
-            v.x = (0.0f < v.x) ? v.x : 0.0f;
-            v.y = (0.0f < v.y) ? v.y : 0.0f;
-            v.z = (0.0f < v.z) ? v.z : 0.0f;
-            v.w = (0.0f < v.w) ? v.w : 0.0f;
-            *reinterpret_cast<float4 *>(stage + uu * xstride + k) = v;
-        }
-        for (int l = 0; l < L; ++l)
-            stage_coh(stage + J + l * H, xstride, nu, H, B.hx,
-                      [&](int uu) { const int b = s.jst[c0 + uu]; return hx_off(p, s.cur[b], l, b); });
-        if (threadIdx.x < 2 * kUC) s.wgkey[threadIdx.x / 2][threadIdx.x % 2] = 0ull;
-        __syncthreads();
-        for (int r = r0 + wave * R; r < r1; r += kWaves * R) {
-            float acc[R * kUC];
+// pp = b_p + W_p . h[L-1]' for this workgroup's tiles.
+__device__ void pred_tiles(const KParams &p, Ctl &s, const Lds &S, const Act &x, int c0, int nc) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const TMat &w = p.w_pred;
+    const int n_own = owned(w.tiles, s.rank, s.P);
+    run_items(n_own, w.KB, S.red,
+              [&](int it, int kb0, int kb1) {
+                  return tile_dot(w, s.rank + it * s.P, x.hi, x.lo, x.kp, 0, kb0, kb1, lane);
+              },
+              [&](int it, f32x4 acc) {
+                  const int tile = s.rank + it * s.P;
+                  const int u = lane & 15;
+                  if (u >= nc) return;
+                  const int b = s.b[s.lst[c0 + u]];
 #pragma unroll
-            for (int i = 0; i < R * kUC; ++i) acc[i] = 0.0f;
-            dot_rows<R, kUC>(p.w_out, r, min(R, r1 - r), stage, xstride, nu, acc, lane);
-            wave_reduce_n<R * kUC>(acc, lane);
-            constexpr int kShift = 6 - ilog2<R * kUC>();
-            const int idx = lane >> kShift;
-            const int rr = idx / kUC, uu = idx % kUC;
-            const int row = r + rr;
-            if ((lane & ((1 << kShift) - 1)) == 0 && uu < nu && row < r1) {
-                float v = acc[0] + p.b_out[row];
-                const int b = s.jst[c0 + uu];
-                if (row == p.blank && p.blank_bias) v += p.blank_bias[b];
-                const int head = row < p.V1 ? 0 : 1;
-                atomicMax(&s.wgkey[uu][head], make_key(v, head ? row - p.V1 : row));
+                  for (int i = 0; i < 4; ++i) {
+                      const int row = tile * kTile + (lane >> 4) * 4 + i;
+                      if (row < p.J) st_coh(p.ppx + (size_t)b * p.J + row, p.b_pred[row] + acc[i]);
+                  }
+              });
+}
+
+// One LSTM step (all layers) and the pred projection for every utterance of
+// the LSTM list.  A small list in a whole-device domain runs layer 0
+// redundantly in every workgroup (no barrier between layers 0 and 1);
+// otherwise every layer is split by unit tiles with a barrier after each.
+__device__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned &epoch) {
+    const int H = p.H, L = p.L;
+    const bool redundant = s.nl <= kSmallB && p.n_dom == 1;
+    const Act &x = S.act[1];
+    lstm_layer0(p, s, S, redundant);
+    // layer l >= 1 and the pred projection read the previous layer's full output
+    auto stage_layer = [&](int layer, int c0, int nc) {
+        stage_act(x, H, nc, B.hx, [&](int u) { const int ul = s.lst[c0 + u]; return hx_off(p, s.cur[ul] ^ 1, layer, s.b[ul]); });
+    };
+    if (redundant) {
+        __syncthreads();
+        for (int i = threadIdx.x; i < kTile * (H / 4); i += kBlock) {
+            const int u = i / (H / 4), k = (i - u * (H / 4)) * 4;
+            put4(x, u, k, u < s.nl ? *reinterpret_cast<const float4 *>(S.h0s + u * H + k) : make_float4(0.f, 0.f, 0.f, 0.f));
+        }
+        __syncthreads();
+        if (L > 1) lstm_upper(p, s, S, x, 1, 0, s.nl);
+    } else {
+        if (!dom_sync(p, s, epoch)) return false;
+        if (L > 1) {
+            for (int c0 = 0; c0 < s.nl; c0 += kTile) {
+                const int nc = min(kTile, s.nl - c0);
+                stage_layer(0, c0, nc);
+                __syncthreads();
+                lstm_upper(p, s, S, x, 1, c0, nc);
+                __syncthreads();
             }
         }
-        // recurrent products for the next LSTM step of these utterances
-        for (int job = wave; job < L * (j1 - j0); job += kWaves) {
-            const int l = job / (j1 - j0), j = j0 + job % (j1 - j0);
-            float acc[4 * kUC];
-#pragma unroll
-            for (int i = 0; i < 4 * kUC; ++i) acc[i] = 0.0f;
-            dot_rows<4, kUC>(p.w_hh[l], 4 * j, 4, stage + J + l * H, xstride, nu, acc, lane);
-            wave_reduce_n<4 * kUC>(acc, lane);
-            constexpr int kShift = 6 - ilog2<4 * kUC>();
-            const int idx = lane >> kShift;
-            const int q = idx / kUC, uu = idx % kUC;
-            if ((lane & ((1 << kShift) - 1)) == 0 && uu < nu)
-                st_coh(p.rx + rx_off(p, l, s.jst[c0 + uu]) + 4 * j + q, acc[0]);
+    }
+    for (int l = 2; l < L; ++l) {
+        if (!dom_sync(p, s, epoch)) return false;
+        for (int c0 = 0; c0 < s.nl; c0 += kTile) {
+            const int nc = min(kTile, s.nl - c0);
+            stage_layer(l - 1, c0, nc);
+            __syncthreads();
+            lstm_upper(p, s, S, x, l, c0, nc);
+            __syncthreads();
         }
-        __syncthreads();
-        if (threadIdx.x < 2 * nu) {
-            const int uu = threadIdx.x / 2, head = threadIdx.x % 2;
-            const unsigned long long k = s.wgkey[uu][head];
-            if (k != 0ull)
-                __hip_atomic_fetch_max(&keys[(size_t)s.jst[c0 + uu] * 2 + head],
-                                       ((unsigned long long)stamp << kStampShift) | k, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (L > 1) {
+        if (!dom_sync(p, s, epoch)) return false;
+    }
+    if (L > 1 || !redundant) {
+        for (int c0 = 0; c0 < s.nl; c0 += kTile) {
+            const int nc = min(kTile, s.nl - c0);
+            stage_layer(L - 1, c0, nc);
+            __syncthreads();
+            pred_tiles(p, s, S, x, c0, nc);
+            __syncthreads();
         }
+    } else {
+        pred_tiles(p, s, S, x, 0, s.nl);     // h0' already staged from LDS
         __syncthreads();
     }
+    for (int i = threadIdx.x; i < s.nl; i += kBlock) {   // the new state becomes current
+        const int ul = s.lst[i];
+        s.cur[ul] ^= 1;
+        s.pend[ul] = -1;
+        s.flags[ul] &= ~kFlagZeroHC;
+    }
+    return dom_sync(p, s, epoch);
 }
 
 // Apply the argmax results of iteration `stamp` to every utterance of the joint
 // list: src/parakeet_tdt.cpp:936-967 (TDT) and src/parakeet_eou.cpp:275-332 (EOU).
-__device__ void decide(const KParams &p, Ctl &s, unsigned stamp, int wg, int nwg) {
+__device__ void decide(const KParams &p, Ctl &s, unsigned stamp) {
     const unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * 2;
     for (int i = threadIdx.x; i < s.nj; i += kBlock) {
-        const int b = s.jst[i];
+        const int ul = s.jst[i], b = s.b[ul];
         const unsigned long long kt = __hip_atomic_load(&keys[(size_t)b * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const unsigned long long kd =
             __hip_atomic_load(&keys[(size_t)b * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (key_stamp(kt) != stamp || (p.Dn > 0 && key_stamp(kd) != stamp)) {
             __hip_atomic_store(p.status, PK_ERR_DEVICE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            s.t[b] = s.T[b];
+            s.t[ul] = s.T[ul];
             continue;
         }
         const int tok = key_index(kt);
         const int di = p.Dn > 0 ? key_index(kd) : -1;
-        const bool writer = (b % nwg) == wg;
-        const int step = s.steps[b]++;
+        const bool writer = (ul % s.P) == s.rank;
+        const int step = s.steps[ul]++;
         if (writer && p.trace) {
             if (step < p.trace_cap) {
                 p.trace[((size_t)b * p.trace_cap + step) * 2] = tok;
                 p.trace[((size_t)b * p.trace_cap + step) * 2 + 1] = di;
             } else {
-                s.flags[b] |= kFlagTraceOverflow;
+                s.flags[ul] |= kFlagTraceOverflow;
             }
         }
         if (p.kind == PK_KIND_TDT) {
             const int dur = p.n_dur > 0 ? p.durations[di] : di;
             const int adv = dur > 1 ? dur : 1;
             if (tok == p.blank) {
-                s.t[b] += adv;
-                s.sym[b] = 0;
+                s.t[ul] += adv;
+                s.sym[ul] = 0;
                 continue;
             }
-            const int n = s.ntok[b]++;
+            const int n = s.ntok[ul]++;
             if (writer) {
                 if (n < p.token_cap) p.tokens[(size_t)b * p.token_cap + n] = tok;
-                else s.flags[b] |= kFlagTokOverflow;
+                else s.flags[ul] |= kFlagTokOverflow;
             }
-            s.pend[b] = tok;
-            s.sym[b] += 1;
-            if (dur > 0 || s.sym[b] >= p.max_sym) {
-                s.t[b] += adv;
-                s.sym[b] = 0;
+            s.pend[ul] = tok;
+            s.sym[ul] += 1;
+            if (dur > 0 || s.sym[ul] >= p.max_sym) {
+                s.t[ul] += adv;
+                s.sym[ul] = 0;
             }
         } else {
             const int max_syms = p.max_sym > 1 ? p.max_sym : 1;
@@ -622,140 +744,101 @@ __device__ void decide(const KParams &p, Ctl &s, unsigned stamp, int wg, int nwg
             if (tok == p.blank || tok == p.eob) {
                 frame_done = true;
             } else if (tok == p.eou) {
-                const int total = (p.tokens_base ? p.tokens_base[b] : 0) + s.ntok[b];
-                if (total > s.segst[b]) {
-                    const int ns = s.nseg[b]++;
+                const int total = (p.tokens_base ? p.tokens_base[b] : 0) + s.ntok[ul];
+                if (total > s.segst[ul]) {
+                    const int ns = s.nseg[ul]++;
                     if (writer) {
                         if (p.segs && ns < p.seg_cap) p.segs[(size_t)b * p.seg_cap + ns] = total;
-                        else s.flags[b] |= kFlagSegOverflow;
+                        else s.flags[ul] |= kFlagSegOverflow;
                     }
-                    s.segst[b] = total;
+                    s.segst[ul] = total;
                 }
-                s.flags[b] |= kFlagZeroHC;
-                s.pend[b] = p.blank;
-                s.last[b] = p.blank;
+                s.flags[ul] |= kFlagZeroHC;
+                s.pend[ul] = p.blank;
+                s.last[ul] = p.blank;
                 frame_done = true;
             } else if (tok >= 0 && tok < p.n_special && p.special[tok]) {
                 frame_done = true;
             } else {
-                const int n = s.ntok[b]++;
+                const int n = s.ntok[ul]++;
                 if (writer) {
                     if (n < p.token_cap) p.tokens[(size_t)b * p.token_cap + n] = tok;
-                    else s.flags[b] |= kFlagTokOverflow;
+                    else s.flags[ul] |= kFlagTokOverflow;
                 }
-                s.pend[b] = tok;
-                s.last[b] = tok;
-                s.sym[b] += 1;
-                if (s.sym[b] >= max_syms) frame_done = true;
+                s.pend[ul] = tok;
+                s.last[ul] = tok;
+                s.sym[ul] += 1;
+                if (s.sym[ul] >= max_syms) frame_done = true;
             }
             if (frame_done) {          // the next frame starts with sym = 0 (src/parakeet_eou.cpp:269)
-                s.t[b] += 1;
-                if (s.t[b] < s.T[b]) s.sym[b] = 0;
+                s.t[ul] += 1;
+                if (s.t[ul] < s.T[ul]) s.sym[ul] = 0;
             }
         }
     }
-}
-
-// One LSTM step (all layers) and the pred projection for every utterance of
-// the LSTM list.  Small lists run layer 0 redundantly in every workgroup
-// (no barrier between layer 0 and layer 1); larger lists split every layer
-// by units with a barrier after each.
-__device__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bufs &B, float *stage, unsigned &epoch, int wg,
-                              int nwg) {
-    const int H = p.H, L = p.L;
-    const bool small = s.nl <= kSmallB;
-    if (small) {
-        // stage layout: [h_0' (nu x H)] [h_1' ...]: layer l's output is layer l+1's input
-        const int nu = s.nl;
-        lstm_layer0(p, s, stage, 0, nu, true, wg, nwg);
-        __syncthreads();
-        for (int l = 1; l < L; ++l) {
-            if (l > 1) {     // deeper layers need the full h_{l-1}' from every owner
-                if (!grid_sync(p, epoch)) return false;
-                stage_coh(stage, H, nu, H, B.hx,
-                          [&](int uu) { const int b = s.lst[uu]; return hx_off(p, s.cur[b] ^ 1, l - 1, b); });
-                __syncthreads();
-            }
-            lstm_upper_layer(p, s, B, stage, H, l, 0, nu, wg, nwg);
-        }
-        if (L > 1) {
-            if (!grid_sync(p, epoch)) return false;
-            stage_coh(stage, H, nu, H, B.hx,
-                      [&](int uu) { const int b = s.lst[uu]; return hx_off(p, s.cur[b] ^ 1, L - 1, b); });
-        }
-        __syncthreads();
-        pred_rows(p, s, stage, 0, nu, wg, nwg);
-    } else {
-        for (int c0 = 0; c0 < s.nl; c0 += kUC * 4) {
-            const int nu = min(kUC * 4, s.nl - c0);
-            lstm_layer0(p, s, nullptr, c0, nu, false, wg, nwg);
-        }
-        if (!grid_sync(p, epoch)) return false;
-        for (int l = 1; l < L; ++l) {
-            for (int c0 = 0; c0 < s.nl; c0 += kUC) {
-                const int nu = min(kUC, s.nl - c0);
-                stage_coh(stage, H, nu, H, B.hx,
-                          [&](int uu) { const int b = s.lst[c0 + uu]; return hx_off(p, s.cur[b] ^ 1, l - 1, b); });
-                __syncthreads();
-                lstm_upper_layer(p, s, B, stage, H, l, c0, nu, wg, nwg);
-                __syncthreads();
-            }
-            if (!grid_sync(p, epoch)) return false;
-        }
-        for (int c0 = 0; c0 < s.nl; c0 += kUC) {
-            const int nu = min(kUC, s.nl - c0);
-            stage_coh(stage, H, nu, H, B.hx,
-                      [&](int uu) { const int b = s.lst[c0 + uu]; return hx_off(p, s.cur[b] ^ 1, L - 1, b); });
-            __syncthreads();
-            pred_rows(p, s, stage, c0, nu, wg, nwg);
-            __syncthreads();
-        }
-    }
-    // the new state becomes current
-    __syncthreads();
-    for (int i = threadIdx.x; i < s.nl; i += kBlock) {
-        const int b = s.lst[i];
-        s.cur[b] ^= 1;
-        s.pend[b] = -1;
-        s.flags[b] &= ~kFlagZeroHC;
-    }
-    return grid_sync(p, epoch);
 }
 
 __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
-    extern __shared__ float stage[];
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
     __shared__ Ctl s;
-    const int wg = blockIdx.x, nwg = gridDim.x;
-    const int n = p.n_utts, H = p.H, L = p.L, J = p.J;
+    const int wg = blockIdx.x;
+    const int H = p.H, L = p.L, J = p.J, n_all = p.n_utts;
     unsigned epoch = 0;
     Bufs B;
-    B.hx = rsrc(p.hx, (unsigned)((size_t)2 * L * n * H * 4));
-    B.cx = rsrc(p.cx, (unsigned)((size_t)2 * L * n * H * 4));
-    B.ppx = rsrc(p.ppx, (unsigned)((size_t)n * J * 4));
-    B.rx = rsrc(p.rx, (unsigned)((size_t)L * n * 4 * H * 4));
+    B.hx = rsrc(p.hx, (unsigned)((size_t)2 * L * n_all * H * 4));
+    B.cx = rsrc(p.cx, (unsigned)((size_t)2 * L * n_all * H * 4));
+    B.ppx = rsrc(p.ppx, (unsigned)((size_t)n_all * J * 4));
+    B.rx = rsrc(p.rx, (unsigned)((size_t)L * n_all * 4 * H * 4));
 
-    for (int b = threadIdx.x; b < n; b += kBlock) {
+    // LDS: activation blocks [hidden | h_0 .. h_{L-1}], then K-split partials
+    Lds S;
+    {
+        unsigned char *q = lds_raw;
+        for (int a = 0; a <= L; ++a) {
+            const int K = a == 0 ? J : H;
+            const int kp = K + kKPad;
+            S.act[a].hi = reinterpret_cast<_Float16 *>(q);
+            S.act[a].lo = S.act[a].hi + kTile * kp;
+            S.act[a].kp = kp;
+            q += (size_t)kTile * kp * 2 * 2;
+        }
+        S.red = reinterpret_cast<f32x4 *>(q);
+        q += (size_t)kWaves * kWave * sizeof(f32x4);
+        S.h0s = reinterpret_cast<float *>(q);
+    }
+
+    if (threadIdx.x == 0) {
+        s.dom = p.wg_dom[wg];
+        s.rank = p.wg_rank[wg];
+        s.P = p.dom_size;
+        s.n = p.dom_n[s.dom];
+    }
+    __syncthreads();
+    for (int ul = threadIdx.x; ul < s.n; ul += kBlock) {
+        const int b = p.dom_list[s.dom * kDomCap + ul];
         const int slot = p.slot[b];
         const int *ctrl = p.slot_ctrl + (size_t)slot * PK_CTRL_N;
         const bool init = ctrl[PK_CTRL_INIT] != 0;
-        s.T[b] = p.T[b];
-        s.ntok[b] = 0;
-        s.steps[b] = 0;
-        s.nseg[b] = 0;
-        s.cur[b] = 0;
-        s.sym[b] = init ? ctrl[PK_CTRL_SYM] : 0;
-        if (p.kind == PK_KIND_EOU && s.T[b] > 0) s.sym[b] = 0;   // reset per frame (src/parakeet_eou.cpp:269)
-        s.last[b] = init ? ctrl[PK_CTRL_LAST] : -1;
-        s.segst[b] = init ? ctrl[PK_CTRL_SEGSTART] : 0;
+        s.b[ul] = b;
+        s.T[ul] = p.T[b];
+        s.ntok[ul] = 0;
+        s.steps[ul] = 0;
+        s.nseg[ul] = 0;
+        s.cur[ul] = 0;
+        s.sym[ul] = init ? ctrl[PK_CTRL_SYM] : 0;
+        if (p.kind == PK_KIND_EOU && s.T[ul] > 0) s.sym[ul] = 0;   // reset per frame (src/parakeet_eou.cpp:269)
+        s.last[ul] = init ? ctrl[PK_CTRL_LAST] : -1;
+        s.segst[ul] = init ? ctrl[PK_CTRL_SEGSTART] : 0;
         const int carry = init ? ctrl[PK_CTRL_CARRY] : 0;
-        s.pend[b] = init ? -1 : p.blank;
-        s.flags[b] = init ? 0 : kFlagZeroHC;
-        if (p.kind == PK_KIND_TDT) s.t[b] = carry > 0 ? min(carry, s.T[b]) : 0;
-        else s.t[b] = 0;
+        s.pend[ul] = init ? -1 : p.blank;
+        s.flags[ul] = init ? 0 : kFlagZeroHC;
+        if (p.kind == PK_KIND_TDT) s.t[ul] = carry > 0 ? min(carry, s.T[ul]) : 0;
+        else s.t[ul] = 0;
     }
+    __syncthreads();
     // copy the slot state of this workgroup's utterances into the exchange buffers
-    for (int b = wg; b < n; b += nwg) {
-        const int slot = p.slot[b];
+    for (int ul = s.rank; ul < s.n; ul += s.P) {
+        const int b = s.b[ul], slot = p.slot[b];
         for (int i = threadIdx.x; i < L * H; i += kBlock) {
             const int l = i / H, k = i - l * H;
             st_coh(p.hx + hx_off(p, 0, l, b) + k, p.slot_h[(size_t)slot * L * H + i]);
@@ -763,38 +846,37 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         }
         for (int i = threadIdx.x; i < J; i += kBlock) st_coh(p.ppx + (size_t)b * J + i, p.slot_pp[(size_t)slot * J + i]);
     }
-    __syncthreads();
-    build_lists(s, n);
-    bool ok = grid_sync(p, epoch);
+    build_lists(s);
+    bool ok = dom_sync(p, s, epoch);
 
     unsigned iter = 0;
     while (ok) {
         if (s.nl == 0 && s.nj == 0) break;
         if ((int)iter >= p.max_iter) {
-            if (wg == 0 && threadIdx.x == 0)
+            if (threadIdx.x == 0)
                 __hip_atomic_store(p.status, PK_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             ok = false;
             break;
         }
         ++iter;
         if (s.nl > 0) {
-            ok = lstm_and_pred(p, s, B, stage, epoch, wg, nwg);
+            ok = lstm_and_pred(p, s, B, S, epoch);
             if (!ok) break;
         }
         if (s.nj > 0) {
-            joint_phase(p, s, B, stage, iter, wg, nwg);
-            ok = grid_sync(p, epoch);
+            joint_phase(p, s, B, S, iter);
+            ok = dom_sync(p, s, epoch);
             if (!ok) break;
-            decide(p, s, iter, wg, nwg);
+            decide(p, s, iter);
         }
         __syncthreads();
-        build_lists(s, n);
+        build_lists(s);
     }
     if (!ok) return;
 
-    for (int b = wg; b < n; b += nwg) {
-        const int slot = p.slot[b];
-        const int cur = s.cur[b];
+    for (int ul = s.rank; ul < s.n; ul += s.P) {
+        const int b = s.b[ul], slot = p.slot[b];
+        const int cur = s.cur[ul];
         for (int i = threadIdx.x; i < L * H; i += kBlock) {
             const int l = i / H, k = i - l * H;
             p.slot_h[(size_t)slot * L * H + i] = ld_coh(p.hx + hx_off(p, cur, l, b) + k);
@@ -804,21 +886,21 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         if (threadIdx.x == 0) {
             int *ctrl = p.slot_ctrl + (size_t)slot * PK_CTRL_N;
             ctrl[PK_CTRL_INIT] = 1;
-            ctrl[PK_CTRL_SYM] = s.sym[b];
-            ctrl[PK_CTRL_CARRY] = (p.kind == PK_KIND_TDT) ? max(0, s.t[b] - s.T[b]) : 0;
-            ctrl[PK_CTRL_LAST] = s.last[b];
-            ctrl[PK_CTRL_SEGSTART] = s.segst[b];
+            ctrl[PK_CTRL_SYM] = s.sym[ul];
+            ctrl[PK_CTRL_CARRY] = (p.kind == PK_KIND_TDT) ? max(0, s.t[ul] - s.T[ul]) : 0;
+            ctrl[PK_CTRL_LAST] = s.last[ul];
+            ctrl[PK_CTRL_SEGSTART] = s.segst[ul];
             ctrl[PK_CTRL_CUR] = 0;
-            p.n_tokens[b] = s.ntok[b];
-            p.steps[b] = s.steps[b];
-            if (p.n_segs) p.n_segs[b] = s.nseg[b];
-            if (s.flags[b] & (kFlagTokOverflow | kFlagSegOverflow))
+            p.n_tokens[b] = s.ntok[ul];
+            p.steps[b] = s.steps[ul];
+            if (p.n_segs) p.n_segs[b] = s.nseg[ul];
+            if (s.flags[ul] & (kFlagTokOverflow | kFlagSegOverflow))
                 __hip_atomic_store(p.status + 2, PK_ERR_OVERFLOW, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (s.flags[b] & kFlagTraceOverflow)
+            if (s.flags[ul] & kFlagTraceOverflow)
                 __hip_atomic_store(p.status + 3, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    if (wg == 0 && threadIdx.x == 0) p.status[1] = (int)iter;
+    if (threadIdx.x == 0) atomicMax(p.status + 1, (int)iter);
 }
 
 }  // namespace pkdev
