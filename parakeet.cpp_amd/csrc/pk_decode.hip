@@ -243,10 +243,10 @@ struct pk_decoder {
     hipEvent_t ev[3] = {};
     DevBuf arena;              // weights
     DevBuf eproj;              // [V1][4H] layer-0 input projection of every token
-    DevBuf slots_h, slots_c, slots_pp, slots_ctrl;
+    DevBuf slots_h, slots_c, slots_pp, slots_r, slots_ctrl;
     DevBuf special;
     // per-call scratch
-    DevBuf d_desc, d_encp, d_keys, d_sync, d_enc, d_out, d_xchg, d_flags;
+    DevBuf d_desc, d_encp, d_keys, d_sync, d_enc, d_out, d_xchg, d_flags, d_prof;
     std::vector<uint8_t> h_desc;
     int last_iters = 0;
 };
@@ -471,21 +471,26 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     if ((rc = dec->slots_h.ensure((size_t)n_slots * L * H * 4))) return cleanup(rc);
     if ((rc = dec->slots_c.ensure((size_t)n_slots * L * H * 4))) return cleanup(rc);
     if ((rc = dec->slots_pp.ensure((size_t)n_slots * J * 4))) return cleanup(rc);
+    if ((rc = dec->slots_r.ensure((size_t)n_slots * L * 4 * H * 4))) return cleanup(rc);
     if ((rc = dec->slots_ctrl.ensure((size_t)n_slots * PK_CTRL_N * 4))) return cleanup(rc);
     if (hipMemset(dec->slots_h.p, 0, dec->slots_h.n) != hipSuccess ||
         hipMemset(dec->slots_c.p, 0, dec->slots_c.n) != hipSuccess ||
         hipMemset(dec->slots_pp.p, 0, dec->slots_pp.n) != hipSuccess ||
+        hipMemset(dec->slots_r.p, 0, dec->slots_r.n) != hipSuccess ||
         hipMemset(dec->slots_ctrl.p, 0, dec->slots_ctrl.n) != hipSuccess)
         return cleanup(fail(PK_ERR_DEVICE, "slot memset"));
     kp.slot_h = dec->slots_h.as<float>();
     kp.slot_c = dec->slots_c.as<float>();
     kp.slot_pp = dec->slots_pp.as<float>();
+    kp.slot_r = dec->slots_r.as<float>();
     kp.slot_ctrl = dec->slots_ctrl.as<int>();
 
     // decode-loop launch shape: one workgroup per CU; LDS = activation blocks
     // [hidden | h_0 .. h_{L-1}] of one 16-utterance tile + K-split partials +
     // the redundant layer-0 output
-    const size_t act = (size_t)kTile * ((J + kKPad) + (size_t)L * (H + kKPad)) * 2 * 2;
+    const size_t act = (size_t)kTile * ((J + kKPad) + (size_t)(H + kKPad)) * 2 * 2;
+    if (std::max(J, H) > 4 * pkdev::kStageMax * kBlock / kTile)
+        return cleanup(fail(PK_ERR_UNSUPPORTED, "hidden sizes above %d", 4 * pkdev::kStageMax * kBlock / kTile));
     const size_t need = act + (size_t)kWaves * kWave * 16 + (size_t)kSmallB * H * 4;
     if (need + sizeof(pkdev::Ctl) + 256 > (size_t)dec->lds_block)
         return cleanup(fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed, %d available", need + sizeof(pkdev::Ctl),
@@ -730,7 +735,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     if ((rc = dec->d_keys.ensure(keys_bytes))) return rc;
     if ((rc = dec->d_sync.ensure(64))) return rc;
     if ((rc = dec->d_flags.ensure((size_t)nwg * kFlagStride * 4))) return rc;
-    const size_t xh = 2 * (size_t)L * m * H, xp = (size_t)m * J, xr = (size_t)L * m * 4 * H;
+    const size_t xh = 2 * (size_t)L * m * H, xp = (size_t)m * J, xr = 2 * (size_t)L * m * 4 * H;
     if ((rc = dec->d_xchg.ensure((2 * xh + xp + xr) * 4))) return rc;
     p.hx = dec->d_xchg.as<float>();
     p.cx = p.hx + xh;
@@ -742,6 +747,14 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     HIP_TRY(hipMemsetAsync(dec->d_keys.p, 0, keys_bytes, dec->stream));
     HIP_TRY(hipMemsetAsync(dec->d_sync.p, 0, 64, dec->stream));
     HIP_TRY(hipMemsetAsync(dec->d_flags.p, 0, (size_t)nwg * kFlagStride * 4, dec->stream));
+    // PK_PROFILE_PHASES=1: workgroup 0 accumulates per-phase wall-clock time (stderr summary)
+    const bool prof = getenv("PK_PROFILE_PHASES") != nullptr;
+    p.prof = nullptr;
+    if (prof) {
+        if ((rc = dec->d_prof.ensure(pkdev::kPrN * 8))) return rc;
+        HIP_TRY(hipMemsetAsync(dec->d_prof.p, 0, pkdev::kPrN * 8, dec->stream));
+        p.prof = dec->d_prof.as<unsigned long long>();
+    }
     void *args[] = {&p};
     HIP_TRY(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(pkdev::decode_loop_kernel), dim3(nwg),
                                        dim3(kBlock), args, dec->lds_bytes, dec->stream));
@@ -780,6 +793,19 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         HIP_TRY(hipStreamSynchronize(dec->stream));
     }
     dec->last_iters = status[1];
+    if (prof) {
+        unsigned long long t[pkdev::kPrN];
+        HIP_TRY(hipMemcpy(t, dec->d_prof.p, sizeof t, hipMemcpyDeviceToHost));
+        static const char *names[pkdev::kPrN] = {"L0", "sync0", "L1", "sync1", "pred", "sync2",
+                                                 "J-stage", "J-compute", "J-sync", "decide", "stageLSTM"};
+        double total = 0;
+        for (double v : t) total += v;
+        fprintf(stderr, "[pk phases] %d iterations, %d domains x %d wg, total %.3f ms:", status[1], pl.n_dom, pl.P,
+                total * 1e-5);
+        for (int i = 0; i < pkdev::kPrN; ++i)
+            fprintf(stderr, " %s=%.2fus", names[i], status[1] ? t[i] * 1e-2 / status[1] : 0.0);
+        fprintf(stderr, "\n");
+    }
     if (status[0]) return fail(status[0], "device decode failed (status %d)", status[0]);
     if (status[2]) return fail(PK_ERR_OVERFLOW, "token or segment capacity exceeded");
     return 0;

@@ -64,6 +64,7 @@ struct KParams {
     float *slot_h;       // [slots][L][H]
     float *slot_c;       // [slots][L][H]
     float *slot_pp;      // [slots][J]  b_p + W_p . h[L-1]
+    float *slot_r;       // [slots][L][4H]  W_hh . h (no bias), unit-major rows
     int *slot_ctrl;      // [slots][PK_CTRL_N]
     // batch
     int n_utts;
@@ -81,7 +82,7 @@ struct KParams {
     float *hx;           // [2][L][n][H] ping-pong by utterance parity
     float *cx;           // [2][L][n][H]
     float *ppx;          // [n][J]
-    float *rx;           // [L][n][4H]  W_hh . h (no bias), unit-major rows
+    float *rx;           // [2][L][n][4H]  W_hh . h (no bias), unit-major rows, ping-pong like hx
     // domains: independent utterance groups, each on dom_size workgroups
     int n_dom, dom_size, nt;
     const int *dom_n;            // [n_dom] utterances per domain
@@ -94,7 +95,21 @@ struct KParams {
     unsigned long long *keys;    // [2][n_utts][2]
     int *status;                 // [0] error code, [1] iterations, [2] overflow, [3] trace overflow
     int max_iter;
+    unsigned long long *prof;    // nullable: per-phase wall-clock totals of workgroup 0 (100 MHz ticks)
 };
+
+// Phase timers (workgroup 0 only, when p.prof is set).
+enum { kPrL0 = 0, kPrSync0, kPrL1, kPrSync1, kPrPred, kPrSync2, kPrJStage, kPrJCompute, kPrJSync, kPrDecide,
+       kPrStageL, kPrN };
+__device__ __forceinline__ void pmark(const KParams &p, unsigned long long &last, int k) {
+    if (!p.prof) return;
+    __syncthreads();
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        const unsigned long long now = __builtin_amdgcn_s_memrealtime();
+        p.prof[k] += now - last;
+        last = now;
+    }
+}
 
 // ---------------------------------------------------------------- memory helpers
 
@@ -141,43 +156,82 @@ __device__ __forceinline__ half8 q8_to_half8(uint2 q) {
 // (hi, lo) with x = hi + lo, row stride kp halves; lane l of the result holds
 // rows 4(l/16)..4(l/16)+3 of utterance column l%16.  q8_0 blocks are
 // multiplied exactly (integers in f16) and scaled by d in f32 per block.
+// Weight fragments are fetched kGrp blocks ahead of their use.
+constexpr int kGrp = 4;
 __device__ __forceinline__ f32x4 tile_dot(const TMat &m, int tile, const _Float16 *xhi, const _Float16 *xlo, int kp,
                                           int col0, int kb0, int kb1, int lane) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     const int xo = (col0 + (lane & 15)) * kp + (lane >> 4) * 8;
     const size_t frag = (size_t)tile * m.KB;
     if (m.type == PK_TYPE_Q8_0) {
-        const uint2 *a = static_cast<const uint2 *>(m.a);
-        const float4 *sc = reinterpret_cast<const float4 *>(m.scale);
-#pragma unroll 4
-        for (int kb = kb0; kb < kb1; ++kb) {
-            const half8 bh = *reinterpret_cast<const half8 *>(xhi + xo + kb * 32);
-            const half8 bl = *reinterpret_cast<const half8 *>(xlo + xo + kb * 32);
-            const half8 w = q8_to_half8(a[(frag + kb) * kWave + lane]);
-            const float4 d = sc[(frag + kb) * 4 + (lane >> 4)];
-            f32x4 p = {0.f, 0.f, 0.f, 0.f};
-            p = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bh, p, 0, 0, 0);
-            p = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bl, p, 0, 0, 0);
-            acc[0] = fmaf(d.x, p[0], acc[0]);
-            acc[1] = fmaf(d.y, p[1], acc[1]);
-            acc[2] = fmaf(d.z, p[2], acc[2]);
-            acc[3] = fmaf(d.w, p[3], acc[3]);
+        const uint2 *a = static_cast<const uint2 *>(m.a) + frag * kWave + lane;
+        const float4 *sc = reinterpret_cast<const float4 *>(m.scale) + frag * 4 + (lane >> 4);
+        uint2 qa[kGrp], qb[kGrp];
+        float4 da[kGrp], db[kGrp];
+#pragma unroll
+        for (int i = 0; i < kGrp; ++i) {
+            qa[i] = qb[i] = make_uint2(0u, 0u);
+            da[i] = db[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < kGrp; ++i)
+            if (kb0 + i < kb1) { qa[i] = a[(kb0 + i) * kWave]; da[i] = sc[(kb0 + i) * 4]; }
+        for (int g = kb0; g < kb1; g += kGrp) {
+#pragma unroll
+            for (int i = 0; i < kGrp; ++i)
+                if (g + kGrp + i < kb1) { qb[i] = a[(g + kGrp + i) * kWave]; db[i] = sc[(g + kGrp + i) * 4]; }
+#pragma unroll
+            for (int i = 0; i < kGrp; ++i) {
+                const int kb = g + i;
+                if (kb < kb1) {
+                    const half8 bh = *reinterpret_cast<const half8 *>(xhi + xo + kb * 32);
+                    const half8 bl = *reinterpret_cast<const half8 *>(xlo + xo + kb * 32);
+                    const half8 w = q8_to_half8(qa[i]);
+                    f32x4 p = {0.f, 0.f, 0.f, 0.f};
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bh, p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bl, p, 0, 0, 0);
+                    acc[0] = fmaf(da[i].x, p[0], acc[0]);
+                    acc[1] = fmaf(da[i].y, p[1], acc[1]);
+                    acc[2] = fmaf(da[i].z, p[2], acc[2]);
+                    acc[3] = fmaf(da[i].w, p[3], acc[3]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < kGrp; ++i) { qa[i] = qb[i]; da[i] = db[i]; }
         }
     } else {
-        const half8 *a = static_cast<const half8 *>(m.a);
-        const half8 *al = static_cast<const half8 *>(m.a_lo);
         const bool two = m.type == PK_TYPE_F32;
-#pragma unroll 4
-        for (int kb = kb0; kb < kb1; ++kb) {
-            const half8 bh = *reinterpret_cast<const half8 *>(xhi + xo + kb * 32);
-            const half8 bl = *reinterpret_cast<const half8 *>(xlo + xo + kb * 32);
-            const half8 w = a[(frag + kb) * kWave + lane];
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bh, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bl, acc, 0, 0, 0);
-            if (two) {
-                const half8 wl = al[(frag + kb) * kWave + lane];
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wl, bh, acc, 0, 0, 0);
+        const half8 *a = static_cast<const half8 *>(m.a) + frag * kWave + lane;
+        const half8 *al = two ? static_cast<const half8 *>(m.a_lo) + frag * kWave + lane : a;
+        half8 wa[kGrp], wb[kGrp], la[kGrp], lb[kGrp];
+#pragma unroll
+        for (int i = 0; i < kGrp; ++i) wa[i] = wb[i] = la[i] = lb[i] = half8{};
+#pragma unroll
+        for (int i = 0; i < kGrp; ++i)
+            if (kb0 + i < kb1) {
+                wa[i] = a[(kb0 + i) * kWave];
+                if (two) la[i] = al[(kb0 + i) * kWave];
             }
+        for (int g = kb0; g < kb1; g += kGrp) {
+#pragma unroll
+            for (int i = 0; i < kGrp; ++i)
+                if (g + kGrp + i < kb1) {
+                    wb[i] = a[(g + kGrp + i) * kWave];
+                    if (two) lb[i] = al[(g + kGrp + i) * kWave];
+                }
+#pragma unroll
+            for (int i = 0; i < kGrp; ++i) {
+                const int kb = g + i;
+                if (kb < kb1) {
+                    const half8 bh = *reinterpret_cast<const half8 *>(xhi + xo + kb * 32);
+                    const half8 bl = *reinterpret_cast<const half8 *>(xlo + xo + kb * 32);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[i], bh, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[i], bl, acc, 0, 0, 0);
+                    if (two) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(la[i], bh, acc, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < kGrp; ++i) { wa[i] = wb[i]; la[i] = lb[i]; }
         }
     }
     return acc;
@@ -388,8 +442,8 @@ __device__ __forceinline__ bool dom_sync(const KParams &p, const Ctl &s, unsigne
 __device__ __forceinline__ size_t hx_off(const KParams &p, int buf, int layer, int b) {
     return (((size_t)buf * p.L + layer) * p.n_utts + b) * p.H;
 }
-__device__ __forceinline__ size_t rx_off(const KParams &p, int layer, int b) {
-    return ((size_t)layer * p.n_utts + b) * 4 * p.H;
+__device__ __forceinline__ size_t rx_off(const KParams &p, int buf, int layer, int b) {
+    return (((size_t)buf * p.L + layer) * p.n_utts + b) * 4 * p.H;
 }
 
 struct Bufs {
@@ -397,14 +451,26 @@ struct Bufs {
 };
 
 // Stage vectors of length K for n <= 16 utterances into an activation block:
-// row u <- src(off(u)) via coherent loads; rows n .. 15 are zero.
+// row u <- src(off(u)) via coherent loads; rows n .. 15 are zero.  Every
+// thread issues all of its loads before converting any of them.
+constexpr int kStageMax = 8;    // float4 per thread: 16 rows x K/4 <= kStageMax * kBlock  (K <= 1024)
 template <class OffFn>
 __device__ __forceinline__ void stage_act(const Act &x, int K, int n, __amdgpu_buffer_rsrc_t r, OffFn off) {
     const int per = K / 4;
-    for (int i = threadIdx.x; i < kTile * per; i += kBlock) {
+    float4 v[kStageMax];
+#pragma unroll
+    for (int j = 0; j < kStageMax; ++j) {
+        const int i = threadIdx.x + j * kBlock;
         const int u = i / per, k = (i - u * per) * 4;
-        const float4 v = u < n ? ld4_coh(r, (unsigned)((off(u) + k) * 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
-        put4(x, u, k, v);
+        v[j] = (i < kTile * per && u < n) ? ld4_coh(r, (unsigned)((off(u) + k) * 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int j = 0; j < kStageMax; ++j) {
+        const int i = threadIdx.x + j * kBlock;
+        if (i < kTile * per) {
+            const int u = i / per, k = (i - u * per) * 4;
+            put4(x, u, k, v[j]);
+        }
     }
 }
 
@@ -447,82 +513,73 @@ struct Lds {
     float *h0s;                   // [kSmallB][H] layer-0 output in redundant mode
 };
 
-// Joint + argmax for this workgroup's output tiles, plus the recurrent
-// products R_l = W_hh_l . h_l of its LSTM unit tiles (for the next step).
-// Utterances are processed 16 at a time (one MFMA column tile).
-__device__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned stamp) {
-    const int J = p.J, H = p.H, L = p.L, lane = threadIdx.x & (kWave - 1);
+// Joint + argmax for this workgroup's output tiles.  Utterances are processed
+// 16 at a time (one MFMA column tile).
+__device__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned stamp,
+                            unsigned long long &tlast) {
+    const int J = p.J, lane = threadIdx.x & (kWave - 1);
     unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * 2;
     if (threadIdx.x < 2 * kDomCap) s.wgkey[threadIdx.x / 2][threadIdx.x % 2] = 0ull;
     const int n_out = owned(p.w_out.tiles, s.rank, s.P);
-    const int n_hh = owned(p.w_hh[0].tiles, s.rank, s.P);
-    const int KBo = p.w_out.KB;
+    const Act &x = S.act[0];
     for (int c0 = 0; c0 < s.nj; c0 += kTile) {
         const int nc = min(kTile, s.nj - c0);
-        // stage hidden = relu(encp[t] + pp) and h_l for this column tile
+        // stage hidden = relu(encp[t] + pp) for this column tile
         {
-            const Act &x = S.act[0];
             const int per = J / 4;
-            for (int i = threadIdx.x; i < kTile * per; i += kBlock) {
+            float4 e[kStageMax], q[kStageMax];
+#pragma unroll
+            for (int j = 0; j < kStageMax; ++j) {
+                const int i = threadIdx.x + j * kBlock;
                 const int u = i / per, k = (i - u * per) * 4;
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (u < nc) {
+                e[j] = q[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (i < kTile * per && u < nc) {
                     const int ul = s.jst[c0 + u], b = s.b[ul];
-                    const float4 e = *reinterpret_cast<const float4 *>(p.encp + (size_t)(p.encp_row[b] + s.t[ul]) * J + k);
-                    const float4 q = ld4_coh(B.ppx, (unsigned)(((size_t)b * J + k) * 4));
-                    v = make_float4(e.x + q.x, e.y + q.y, e.z + q.z, e.w + q.w);
+                    e[j] = *reinterpret_cast<const float4 *>(p.encp + (size_t)(p.encp_row[b] + s.t[ul]) * J + k);
+                    q[j] = ld4_coh(B.ppx, (unsigned)(((size_t)b * J + k) * 4));
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < kStageMax; ++j) {
+                const int i = threadIdx.x + j * kBlock;
+                if (i < kTile * per) {
+                    const int u = i / per, k = (i - u * per) * 4;
+                    float4 v = make_float4(e[j].x + q[j].x, e[j].y + q[j].y, e[j].z + q[j].z, e[j].w + q[j].w);
                     v.x = (0.0f < v.x) ? v.x : 0.0f;
                     v.y = (0.0f < v.y) ? v.y : 0.0f;
                     v.z = (0.0f < v.z) ? v.z : 0.0f;
                     v.w = (0.0f < v.w) ? v.w : 0.0f;
+                    put4(x, u, k, v);
                 }
-                put4(x, u, k, v);
             }
         }
-        for (int l = 0; l < L; ++l)
-            stage_act(S.act[1 + l], H, nc, B.hx, [&](int u) {
-                const int ul = s.jst[c0 + u];
-                return hx_off(p, s.cur[ul], l, s.b[ul]);
-            });
         __syncthreads();
-        run_items(n_out + L * n_hh, KBo, S.red,
+        pmark(p, tlast, kPrJStage);
+        run_items(n_out, p.w_out.KB, S.red,
                   [&](int k, int kb0, int kb1) {
-                      if (k < n_out)
-                          return tile_dot(p.w_out, s.rank + k * s.P, S.act[0].hi, S.act[0].lo, S.act[0].kp, 0, kb0,
-                                          kb1, lane);
-                      const int l = (k - n_out) / n_hh, tile = s.rank + ((k - n_out) % n_hh) * s.P;
-                      const Act &x = S.act[1 + l];
-                      const int kbh = p.w_hh[l].KB;
-                      return tile_dot(p.w_hh[l], tile, x.hi, x.lo, x.kp, 0, kb0 * kbh / KBo, kb1 * kbh / KBo, lane);
+                      return tile_dot(p.w_out, s.rank + k * s.P, x.hi, x.lo, x.kp, 0, kb0, kb1, lane);
                   },
                   [&](int k, f32x4 acc) {
                       const int u = lane & 15;
                       if (u >= nc) return;
-                      const int ul = s.jst[c0 + u], b = s.b[ul];
-                      if (k < n_out) {
-                          const int tile = s.rank + k * s.P;
-                          unsigned long long best[2] = {0ull, 0ull};
+                      const int b = s.b[s.jst[c0 + u]];
+                      const int tile = s.rank + k * s.P;
+                      unsigned long long best[2] = {0ull, 0ull};
 #pragma unroll
-                          for (int i = 0; i < 4; ++i) {
-                              const int row = tile * kTile + (lane >> 4) * 4 + i;
-                              if (row >= p.Vo) continue;
-                              float v = acc[i] + p.b_out[row];
-                              if (row == p.blank && p.blank_bias) v += p.blank_bias[b];
-                              const int head = row < p.V1 ? 0 : 1;
-                              const unsigned long long key = make_key(v, head ? row - p.V1 : row);
-                              best[head] = key > best[head] ? key : best[head];
-                          }
-                          if (best[0]) atomicMax(&s.wgkey[c0 + u][0], best[0]);
-                          if (best[1]) atomicMax(&s.wgkey[c0 + u][1], best[1]);
-                      } else {
-                          const int l = (k - n_out) / n_hh, tile = s.rank + ((k - n_out) % n_hh) * s.P;
-                          const int row0 = tile * kTile + (lane >> 4) * 4;    // unit-major: gates of one unit
-                          if (row0 < 4 * H)
-                              st4_coh(B.rx, (unsigned)((rx_off(p, l, b) + row0) * 4),
-                                      make_float4(acc[0], acc[1], acc[2], acc[3]));
+                      for (int i = 0; i < 4; ++i) {
+                          const int row = tile * kTile + (lane >> 4) * 4 + i;
+                          if (row >= p.Vo) continue;
+                          float v = acc[i] + p.b_out[row];
+                          if (row == p.blank && p.blank_bias) v += p.blank_bias[b];
+                          const int head = row < p.V1 ? 0 : 1;
+                          const unsigned long long key = make_key(v, head ? row - p.V1 : row);
+                          best[head] = key > best[head] ? key : best[head];
                       }
+                      if (best[0]) atomicMax(&s.wgkey[c0 + u][0], best[0]);
+                      if (best[1]) atomicMax(&s.wgkey[c0 + u][1], best[1]);
                   });
         __syncthreads();
+        pmark(p, tlast, kPrJCompute);
     }
     if (threadIdx.x < 2 * s.nj) {
         const int u = threadIdx.x / 2, head = threadIdx.x % 2;
@@ -554,7 +611,7 @@ __device__ void lstm_layer0(const KParams &p, Ctl &s, const Lds &S, bool redunda
         float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
         float c_prev = 0.0f;
         if (!zero) {
-            const float *rp = p.rx + rx_off(p, 0, b) + 4 * j;
+            const float *rp = p.rx + rx_off(p, cur, 0, b) + 4 * j;
             r = make_float4(ld_coh(rp), ld_coh(rp + 1), ld_coh(rp + 2), ld_coh(rp + 3));
             c_prev = ld_coh(p.cx + hx_off(p, cur, 0, b) + j);
         }
@@ -569,31 +626,56 @@ __device__ void lstm_layer0(const KParams &p, Ctl &s, const Lds &S, bool redunda
     }
 }
 
-// Layer l >= 1 for this workgroup's unit tiles: gates = W_ih_l . x + R_l +
-// b_ih + b_hh; the four rows a lane holds are the four gates of one unit, so
-// the cell update happens in the epilogue.
-__device__ void lstm_upper(const KParams &p, Ctl &s, const Lds &S, const Act &x, int layer, int c0, int nc) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const TMat &w = p.w_ih[layer];
-    const int n_own = owned(w.tiles, s.rank, s.P);
-    run_items(n_own, w.KB, S.red,
+// Items of the phase that consumes layer lc's new output h_lc' (staged in x):
+//   consumer tiles   W_ih_{lc+1} (LSTM layer lc+1, cell update in the epilogue:
+//                    the four rows a lane holds are the four gates of one unit)
+//                    or W_p (pred projection) when lc is the last layer;
+//   recurrent tiles  W_hh_lc . h_lc' -> R_lc for the utterance's next step
+//                    (stored in the other ping-pong half of rx).
+// Column tile: utterances lst[c0 .. c0+nc).
+__device__ void consume_layer(const KParams &p, Ctl &s, const Lds &S, const Bufs &B, const Act &x, int lc, int c0,
+                              int nc) {
+    const int lane = threadIdx.x & (kWave - 1), H = p.H;
+    const bool last = lc == p.L - 1;
+    const TMat &wc = last ? p.w_pred : p.w_ih[lc + 1];
+    const TMat &wr = p.w_hh[lc];
+    const int n_c = owned(wc.tiles, s.rank, s.P), n_r = owned(wr.tiles, s.rank, s.P);
+    run_items(n_c + n_r, wc.KB, S.red,
               [&](int it, int kb0, int kb1) {
-                  return tile_dot(w, s.rank + it * s.P, x.hi, x.lo, x.kp, 0, kb0, kb1, lane);
+                  if (it < n_c) return tile_dot(wc, s.rank + it * s.P, x.hi, x.lo, x.kp, 0, kb0, kb1, lane);
+                  return tile_dot(wr, s.rank + (it - n_c) * s.P, x.hi, x.lo, x.kp, 0, kb0 * wr.KB / wc.KB,
+                                  kb1 * wr.KB / wc.KB, lane);
               },
               [&](int it, f32x4 acc) {
-                  const int tile = s.rank + it * s.P;
                   const int u = lane & 15;
                   if (u >= nc) return;
-                  const int j = tile * 4 + (lane >> 4);
-                  if (j >= p.H) return;
                   const int ul = s.lst[c0 + u], b = s.b[ul];
-                  const bool zero = s.flags[ul] & kFlagZeroHC;
                   const int cur = s.cur[ul];
+                  if (it >= n_c) {          // recurrent product for the next step
+                      const int row0 = (s.rank + (it - n_c) * s.P) * kTile + (lane >> 4) * 4;
+                      if (row0 < 4 * H)
+                          st4_coh(B.rx, (unsigned)((rx_off(p, cur ^ 1, lc, b) + row0) * 4),
+                                  make_float4(acc[0], acc[1], acc[2], acc[3]));
+                      return;
+                  }
+                  const int tile = s.rank + it * s.P;
+                  if (last) {               // pred projection
+#pragma unroll
+                      for (int i = 0; i < 4; ++i) {
+                          const int row = tile * kTile + (lane >> 4) * 4 + i;
+                          if (row < p.J) st_coh(p.ppx + (size_t)b * p.J + row, p.b_pred[row] + acc[i]);
+                      }
+                      return;
+                  }
+                  const int layer = lc + 1;
+                  const int j = tile * 4 + (lane >> 4);
+                  if (j >= H) return;
+                  const bool zero = s.flags[ul] & kFlagZeroHC;
                   const float *bl = p.b_lstm[layer];
                   float g[4];
 #pragma unroll
                   for (int q = 0; q < 4; ++q) {
-                      const float r = zero ? 0.0f : ld_coh(p.rx + rx_off(p, layer, b) + 4 * j + q);
+                      const float r = zero ? 0.0f : ld_coh(p.rx + rx_off(p, cur, layer, b) + 4 * j + q);
                       g[q] = (acc[q] + r) + bl[4 * j + q];
                   }
                   const float c_prev = zero ? 0.0f : ld_coh(p.cx + hx_off(p, cur, layer, b) + j);
@@ -604,85 +686,42 @@ __device__ void lstm_upper(const KParams &p, Ctl &s, const Lds &S, const Act &x,
               });
 }
 
-// pp = b_p + W_p . h[L-1]' for this workgroup's tiles.
-__device__ void pred_tiles(const KParams &p, Ctl &s, const Lds &S, const Act &x, int c0, int nc) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const TMat &w = p.w_pred;
-    const int n_own = owned(w.tiles, s.rank, s.P);
-    run_items(n_own, w.KB, S.red,
-              [&](int it, int kb0, int kb1) {
-                  return tile_dot(w, s.rank + it * s.P, x.hi, x.lo, x.kp, 0, kb0, kb1, lane);
-              },
-              [&](int it, f32x4 acc) {
-                  const int tile = s.rank + it * s.P;
-                  const int u = lane & 15;
-                  if (u >= nc) return;
-                  const int b = s.b[s.lst[c0 + u]];
-#pragma unroll
-                  for (int i = 0; i < 4; ++i) {
-                      const int row = tile * kTile + (lane >> 4) * 4 + i;
-                      if (row < p.J) st_coh(p.ppx + (size_t)b * p.J + row, p.b_pred[row] + acc[i]);
-                  }
-              });
-}
-
-// One LSTM step (all layers) and the pred projection for every utterance of
-// the LSTM list.  A small list in a whole-device domain runs layer 0
-// redundantly in every workgroup (no barrier between layers 0 and 1);
-// otherwise every layer is split by unit tiles with a barrier after each.
-__device__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned &epoch) {
+// One LSTM step (all layers), the pred projection and the recurrent products
+// for every utterance of the LSTM list.  A small list in a whole-device
+// domain runs layer 0 redundantly in every workgroup (no barrier between
+// layers 0 and 1); otherwise layer 0 is split by unit tiles and followed by a
+// barrier.  Each later phase stages one layer's full new output and runs the
+// tiles that consume it.
+__device__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned &epoch,
+                              unsigned long long &tlast) {
     const int H = p.H, L = p.L;
     const bool redundant = s.nl <= kSmallB && p.n_dom == 1;
     const Act &x = S.act[1];
     lstm_layer0(p, s, S, redundant);
-    // layer l >= 1 and the pred projection read the previous layer's full output
-    auto stage_layer = [&](int layer, int c0, int nc) {
-        stage_act(x, H, nc, B.hx, [&](int u) { const int ul = s.lst[c0 + u]; return hx_off(p, s.cur[ul] ^ 1, layer, s.b[ul]); });
-    };
-    if (redundant) {
-        __syncthreads();
-        for (int i = threadIdx.x; i < kTile * (H / 4); i += kBlock) {
-            const int u = i / (H / 4), k = (i - u * (H / 4)) * 4;
-            put4(x, u, k, u < s.nl ? *reinterpret_cast<const float4 *>(S.h0s + u * H + k) : make_float4(0.f, 0.f, 0.f, 0.f));
-        }
-        __syncthreads();
-        if (L > 1) lstm_upper(p, s, S, x, 1, 0, s.nl);
-    } else {
-        if (!dom_sync(p, s, epoch)) return false;
-        if (L > 1) {
+    pmark(p, tlast, kPrL0);
+    for (int lc = 0; lc < L; ++lc) {
+        if (lc == 0 && redundant) {
+            __syncthreads();
+            for (int i = threadIdx.x; i < kTile * (H / 4); i += kBlock) {
+                const int u = i / (H / 4), k = (i - u * (H / 4)) * 4;
+                put4(x, u, k, u < s.nl ? *reinterpret_cast<const float4 *>(S.h0s + u * H + k) : make_float4(0.f, 0.f, 0.f, 0.f));
+            }
+            __syncthreads();
+            consume_layer(p, s, S, B, x, 0, 0, s.nl);
+            __syncthreads();
+        } else {
+            if (!dom_sync(p, s, epoch)) return false;
+            pmark(p, tlast, lc == 0 ? kPrSync0 : kPrSync1);
             for (int c0 = 0; c0 < s.nl; c0 += kTile) {
                 const int nc = min(kTile, s.nl - c0);
-                stage_layer(0, c0, nc);
+                stage_act(x, H, nc, B.hx, [&](int u) { const int ul = s.lst[c0 + u]; return hx_off(p, s.cur[ul] ^ 1, lc, s.b[ul]); });
                 __syncthreads();
-                lstm_upper(p, s, S, x, 1, c0, nc);
+                pmark(p, tlast, kPrStageL);
+                consume_layer(p, s, S, B, x, lc, c0, nc);
                 __syncthreads();
             }
         }
-    }
-    for (int l = 2; l < L; ++l) {
-        if (!dom_sync(p, s, epoch)) return false;
-        for (int c0 = 0; c0 < s.nl; c0 += kTile) {
-            const int nc = min(kTile, s.nl - c0);
-            stage_layer(l - 1, c0, nc);
-            __syncthreads();
-            lstm_upper(p, s, S, x, l, c0, nc);
-            __syncthreads();
-        }
-    }
-    if (L > 1) {
-        if (!dom_sync(p, s, epoch)) return false;
-    }
-    if (L > 1 || !redundant) {
-        for (int c0 = 0; c0 < s.nl; c0 += kTile) {
-            const int nc = min(kTile, s.nl - c0);
-            stage_layer(L - 1, c0, nc);
-            __syncthreads();
-            pred_tiles(p, s, S, x, c0, nc);
-            __syncthreads();
-        }
-    } else {
-        pred_tiles(p, s, S, x, 0, s.nl);     // h0' already staged from LDS
-        __syncthreads();
+        pmark(p, tlast, lc == L - 1 ? kPrPred : kPrL1);
     }
     for (int i = threadIdx.x; i < s.nl; i += kBlock) {   // the new state becomes current
         const int ul = s.lst[i];
@@ -690,7 +729,9 @@ __device__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bufs &B, const Lds
         s.pend[ul] = -1;
         s.flags[ul] &= ~kFlagZeroHC;
     }
-    return dom_sync(p, s, epoch);
+    const bool ok = dom_sync(p, s, epoch);
+    pmark(p, tlast, kPrSync2);
+    return ok;
 }
 
 // Apply the argmax results of iteration `stamp` to every utterance of the joint
@@ -788,13 +829,13 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
     B.hx = rsrc(p.hx, (unsigned)((size_t)2 * L * n_all * H * 4));
     B.cx = rsrc(p.cx, (unsigned)((size_t)2 * L * n_all * H * 4));
     B.ppx = rsrc(p.ppx, (unsigned)((size_t)n_all * J * 4));
-    B.rx = rsrc(p.rx, (unsigned)((size_t)L * n_all * 4 * H * 4));
+    B.rx = rsrc(p.rx, (unsigned)((size_t)2 * L * n_all * 4 * H * 4));
 
     // LDS: activation blocks [hidden | h_0 .. h_{L-1}], then K-split partials
     Lds S;
     {
         unsigned char *q = lds_raw;
-        for (int a = 0; a <= L; ++a) {
+        for (int a = 0; a <= 1; ++a) {      // [hidden | one layer output]
             const int K = a == 0 ? J : H;
             const int kp = K + kKPad;
             S.act[a].hi = reinterpret_cast<_Float16 *>(q);
@@ -845,11 +886,16 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
             st_coh(p.cx + hx_off(p, 0, l, b) + k, p.slot_c[(size_t)slot * L * H + i]);
         }
         for (int i = threadIdx.x; i < J; i += kBlock) st_coh(p.ppx + (size_t)b * J + i, p.slot_pp[(size_t)slot * J + i]);
+        for (int i = threadIdx.x; i < L * 4 * H; i += kBlock) {
+            const int l = i / (4 * H), k = i - l * 4 * H;
+            st_coh(p.rx + rx_off(p, 0, l, b) + k, p.slot_r[(size_t)slot * L * 4 * H + i]);
+        }
     }
     build_lists(s);
     bool ok = dom_sync(p, s, epoch);
 
     unsigned iter = 0;
+    unsigned long long tlast = __builtin_amdgcn_s_memrealtime();
     while (ok) {
         if (s.nl == 0 && s.nj == 0) break;
         if ((int)iter >= p.max_iter) {
@@ -860,17 +906,19 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         }
         ++iter;
         if (s.nl > 0) {
-            ok = lstm_and_pred(p, s, B, S, epoch);
+            ok = lstm_and_pred(p, s, B, S, epoch, tlast);
             if (!ok) break;
         }
         if (s.nj > 0) {
-            joint_phase(p, s, B, S, iter);
+            joint_phase(p, s, B, S, iter, tlast);
             ok = dom_sync(p, s, epoch);
+            pmark(p, tlast, kPrJSync);
             if (!ok) break;
             decide(p, s, iter);
         }
         __syncthreads();
         build_lists(s);
+        pmark(p, tlast, kPrDecide);
     }
     if (!ok) return;
 
@@ -883,6 +931,10 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
             p.slot_c[(size_t)slot * L * H + i] = ld_coh(p.cx + hx_off(p, cur, l, b) + k);
         }
         for (int i = threadIdx.x; i < J; i += kBlock) p.slot_pp[(size_t)slot * J + i] = ld_coh(p.ppx + (size_t)b * J + i);
+        for (int i = threadIdx.x; i < L * 4 * H; i += kBlock) {
+            const int l = i / (4 * H), k = i - l * 4 * H;
+            p.slot_r[(size_t)slot * L * 4 * H + i] = ld_coh(p.rx + rx_off(p, cur, l, b) + k);
+        }
         if (threadIdx.x == 0) {
             int *ctrl = p.slot_ctrl + (size_t)slot * PK_CTRL_N;
             ctrl[PK_CTRL_INIT] = 1;
