@@ -38,6 +38,11 @@ def parse():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-utts", type=int, default=16)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run a plain device copy of MIB MiB (calibrates hardware byte counters)")
+    ap.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="counter_collection.csv of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
+                         "this bench with --copy-probe 256: fills roofline.traffic")
     return ap.parse_args()
 
 
@@ -114,6 +119,21 @@ def main():
     graft.load_package()
     from parakeet_amd import gguf, hipmem, pk, roofline, synth
 
+    copy_probe = None
+    if args.copy_probe > 0:
+        import ctypes
+        lib = ctypes.CDLL(os.path.join(ROOT, "parakeet.cpp_amd", "libpk_calib.so"))
+        lib.pk_calib_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+        nbytes = args.copy_probe << 20
+        src, dst = hipmem.DeviceArray(nbytes), hipmem.DeviceArray(nbytes)
+        src.zero()
+        rc = lib.pk_calib_copy(dst.ptr, src.ptr, nbytes)
+        if rc != 0:
+            raise RuntimeError(f"pk_calib_copy failed: {rc}")
+        src.free()
+        dst.free()
+        copy_probe = {"kernel": "calib_copy_kernel", "bytes_read": nbytes, "bytes_written": nbytes}
+
     B, T, D, MS = args.batch, args.frames, 1024, 10
     tmp = tempfile.mkdtemp()
     path = os.path.join(tmp, "tdt-0.6b-v3-q8_0.gguf")
@@ -176,6 +196,15 @@ def main():
                      "achieved_tflops": round(enc_flops / (enc_ms * 1e-3) / 1e12, 3) if enc_ms > 0 else None,
                      "algorithmic_bytes": enc_bytes, "algorithmic_flops": enc_flops},
     }
+
+    if copy_probe:
+        out["copy_probe"] = copy_probe
+    if args.traffic:
+        tr = roofline.pmc_traffic(*args.traffic)
+        out["roofline"]["traffic"] = round(tr["bytes_per_launch"], 0)
+        out["roofline"]["traffic_detail"] = {
+            k: {"kib_per_dispatch": round(v["kib_per_dispatch"], 1), "copy_factor": round(v["factor"], 4)}
+            for k, v in tr.items() if k != "bytes_per_launch"}
 
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))

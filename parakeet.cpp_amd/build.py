@@ -2,6 +2,8 @@
 
   libparakeet_hip.so      HIP kernels + C ABI      (csrc/pk_decode.hip)
   libparakeet_decoder.so  C++ decoder API           (csrc/parakeet_decoder.cpp, csrc/gguf_reader.cpp)
+  libpk_calib.so          copy kernel of known size (csrc/pk_calib.hip), used by bench.py to scale
+                          hardware byte counters
 
 Called by __graft_entry__.build(); every call recompiles.
 """
@@ -36,6 +38,13 @@ def build_hip():
     return out
 
 
+def build_calib():
+    out = os.path.join(HERE, "libpk_calib.so")
+    _run([HIPCC, *HIP_FLAGS, "-shared", os.path.join(CSRC, "pk_calib.hip"), "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build_decoder():
     srcs = [os.path.join(CSRC, f) for f in ("parakeet_decoder.cpp", "gguf_reader.cpp")]
     if not all(os.path.exists(s) for s in srcs):
@@ -48,7 +57,7 @@ def build_decoder():
 
 
 def build_all():
-    return [build_hip(), build_decoder()]
+    return [build_hip(), build_decoder(), build_calib()]
 
 
 if __name__ == "__main__":

@@ -98,18 +98,10 @@ struct KParams {
     unsigned long long *prof;    // nullable: per-phase wall-clock totals of workgroup 0 (100 MHz ticks)
 };
 
-// Phase timers (workgroup 0 only, when p.prof is set).
+// Phase timers (workgroup 0 only, when p.prof is set): totals kept in LDS,
+// written to p.prof when the loop ends.
 enum { kPrL0 = 0, kPrSync0, kPrL1, kPrSync1, kPrPred, kPrSync2, kPrJStage, kPrJCompute, kPrJSync, kPrDecide,
        kPrStageL, kPrN };
-__device__ __forceinline__ void pmark(const KParams &p, unsigned long long &last, int k) {
-    if (!p.prof) return;
-    __syncthreads();
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        const unsigned long long now = __builtin_amdgcn_s_memrealtime();
-        p.prof[k] += now - last;
-        last = now;
-    }
-}
 
 // ---------------------------------------------------------------- memory helpers
 
@@ -385,7 +377,18 @@ struct Ctl {                      // per-workgroup copy of its domain's control 
     int n, nl, nj;
     int dom, rank, P;
     unsigned long long wgkey[kDomCap][2];
+    unsigned long long prof[kPrN];
 };
+
+__device__ __forceinline__ void pmark(const KParams &p, Ctl &s, unsigned long long &last, int k) {
+    if (!p.prof) return;
+    __syncthreads();
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        const unsigned long long now = __builtin_amdgcn_s_memrealtime();
+        s.prof[k] += now - last;
+        last = now;
+    }
+}
 
 // Compact the LSTM list (pending token) and the joint list (frames left).
 __device__ void build_lists(Ctl &s) {
@@ -554,7 +557,7 @@ __device__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &
             }
         }
         __syncthreads();
-        pmark(p, tlast, kPrJStage);
+        pmark(p, s, tlast, kPrJStage);
         run_items(n_out, p.w_out.KB, S.red,
                   [&](int k, int kb0, int kb1) {
                       return tile_dot(p.w_out, s.rank + k * s.P, x.hi, x.lo, x.kp, 0, kb0, kb1, lane);
@@ -579,7 +582,7 @@ __device__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &
                       if (best[1]) atomicMax(&s.wgkey[c0 + u][1], best[1]);
                   });
         __syncthreads();
-        pmark(p, tlast, kPrJCompute);
+        pmark(p, s, tlast, kPrJCompute);
     }
     if (threadIdx.x < 2 * s.nj) {
         const int u = threadIdx.x / 2, head = threadIdx.x % 2;
@@ -633,8 +636,9 @@ __device__ void lstm_layer0(const KParams &p, Ctl &s, const Lds &S, bool redunda
 //   recurrent tiles  W_hh_lc . h_lc' -> R_lc for the utterance's next step
 //                    (stored in the other ping-pong half of rx).
 // Column tile: utterances lst[c0 .. c0+nc).
-__device__ void consume_layer(const KParams &p, Ctl &s, const Lds &S, const Bufs &B, const Act &x, int lc, int c0,
-                              int nc) {
+// Both matrices have K = H, so they share the K split.
+__device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Lds &S, const Bufs &B, const Act &x,
+                                              int lc, int c0, int nc) {
     const int lane = threadIdx.x & (kWave - 1), H = p.H;
     const bool last = lc == p.L - 1;
     const TMat &wc = last ? p.w_pred : p.w_ih[lc + 1];
@@ -642,9 +646,9 @@ __device__ void consume_layer(const KParams &p, Ctl &s, const Lds &S, const Bufs
     const int n_c = owned(wc.tiles, s.rank, s.P), n_r = owned(wr.tiles, s.rank, s.P);
     run_items(n_c + n_r, wc.KB, S.red,
               [&](int it, int kb0, int kb1) {
-                  if (it < n_c) return tile_dot(wc, s.rank + it * s.P, x.hi, x.lo, x.kp, 0, kb0, kb1, lane);
-                  return tile_dot(wr, s.rank + (it - n_c) * s.P, x.hi, x.lo, x.kp, 0, kb0 * wr.KB / wc.KB,
-                                  kb1 * wr.KB / wc.KB, lane);
+                  const bool rec = it >= n_c;
+                  return tile_dot(rec ? wr : wc, s.rank + (rec ? it - n_c : it) * s.P, x.hi, x.lo, x.kp, 0, kb0, kb1,
+                                  lane);
               },
               [&](int it, f32x4 acc) {
                   const int u = lane & 15;
@@ -698,30 +702,30 @@ __device__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bufs &B, const Lds
     const bool redundant = s.nl <= kSmallB && p.n_dom == 1;
     const Act &x = S.act[1];
     lstm_layer0(p, s, S, redundant);
-    pmark(p, tlast, kPrL0);
+    pmark(p, s, tlast, kPrL0);
     for (int lc = 0; lc < L; ++lc) {
-        if (lc == 0 && redundant) {
-            __syncthreads();
-            for (int i = threadIdx.x; i < kTile * (H / 4); i += kBlock) {
-                const int u = i / (H / 4), k = (i - u * (H / 4)) * 4;
-                put4(x, u, k, u < s.nl ? *reinterpret_cast<const float4 *>(S.h0s + u * H + k) : make_float4(0.f, 0.f, 0.f, 0.f));
-            }
-            __syncthreads();
-            consume_layer(p, s, S, B, x, 0, 0, s.nl);
-            __syncthreads();
-        } else {
+        const bool local = lc == 0 && redundant;     // h_0' is in LDS already
+        if (!local) {
             if (!dom_sync(p, s, epoch)) return false;
-            pmark(p, tlast, lc == 0 ? kPrSync0 : kPrSync1);
-            for (int c0 = 0; c0 < s.nl; c0 += kTile) {
-                const int nc = min(kTile, s.nl - c0);
-                stage_act(x, H, nc, B.hx, [&](int u) { const int ul = s.lst[c0 + u]; return hx_off(p, s.cur[ul] ^ 1, lc, s.b[ul]); });
-                __syncthreads();
-                pmark(p, tlast, kPrStageL);
-                consume_layer(p, s, S, B, x, lc, c0, nc);
-                __syncthreads();
-            }
+            pmark(p, s, tlast, lc == 0 ? kPrSync0 : kPrSync1);
         }
-        pmark(p, tlast, lc == L - 1 ? kPrPred : kPrL1);
+        for (int c0 = 0; c0 < s.nl; c0 += kTile) {
+            const int nc = min(kTile, s.nl - c0);
+            if (local) {
+                __syncthreads();
+                for (int i = threadIdx.x; i < kTile * (H / 4); i += kBlock) {
+                    const int u = i / (H / 4), k = (i - u * (H / 4)) * 4;
+                    put4(x, u, k, u < nc ? *reinterpret_cast<const float4 *>(S.h0s + u * H + k) : make_float4(0.f, 0.f, 0.f, 0.f));
+                }
+            } else {
+                stage_act(x, H, nc, B.hx, [&](int u) { const int ul = s.lst[c0 + u]; return hx_off(p, s.cur[ul] ^ 1, lc, s.b[ul]); });
+            }
+            __syncthreads();
+            pmark(p, s, tlast, kPrStageL);
+            consume_layer(p, s, S, B, x, lc, c0, nc);
+            __syncthreads();
+        }
+        pmark(p, s, tlast, lc == L - 1 ? kPrPred : kPrL1);
     }
     for (int i = threadIdx.x; i < s.nl; i += kBlock) {   // the new state becomes current
         const int ul = s.lst[i];
@@ -730,7 +734,7 @@ __device__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bufs &B, const Lds
         s.flags[ul] &= ~kFlagZeroHC;
     }
     const bool ok = dom_sync(p, s, epoch);
-    pmark(p, tlast, kPrSync2);
+    pmark(p, s, tlast, kPrSync2);
     return ok;
 }
 
@@ -848,6 +852,7 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         S.h0s = reinterpret_cast<float *>(q);
     }
 
+    if (threadIdx.x < kPrN) s.prof[threadIdx.x] = 0ull;
     if (threadIdx.x == 0) {
         s.dom = p.wg_dom[wg];
         s.rank = p.wg_rank[wg];
@@ -912,14 +917,15 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         if (s.nj > 0) {
             joint_phase(p, s, B, S, iter, tlast);
             ok = dom_sync(p, s, epoch);
-            pmark(p, tlast, kPrJSync);
+            pmark(p, s, tlast, kPrJSync);
             if (!ok) break;
             decide(p, s, iter);
         }
         __syncthreads();
         build_lists(s);
-        pmark(p, tlast, kPrDecide);
+        pmark(p, s, tlast, kPrDecide);
     }
+    if (p.prof && wg == 0 && threadIdx.x < kPrN) p.prof[threadIdx.x] = s.prof[threadIdx.x];
     if (!ok) return;
 
     for (int ul = s.rank; ul < s.n; ul += s.P) {

@@ -83,3 +83,29 @@ def lockstep_counts(traces: list, kind: int, blank: int, eou: int = -1, eob: int
         np.add.at(A_l, idx, 1)
     last = int(max(np.max(np.nonzero(A_j)[0], initial=0), np.max(np.nonzero(A_l)[0], initial=0)))
     return A_j[1:last + 1], A_l[1:last + 1]
+
+
+def _pmc_rows(path: str, counter: str):
+    import csv
+    with open(path, newline="") as f:
+        return [r for r in csv.DictReader(f) if r.get("Counter_Name") == counter]
+
+
+def pmc_traffic(fetch_csv: str, write_csv: str, kernel: str = "decode_loop_kernel",
+                probe: str = "calib_copy_kernel", probe_bytes: int = 256 << 20):
+    """HBM bytes per launch of `kernel` from two rocprofv3 --pmc runs
+    (FETCH_SIZE, then WRITE_SIZE; counter_collection.csv, values in KiB per
+    dispatch), each scaled so that the copy kernel of the same run reads
+    `probe_bytes` read and `probe_bytes` written.  Returns a dict."""
+    out = {}
+    for name, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = _pmc_rows(path, name)
+        cal = [float(r["Counter_Value"]) for r in rows if probe in r["Kernel_Name"]]
+        vals = [float(r["Counter_Value"]) for r in rows if kernel in r["Kernel_Name"]]
+        if not cal or not vals:
+            raise ValueError(f"{path}: no {probe} or {kernel} dispatch with {name}")
+        factor = probe_bytes / (cal[0] * 1024.0)
+        out[name] = {"kib_per_dispatch": float(np.mean(vals)), "copy_kib": cal[0], "factor": factor,
+                     "bytes_per_launch": float(np.mean(vals)) * 1024.0 * factor}
+    out["bytes_per_launch"] = out["FETCH_SIZE"]["bytes_per_launch"] + out["WRITE_SIZE"]["bytes_per_launch"]
+    return out
