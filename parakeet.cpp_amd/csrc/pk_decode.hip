@@ -171,7 +171,7 @@ int vec_f32(const pk_tensor &t, int n, const std::vector<int> *map, std::vector<
 struct HostTiled {
     int type = 0, rows = 0, tiles = 0, KB = 0;
     std::vector<uint8_t> a, a_lo;
-    std::vector<float> scale;
+    std::vector<uint16_t> scale;   // q8_0 block scales as stored (f16 bits)
 };
 
 int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *map, HostTiled &out, const char *name) {
@@ -185,7 +185,7 @@ int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *
     const uint8_t *src = static_cast<const uint8_t *>(t.data);
     if (t.type == PK_TYPE_Q8_0) {
         out.a.assign(frags * kWave * 8, 0);
-        out.scale.assign(frags * kTile, 0.0f);
+        out.scale.assign(frags * kTile, 0);
         for (int tile = 0; tile < out.tiles; ++tile)
             for (int r = 0; r < kTile; ++r) {
                 const int row = tile * kTile + r;
@@ -195,7 +195,7 @@ int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *
                     const size_t f = (size_t)tile * out.KB + kb;
                     uint16_t dh;
                     memcpy(&dh, srow + 34 * kb, 2);
-                    out.scale[f * kTile + r] = f16_to_f32(dh);
+                    out.scale[f * kTile + r] = dh;
                     for (int g = 0; g < 4; ++g)   // lane r + 16 g holds q[8g .. 8g+8)
                         memcpy(&out.a[(f * kWave + r + 16 * g) * 8], srow + 34 * kb + 2 + 8 * g, 8);
                 }
@@ -238,7 +238,8 @@ struct pk_decoder {
     int device = 0;
     int n_cu = 0, lds_block = 0;
     int nwg = 0;               // decode-loop workgroups
-    size_t lds_bytes = 0;      // dynamic LDS of the decode loop
+    size_t lds_bytes = 0;      // dynamic LDS limit of the decode loop
+    size_t lds_fixed = 0;      // activation blocks + redundant layer-0 output
     hipStream_t stream = nullptr;
     hipEvent_t ev[3] = {};
     DevBuf arena;              // weights
@@ -284,7 +285,7 @@ void arena_tiled(Arena &ar, HostTiled &h, TMat &m) {
     m.KB = h.KB;
     ar.add(h.a.data(), h.a.size(), &m.a);
     ar.add(h.a_lo.data(), h.a_lo.size(), &m.a_lo);
-    ar.add(h.scale.data(), h.scale.size() * 4, reinterpret_cast<const void **>(&m.scale));
+    ar.add(h.scale.data(), h.scale.size() * 2, reinterpret_cast<const void **>(&m.scale));
 }
 
 // Domain plan for m utterances over nwg workgroups (see KParams::n_dom).
@@ -422,6 +423,14 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     arena_tiled(ar, tiled[2 * L], kp.w_pred);
     if ((rc = tile_matrix(d->joint_out_w, Vo, J, nullptr, tiled[2 * L + 1], "joint.out.weight"))) return cleanup(rc);
     arena_tiled(ar, tiled[2 * L + 1], kp.w_out);
+    // a phase multiplies one staged vector by two matrices in one pass: W_ih[l+1] (or
+    // W_p) with W_hh[l]; the pair must share a storage type
+    for (int l = 0; l < L; ++l) {
+        const HostTiled &consumer = l + 1 < L ? tiled[2 * (l + 1)] : tiled[2 * L];
+        if (consumer.type != tiled[2 * l + 1].type)
+            return cleanup(fail(PK_ERR_UNSUPPORTED, "layer %d: w_hh type %d differs from its consumer's type %d", l,
+                                tiled[2 * l + 1].type, consumer.type));
+    }
     std::vector<float> b_pred, b_out, b_enc, w_enc;
     if ((rc = vec_f32(d->joint_pred_b, J, nullptr, b_pred, "joint.pred.bias"))) return cleanup(rc);
     if ((rc = vec_f32(d->joint_out_b, Vo, nullptr, b_out, "joint.out.bias"))) return cleanup(rc);
@@ -489,11 +498,12 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     // [hidden | h_0 .. h_{L-1}] of one 16-utterance tile + K-split partials +
     // the redundant layer-0 output
     const size_t act = (size_t)kTile * ((J + kKPad) + (size_t)(H + kKPad)) * 2 * 2;
-    if (std::max(J, H) > 4 * pkdev::kStageMax * kBlock / kTile)
-        return cleanup(fail(PK_ERR_UNSUPPORTED, "hidden sizes above %d", 4 * pkdev::kStageMax * kBlock / kTile));
-    const size_t need = act + (size_t)kWaves * kWave * 16 + (size_t)kSmallB * H * 4;
-    if (need + sizeof(pkdev::Ctl) + 256 > (size_t)dec->lds_block)
-        return cleanup(fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed, %d available", need + sizeof(pkdev::Ctl),
+    if (std::max(J, H) > 4096)
+        return cleanup(fail(PK_ERR_UNSUPPORTED, "hidden sizes above 4096"));
+    dec->lds_fixed = act + (size_t)kSmallB * H * 4;
+    const size_t need = (size_t)dec->lds_block - sizeof(pkdev::Ctl) - 512;   // upper bound of any launch
+    if (dec->lds_fixed + (size_t)2 * kWaves * kWave * 16 > need)
+        return cleanup(fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed, %d available", dec->lds_fixed + sizeof(pkdev::Ctl),
                             dec->lds_block));
     dec->lds_bytes = need;
     if (hipFuncSetAttribute(reinterpret_cast<const void *>(pkdev::decode_loop_kernel),
@@ -755,9 +765,21 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         HIP_TRY(hipMemsetAsync(dec->d_prof.p, 0, pkdev::kPrN * 8, dec->stream));
         p.prof = dec->d_prof.as<unsigned long long>();
     }
+    // LDS partial slots: the most items any phase gives one workgroup, plus one per wave
+    {
+        auto items = [&](const pkdev::TMat &m) { return (m.tiles + pl.P - 1) / pl.P; };
+        int most = items(p.w_out);
+        for (int l = 0; l < p.L; ++l)
+            most = std::max(most, items(l + 1 < p.L ? p.w_ih[l + 1] : p.w_pred) + items(p.w_hh[l]));
+        p.red_slots = most + kWaves;
+    }
+    const size_t lds = dec->lds_fixed + (size_t)p.red_slots * kWave * 16;
+    if (lds > dec->lds_bytes)
+        return fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed for %d workgroups per domain, %zu available", lds, pl.P,
+                    dec->lds_bytes);
     void *args[] = {&p};
     HIP_TRY(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(pkdev::decode_loop_kernel), dim3(nwg),
-                                       dim3(kBlock), args, dec->lds_bytes, dec->stream));
+                                       dim3(kBlock), args, lds, dec->stream));
     HIP_TRY(hipEventRecord(dec->ev[2], dec->stream));
     int status[4] = {0, 0, 0, 0};
     HIP_TRY(hipMemcpyAsync(status, p.status, sizeof status, hipMemcpyDeviceToHost, dec->stream));

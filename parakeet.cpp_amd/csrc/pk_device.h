@@ -40,13 +40,14 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // A weight matrix [rows][K] laid out as MFMA A fragments: for row tile t and
 // K block kb (32 columns), lane l holds the 8 consecutive weights of row
 // 16t + l%16 starting at column 32kb + 8(l/16).  q8_0: 8 int8 per lane plus
-// the block scales d[16t + r][kb] at scale[(t*KB + kb)*16 + r]; f16: 8 halves
-// per lane; f32: the same two f16 planes holding hi = f16(w), lo = f16(w - hi).
+// the block scales d[16t + r][kb] (the stored f16 bits) at
+// scale[(t*KB + kb)*16 + r]; f16: 8 halves per lane; f32: two f16 planes
+// holding hi = f16(w), lo = f16(w - hi).
 struct TMat {
-    const void *a;        // fragment plane
-    const void *a_lo;     // f32 weights: low halves
-    const float *scale;   // q8_0 block scales
-    int type;             // PK_TYPE_Q8_0, PK_TYPE_F16, PK_TYPE_F32
+    const void *a;                 // fragment plane
+    const void *a_lo;              // f32 weights: low halves
+    const unsigned short *scale;   // q8_0 block scales, f16 bits
+    int type;                      // PK_TYPE_Q8_0, PK_TYPE_F16, PK_TYPE_F32
     int rows, tiles, KB;
 };
 
@@ -92,9 +93,10 @@ struct KParams {
     const int *dom_wg;           // [n_dom][dom_size] workgroup of each rank
     // sync
     unsigned *flags;             // [nwg * kFlagStride]
-    unsigned long long *keys;    // [2][n_utts][2]
+    unsigned long long *keys;    // [2][n_utts][2] best keys, by iteration parity
     int *status;                 // [0] error code, [1] iterations, [2] overflow, [3] trace overflow
     int max_iter;
+    int red_slots;               // LDS partial slots: items of the largest phase + kWaves
     unsigned long long *prof;    // nullable: per-phase wall-clock totals of workgroup 0 (100 MHz ticks)
 };
 
@@ -141,92 +143,6 @@ __device__ __forceinline__ half8 q8_to_half8(uint2 q) {
     half2v p2 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u)) - off;
     half2v p3 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)) - off;
     return half8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-}
-
-// Partial product of one 16-row weight tile with one 16-utterance activation
-// tile over K blocks [kb0, kb1).  Activations are staged in LDS as f16 pairs
-// (hi, lo) with x = hi + lo, row stride kp halves; lane l of the result holds
-// rows 4(l/16)..4(l/16)+3 of utterance column l%16.  q8_0 blocks are
-// multiplied exactly (integers in f16) and scaled by d in f32 per block.
-// Weight fragments are fetched kGrp blocks ahead of their use.
-constexpr int kGrp = 4;
-__device__ __forceinline__ f32x4 tile_dot(const TMat &m, int tile, const _Float16 *xhi, const _Float16 *xlo, int kp,
-                                          int col0, int kb0, int kb1, int lane) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    const int xo = (col0 + (lane & 15)) * kp + (lane >> 4) * 8;
-    const size_t frag = (size_t)tile * m.KB;
-    if (m.type == PK_TYPE_Q8_0) {
-        const uint2 *a = static_cast<const uint2 *>(m.a) + frag * kWave + lane;
-        const float4 *sc = reinterpret_cast<const float4 *>(m.scale) + frag * 4 + (lane >> 4);
-        uint2 qa[kGrp], qb[kGrp];
-        float4 da[kGrp], db[kGrp];
-#pragma unroll
-        for (int i = 0; i < kGrp; ++i) {
-            qa[i] = qb[i] = make_uint2(0u, 0u);
-            da[i] = db[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int i = 0; i < kGrp; ++i)
-            if (kb0 + i < kb1) { qa[i] = a[(kb0 + i) * kWave]; da[i] = sc[(kb0 + i) * 4]; }
-        for (int g = kb0; g < kb1; g += kGrp) {
-#pragma unroll
-            for (int i = 0; i < kGrp; ++i)
-                if (g + kGrp + i < kb1) { qb[i] = a[(g + kGrp + i) * kWave]; db[i] = sc[(g + kGrp + i) * 4]; }
-#pragma unroll
-            for (int i = 0; i < kGrp; ++i) {
-                const int kb = g + i;
-                if (kb < kb1) {
-                    const half8 bh = *reinterpret_cast<const half8 *>(xhi + xo + kb * 32);
-                    const half8 bl = *reinterpret_cast<const half8 *>(xlo + xo + kb * 32);
-                    const half8 w = q8_to_half8(qa[i]);
-                    f32x4 p = {0.f, 0.f, 0.f, 0.f};
-                    p = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bh, p, 0, 0, 0);
-                    p = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bl, p, 0, 0, 0);
-                    acc[0] = fmaf(da[i].x, p[0], acc[0]);
-                    acc[1] = fmaf(da[i].y, p[1], acc[1]);
-                    acc[2] = fmaf(da[i].z, p[2], acc[2]);
-                    acc[3] = fmaf(da[i].w, p[3], acc[3]);
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < kGrp; ++i) { qa[i] = qb[i]; da[i] = db[i]; }
-        }
-    } else {
-        const bool two = m.type == PK_TYPE_F32;
-        const half8 *a = static_cast<const half8 *>(m.a) + frag * kWave + lane;
-        const half8 *al = two ? static_cast<const half8 *>(m.a_lo) + frag * kWave + lane : a;
-        half8 wa[kGrp], wb[kGrp], la[kGrp], lb[kGrp];
-#pragma unroll
-        for (int i = 0; i < kGrp; ++i) wa[i] = wb[i] = la[i] = lb[i] = half8{};
-#pragma unroll
-        for (int i = 0; i < kGrp; ++i)
-            if (kb0 + i < kb1) {
-                wa[i] = a[(kb0 + i) * kWave];
-                if (two) la[i] = al[(kb0 + i) * kWave];
-            }
-        for (int g = kb0; g < kb1; g += kGrp) {
-#pragma unroll
-            for (int i = 0; i < kGrp; ++i)
-                if (g + kGrp + i < kb1) {
-                    wb[i] = a[(g + kGrp + i) * kWave];
-                    if (two) lb[i] = al[(g + kGrp + i) * kWave];
-                }
-#pragma unroll
-            for (int i = 0; i < kGrp; ++i) {
-                const int kb = g + i;
-                if (kb < kb1) {
-                    const half8 bh = *reinterpret_cast<const half8 *>(xhi + xo + kb * 32);
-                    const half8 bl = *reinterpret_cast<const half8 *>(xlo + xo + kb * 32);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[i], bh, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa[i], bl, acc, 0, 0, 0);
-                    if (two) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(la[i], bh, acc, 0, 0, 0);
-                }
-            }
-#pragma unroll
-            for (int i = 0; i < kGrp; ++i) { wa[i] = wb[i]; la[i] = lb[i]; }
-        }
-    }
-    return acc;
 }
 
 __device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo) {
@@ -376,7 +292,7 @@ struct Ctl {                      // per-workgroup copy of its domain's control 
     int lst[kDomCap], jst[kDomCap];
     int n, nl, nj;
     int dom, rank, P;
-    unsigned long long wgkey[kDomCap][2];
+    unsigned long long wgkey[kDomCap][2];   // this workgroup's best key per utterance and head
     unsigned long long prof[kPrN];
 };
 
@@ -391,7 +307,7 @@ __device__ __forceinline__ void pmark(const KParams &p, Ctl &s, unsigned long lo
 }
 
 // Compact the LSTM list (pending token) and the joint list (frames left).
-__device__ void build_lists(Ctl &s) {
+__device__ __forceinline__ void build_lists(Ctl &s) {
     if (threadIdx.x < kWave) {
         const int lane = threadIdx.x;
         const bool fl = lane < s.n && s.pend[lane] >= 0;
@@ -424,10 +340,12 @@ __device__ __forceinline__ bool dom_sync(const KParams &p, const Ctl &s, unsigne
     }
     __syncthreads();
     if (threadIdx.x < s.P) {
+        // tight poll; the error word and the clock are checked every 64 polls
         unsigned *f = p.flags + (size_t)p.dom_wg[s.dom * s.P + threadIdx.x] * kFlagStride;
         const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        unsigned n = 0;
         while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < epoch) {
-            __builtin_amdgcn_s_sleep(1);
+            if ((++n & 63) != 0) continue;
             if (__hip_atomic_load(p.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) { s_ok = 0; break; }
             if (__builtin_amdgcn_s_memrealtime() - t0 > 200000000ull) {   // 100 MHz clock: 2 s
                 __hip_atomic_store(p.status, PK_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -456,55 +374,179 @@ struct Bufs {
 // Stage vectors of length K for n <= 16 utterances into an activation block:
 // row u <- src(off(u)) via coherent loads; rows n .. 15 are zero.  Every
 // thread issues all of its loads before converting any of them.
-constexpr int kStageMax = 8;    // float4 per thread: 16 rows x K/4 <= kStageMax * kBlock  (K <= 1024)
+constexpr int kStageMax = 5;    // float4 per thread per round: one round covers 16 rows of K <= 640
 template <class OffFn>
 __device__ __forceinline__ void stage_act(const Act &x, int K, int n, __amdgpu_buffer_rsrc_t r, OffFn off) {
     const int per = K / 4;
-    float4 v[kStageMax];
+    for (int base = 0; base < kTile * per; base += kStageMax * kBlock) {
+        float4 v[kStageMax];
 #pragma unroll
-    for (int j = 0; j < kStageMax; ++j) {
-        const int i = threadIdx.x + j * kBlock;
-        const int u = i / per, k = (i - u * per) * 4;
-        v[j] = (i < kTile * per && u < n) ? ld4_coh(r, (unsigned)((off(u) + k) * 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int j = 0; j < kStageMax; ++j) {
-        const int i = threadIdx.x + j * kBlock;
-        if (i < kTile * per) {
+        for (int j = 0; j < kStageMax; ++j) {
+            const int i = base + threadIdx.x + j * kBlock;
             const int u = i / per, k = (i - u * per) * 4;
-            put4(x, u, k, v[j]);
+            v[j] = (i < kTile * per && u < n) ? ld4_coh(r, (unsigned)((off(u) + k) * 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < kStageMax; ++j) {
+            const int i = base + threadIdx.x + j * kBlock;
+            if (i < kTile * per) {
+                const int u = i / per, k = (i - u * per) * 4;
+                put4(x, u, k, v[j]);
+            }
         }
     }
 }
 
-// Work split of a set of (tile, utterance-tile) items over the 8 waves:
-// with few items, K is split S ways and the partials are summed in LDS in a
-// fixed order (deterministic).  fn(item, kb0, kb1) returns the partial;
-// epi(item, acc) consumes the total.
-template <class DotFn, class EpiFn>
-__device__ __forceinline__ void run_items(int n_items, int KB, f32x4 *red, DotFn dot, EpiFn epi) {
+// ---------------------------------------------------------------- MFMA phase engine
+//
+// A phase multiplies weight row tiles ("items") by one staged 16-utterance
+// activation block.  Items 0 .. n_a-1 are tiles rank, rank+P, ... of matrix A,
+// items n_a .. n_items-1 the same of matrix B (same storage type and K).  Each
+// item's K blocks are cut into units of at most kUnit blocks (f32 weights count
+// every K block twice, once per f16 plane); the units are numbered item-major
+// and every wave takes a contiguous range of them.  A unit's fragments are
+// loaded with one batch of loads and multiplied by straight-line code, so
+// loads, LDS reads and MFMAs of different blocks overlap.  A wave keeps a running
+// partial while its units belong to one item and leaves one partial per
+// (item, wave) in LDS slot item + wave; phase_reduce sums each item's partials
+// in wave order -- a fixed order, so results do not depend on timing.
+
+constexpr int kUnit = 10;  // K blocks per unit
+
+// Fragments of one unit: blocks sb0 .. sb0+nb-1 of one tile; blocks past nb
+// read as zero (buffer loads past the range return 0).
+template <bool Q8>
+__device__ __forceinline__ void unit_load(const TMat &m, bool two, int tile, int sb0, int nb, int lane,
+                                          uint4 (&f)[kUnit]) {
+    const unsigned bad = 0x80000000u;
+    if (Q8) {
+        const __amdgpu_buffer_rsrc_t rq = rsrc(m.a, (unsigned)m.tiles * m.KB * kWave * 8u);
+        const __amdgpu_buffer_rsrc_t rs = rsrc(m.scale, (unsigned)m.tiles * m.KB * kTile * 2u);
+        const unsigned f0 = (unsigned)tile * m.KB + sb0;
+#pragma unroll
+        for (int j = 0; j < kUnit; ++j) {
+            const bool ok = j < nb;
+            const unsigned oq = ok ? ((f0 + j) * kWave + lane) * 8u : bad;
+            const unsigned os = ok ? ((f0 + j) * kTile + (lane >> 4) * 4u) * 2u : bad;
+            const uint2 q = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, oq, 0, 0));
+            const uint2 d = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, os, 0, 0));
+            f[j] = make_uint4(q.x, q.y, d.x, d.y);
+        }
+    } else {
+        const unsigned bytes = (unsigned)m.tiles * m.KB * kWave * 16u;
+        const __amdgpu_buffer_rsrc_t rh = rsrc(m.a, bytes);
+        const __amdgpu_buffer_rsrc_t rl = rsrc(two ? m.a_lo : m.a, bytes);
+#pragma unroll
+        for (int j = 0; j < kUnit; ++j) {
+            const int sb = sb0 + j;
+            const int kb = two ? sb >> 1 : sb;
+            const unsigned o = j < nb ? (((unsigned)tile * m.KB + kb) * kWave + lane) * 16u : bad;
+            f[j] = __builtin_bit_cast(uint4, (two && (sb & 1)) ? __builtin_amdgcn_raw_buffer_load_b128(rl, o, 0, 0)
+                                                               : __builtin_amdgcn_raw_buffer_load_b128(rh, o, 0, 0));
+        }
+    }
+}
+
+// acc += (unit's weight blocks) . (activation blocks); xo = this lane's
+// activation offset.  Zero blocks past nb add nothing.
+template <bool Q8>
+__device__ __forceinline__ f32x4 unit_mma(const uint4 (&f)[kUnit], const Act &x, int xo, bool two, int sb0, int nb,
+                                          f32x4 acc) {
+#pragma unroll
+    for (int j = 0; j < kUnit; ++j) {
+        const int sb = min(sb0 + j, sb0 + nb - 1);
+        const int kb = two ? sb >> 1 : sb;
+        const half8 bh = *reinterpret_cast<const half8 *>(x.hi + xo + kb * 32);
+        const half8 bl = *reinterpret_cast<const half8 *>(x.lo + xo + kb * 32);
+        if (Q8) {
+            const half8 w = q8_to_half8(make_uint2(f[j].x, f[j].y));
+            f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bh, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            p = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bl, p, 0, 0, 0);
+            const half2v d01 = __builtin_bit_cast(half2v, f[j].z), d23 = __builtin_bit_cast(half2v, f[j].w);
+            acc[0] = fmaf((float)d01[0], p[0], acc[0]);
+            acc[1] = fmaf((float)d01[1], p[1], acc[1]);
+            acc[2] = fmaf((float)d23[0], p[2], acc[2]);
+            acc[3] = fmaf((float)d23[1], p[3], acc[3]);
+        } else {
+            // f16 weights: hi and lo activations; f32 weights: the lo plane (odd
+            // sub-blocks) skips the lo activations (lo x lo is below f32 rounding)
+            const half8 w = __builtin_bit_cast(half8, f[j]);
+            const half8 b2 = (two && ((sb0 + j) & 1)) ? half8{} : bl;
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, b2, acc, 0, 0, 0);
+        }
+    }
+    return acc;
+}
+
+// Wave w's unit range [c0, c1) of N units.
+__device__ __forceinline__ int wave_cut(int N, int w) { return (int)(((long long)N * w) / kWaves); }
+
+__device__ __forceinline__ int blocks_per_item(const TMat &m) { return m.type == PK_TYPE_F32 ? 2 * m.KB : m.KB; }
+
+template <bool Q8>
+__device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
+                                               const Act &x, f32x4 *red) {
+    // wave-uniform unit bookkeeping: the weight buffer descriptors stay in SGPRs
+    const int lane = threadIdx.x & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const bool two = !Q8 && A.type == PK_TYPE_F32;
+    const int KBe = two ? 2 * A.KB : A.KB;
+    const int S = (KBe + kUnit - 1) / kUnit;          // units per item
+    const int N = n_items * S;
+    const int c0 = wave_cut(N, wave), c1 = wave_cut(N, wave + 1);
+    if (c0 >= c1) return;
+    const int xo = (lane & 15) * x.kp + (lane >> 4) * 8;
+    auto unit = [&](int u, int &item, int &sb0, int &nb) {
+        item = u / S;
+        const int c = u - item * S;
+        sb0 = c * kUnit;
+        nb = min(kUnit, KBe - sb0);
+    };
+    auto fetch = [&](int item, int sb0, int nb, uint4 (&f)[kUnit]) {
+        const bool in_a = item < n_a;
+        unit_load<Q8>(in_a ? A : Bm, two, rank + (in_a ? item : item - n_a) * P, sb0, nb, lane, f);
+    };
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int u = c0; u < c1; ++u) {
+        int item, sb0, nb;
+        unit(u, item, sb0, nb);
+        uint4 f[kUnit];
+        fetch(item, sb0, nb, f);
+        acc = unit_mma<Q8>(f, x, xo, two, sb0, nb, acc);
+        if (u + 1 == c1 || (u + 1) / S != item) {
+            red[(item + wave) * kWave + lane] = acc;
+            acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+}
+
+// Sum each item's partials in wave order and run epi(item, acc); items are
+// dealt round robin over the waves.  Brackets the LDS traffic with barriers.
+template <class EpiFn>
+__device__ __forceinline__ void phase_reduce(int n_items, int S, const f32x4 *red, EpiFn epi) {
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    if (n_items <= 0) return;
-    int S = kWaves / n_items;
-    if (S < 1) S = 1;
-    if (S > KB) S = KB;
-    if (S == 1) {
-        for (int it = wave; it < n_items; it += kWaves) epi(it, dot(it, 0, KB));
-        return;
-    }
-    const int units = n_items * S;          // <= kWaves
-    if (wave < units) {
-        const int it = wave / S, s = wave % S;
-        const int kb0 = s * KB / S, kb1 = (s + 1) * KB / S;
-        red[wave * kWave + lane] = dot(it, kb0, kb1);
-    }
+    const int N = n_items * S;
     __syncthreads();
     for (int it = wave; it < n_items; it += kWaves) {
-        f32x4 acc = red[(it * S) * kWave + lane];
-        for (int s = 1; s < S; ++s) acc += red[(it * S + s) * kWave + lane];
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int w = 0; w < kWaves; ++w) {
+            const int a0 = wave_cut(N, w), a1 = wave_cut(N, w + 1);
+            if (a0 < a1 && a0 < (it + 1) * S && a1 > it * S) acc += red[(it + w) * kWave + lane];
+        }
         epi(it, acc);
     }
     __syncthreads();
+}
+
+// Products of one phase for this workgroup, then the epilogue per item.
+template <class EpiFn>
+__device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
+                                          const Act &x, f32x4 *red, EpiFn epi) {
+    if (n_items <= 0) return;
+    if (A.type == PK_TYPE_Q8_0) phase_partials<true>(A, n_a, Bm, n_items, rank, P, x, red);
+    else phase_partials<false>(A, n_a, Bm, n_items, rank, P, x, red);
+    const int KBe = A.type == PK_TYPE_F32 ? 2 * A.KB : A.KB;
+    phase_reduce(n_items, (KBe + kUnit - 1) / kUnit, red, epi);
 }
 
 // Tiles of a matrix with `tiles` row tiles owned by rank r of P: t = r, r+P, ...
@@ -512,28 +554,27 @@ __device__ __forceinline__ int owned(int tiles, int r, int P) { return tiles > r
 
 struct Lds {
     Act act[1 + PK_MAX_LAYERS];   // staged activation blocks
-    f32x4 *red;                   // [kWaves][kWave] K-split partials
+    f32x4 *red;                   // [red_slots][kWave] per-(item, wave) partials
     float *h0s;                   // [kSmallB][H] layer-0 output in redundant mode
 };
 
 // Joint + argmax for this workgroup's output tiles.  Utterances are processed
 // 16 at a time (one MFMA column tile).
-__device__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned stamp,
+__device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned stamp,
                             unsigned long long &tlast) {
     const int J = p.J, lane = threadIdx.x & (kWave - 1);
-    unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * 2;
     if (threadIdx.x < 2 * kDomCap) s.wgkey[threadIdx.x / 2][threadIdx.x % 2] = 0ull;
     const int n_out = owned(p.w_out.tiles, s.rank, s.P);
     const Act &x = S.act[0];
     for (int c0 = 0; c0 < s.nj; c0 += kTile) {
         const int nc = min(kTile, s.nj - c0);
         // stage hidden = relu(encp[t] + pp) for this column tile
-        {
+        for (int base = 0; base < kTile * (J / 4); base += kStageMax * kBlock) {
             const int per = J / 4;
             float4 e[kStageMax], q[kStageMax];
 #pragma unroll
             for (int j = 0; j < kStageMax; ++j) {
-                const int i = threadIdx.x + j * kBlock;
+                const int i = base + threadIdx.x + j * kBlock;
                 const int u = i / per, k = (i - u * per) * 4;
                 e[j] = q[j] = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (i < kTile * per && u < nc) {
@@ -544,7 +585,7 @@ __device__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &
             }
 #pragma unroll
             for (int j = 0; j < kStageMax; ++j) {
-                const int i = threadIdx.x + j * kBlock;
+                const int i = base + threadIdx.x + j * kBlock;
                 if (i < kTile * per) {
                     const int u = i / per, k = (i - u * per) * 4;
                     float4 v = make_float4(e[j].x + q[j].x, e[j].y + q[j].y, e[j].z + q[j].z, e[j].w + q[j].w);
@@ -558,32 +599,62 @@ __device__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &
         }
         __syncthreads();
         pmark(p, s, tlast, kPrJStage);
-        run_items(n_out, p.w_out.KB, S.red,
-                  [&](int k, int kb0, int kb1) {
-                      return tile_dot(p.w_out, s.rank + k * s.P, x.hi, x.lo, x.kp, 0, kb0, kb1, lane);
-                  },
+        // bias rows of this wave's first two items and the blank offset of this
+        // lane's utterance, loaded before the products
+        const int u = lane & 15, wave = threadIdx.x / kWave;
+        const int b_u = u < nc ? s.b[s.jst[c0 + u]] : 0;
+        const float bb = (u < nc && p.blank_bias) ? p.blank_bias[b_u] : 0.0f;
+        float4 pre_b[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int row0 = (s.rank + (wave + k * kWaves) * s.P) * kTile + (lane >> 4) * 4;
+            pre_b[k].x = row0 < p.Vo ? p.b_out[row0] : 0.0f;
+            pre_b[k].y = row0 + 1 < p.Vo ? p.b_out[row0 + 1] : 0.0f;
+            pre_b[k].z = row0 + 2 < p.Vo ? p.b_out[row0 + 2] : 0.0f;
+            pre_b[k].w = row0 + 3 < p.Vo ? p.b_out[row0 + 3] : 0.0f;
+        }
+        // each lane keeps its best key per head over all its rows; lanes of one
+        // column then combine, and one LDS atomic per column and head follows
+        unsigned long long best0 = 0ull, best1 = 0ull;
+        run_phase(p.w_out, n_out, p.w_out, n_out, s.rank, s.P, x, S.red,
                   [&](int k, f32x4 acc) {
-                      const int u = lane & 15;
                       if (u >= nc) return;
-                      const int b = s.b[s.jst[c0 + u]];
                       const int tile = s.rank + k * s.P;
-                      unsigned long long best[2] = {0ull, 0ull};
+                      const int kk = (k - wave) / kWaves;
+                      const float4 bias4 = kk == 0 ? pre_b[0] : pre_b[1];
 #pragma unroll
                       for (int i = 0; i < 4; ++i) {
                           const int row = tile * kTile + (lane >> 4) * 4 + i;
                           if (row >= p.Vo) continue;
-                          float v = acc[i] + p.b_out[row];
-                          if (row == p.blank && p.blank_bias) v += p.blank_bias[b];
-                          const int head = row < p.V1 ? 0 : 1;
-                          const unsigned long long key = make_key(v, head ? row - p.V1 : row);
-                          best[head] = key > best[head] ? key : best[head];
+                          const float bias = kk < 2 ? (i == 0 ? bias4.x : i == 1 ? bias4.y : i == 2 ? bias4.z : bias4.w)
+                                                    : p.b_out[row];
+                          float v = acc[i] + bias;
+                          if (row == p.blank) v += bb;
+                          if (row < p.V1) {
+                              const unsigned long long key = make_key(v, row);
+                              best0 = key > best0 ? key : best0;
+                          } else {
+                              const unsigned long long key = make_key(v, row - p.V1);
+                              best1 = key > best1 ? key : best1;
+                          }
                       }
-                      if (best[0]) atomicMax(&s.wgkey[c0 + u][0], best[0]);
-                      if (best[1]) atomicMax(&s.wgkey[c0 + u][1], best[1]);
                   });
+#pragma unroll
+        for (int m = 16; m < kWave; m <<= 1) {
+            const unsigned long long o0 = __shfl_xor(best0, m, kWave), o1 = __shfl_xor(best1, m, kWave);
+            best0 = o0 > best0 ? o0 : best0;
+            best1 = o1 > best1 ? o1 : best1;
+        }
+        if (lane < 16 && u < nc) {
+            if (best0) atomicMax(&s.wgkey[c0 + u][0], best0);
+            if (best1) atomicMax(&s.wgkey[c0 + u][1], best1);
+        }
         __syncthreads();
         pmark(p, s, tlast, kPrJCompute);
     }
+    // one device-scope max per utterance and head: the stamp keeps keys of
+    // iteration `stamp` above every older key in the same parity buffer
+    unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * 2;
     if (threadIdx.x < 2 * s.nj) {
         const int u = threadIdx.x / 2, head = threadIdx.x % 2;
         const unsigned long long k = s.wgkey[u][head];
@@ -598,7 +669,7 @@ __device__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &
 // elementwise per unit.  redundant: every unit for every listed utterance,
 // h' kept in LDS (h0s) as well; otherwise only this workgroup's unit tiles.
 // Owners store h', c' coherently.
-__device__ void lstm_layer0(const KParams &p, Ctl &s, const Lds &S, bool redundant) {
+__device__ __forceinline__ void lstm_layer0(const KParams &p, Ctl &s, const Lds &S, bool redundant) {
     const int H = p.H;
     const int groups = p.w_hh[0].tiles;                 // unit groups of 4
     const int n_own = owned(groups, s.rank, s.P);
@@ -636,7 +707,7 @@ __device__ void lstm_layer0(const KParams &p, Ctl &s, const Lds &S, bool redunda
 //   recurrent tiles  W_hh_lc . h_lc' -> R_lc for the utterance's next step
 //                    (stored in the other ping-pong half of rx).
 // Column tile: utterances lst[c0 .. c0+nc).
-// Both matrices have K = H, so they share the K split.
+// Both matrices have K = H and the same storage type.
 __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Lds &S, const Bufs &B, const Act &x,
                                               int lc, int c0, int nc) {
     const int lane = threadIdx.x & (kWave - 1), H = p.H;
@@ -644,12 +715,28 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
     const TMat &wc = last ? p.w_pred : p.w_ih[lc + 1];
     const TMat &wr = p.w_hh[lc];
     const int n_c = owned(wc.tiles, s.rank, s.P), n_r = owned(wr.tiles, s.rank, s.P);
-    run_items(n_c + n_r, wc.KB, S.red,
-              [&](int it, int kb0, int kb1) {
-                  const bool rec = it >= n_c;
-                  return tile_dot(rec ? wr : wc, s.rank + (rec ? it - n_c : it) * s.P, x.hi, x.lo, x.kp, 0, kb0, kb1,
-                                  lane);
-              },
+    // Cell-update operands (R, c_prev, bias) of this wave's first kPre consumer
+    // items: they were written one step earlier, so they are loaded before the
+    // products rather than after them.
+    constexpr int kPre = 2;
+    const int wave = threadIdx.x / kWave, layer = lc + 1;
+    float4 pre_r[kPre], pre_b[kPre];
+    float pre_c[kPre];
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+        pre_r[k] = pre_b[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        pre_c[k] = 0.0f;
+        const int it = wave + k * kWaves, u = lane & 15;
+        if (last || it >= n_c || u >= nc) continue;
+        const int j = (s.rank + it * s.P) * 4 + (lane >> 4);
+        if (j >= H) continue;
+        const int ul = s.lst[c0 + u], b = s.b[ul], cur = s.cur[ul];
+        pre_b[k] = *reinterpret_cast<const float4 *>(p.b_lstm[layer] + 4 * j);
+        if (s.flags[ul] & kFlagZeroHC) continue;
+        pre_r[k] = ld4_coh(B.rx, (unsigned)((rx_off(p, cur, layer, b) + 4 * j) * 4));
+        pre_c[k] = ld_coh(p.cx + hx_off(p, cur, layer, b) + j);
+    }
+    run_phase(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red,
               [&](int it, f32x4 acc) {
                   const int u = lane & 15;
                   if (u >= nc) return;
@@ -671,20 +758,25 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
                       }
                       return;
                   }
-                  const int layer = lc + 1;
                   const int j = tile * 4 + (lane >> 4);
                   if (j >= H) return;
-                  const bool zero = s.flags[ul] & kFlagZeroHC;
-                  const float *bl = p.b_lstm[layer];
-                  float g[4];
-#pragma unroll
-                  for (int q = 0; q < 4; ++q) {
-                      const float r = zero ? 0.0f : ld_coh(p.rx + rx_off(p, cur, layer, b) + 4 * j + q);
-                      g[q] = (acc[q] + r) + bl[4 * j + q];
+                  const int k = (it - wave) / kWaves;
+                  float4 r, bias;
+                  float c_prev;
+                  if (k < kPre) {
+                      r = k == 0 ? pre_r[0] : pre_r[kPre - 1];
+                      bias = k == 0 ? pre_b[0] : pre_b[kPre - 1];
+                      c_prev = k == 0 ? pre_c[0] : pre_c[kPre - 1];
+                  } else {
+                      const bool zero = s.flags[ul] & kFlagZeroHC;
+                      bias = *reinterpret_cast<const float4 *>(p.b_lstm[layer] + 4 * j);
+                      r = zero ? make_float4(0.f, 0.f, 0.f, 0.f)
+                               : ld4_coh(B.rx, (unsigned)((rx_off(p, cur, layer, b) + 4 * j) * 4));
+                      c_prev = zero ? 0.0f : ld_coh(p.cx + hx_off(p, cur, layer, b) + j);
                   }
-                  const float c_prev = zero ? 0.0f : ld_coh(p.cx + hx_off(p, cur, layer, b) + j);
                   float c_new, h_new;
-                  cell(g[0], g[1], g[2], g[3], c_prev, c_new, h_new);
+                  cell((acc[0] + r.x) + bias.x, (acc[1] + r.y) + bias.y, (acc[2] + r.z) + bias.z,
+                       (acc[3] + r.w) + bias.w, c_prev, c_new, h_new);
                   st_coh(p.cx + hx_off(p, cur ^ 1, layer, b) + j, c_new);
                   st_coh(p.hx + hx_off(p, cur ^ 1, layer, b) + j, h_new);
               });
@@ -696,7 +788,7 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
 // layers 0 and 1); otherwise layer 0 is split by unit tiles and followed by a
 // barrier.  Each later phase stages one layer's full new output and runs the
 // tiles that consume it.
-__device__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned &epoch,
+__device__ __forceinline__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned &epoch,
                               unsigned long long &tlast) {
     const int H = p.H, L = p.L;
     const bool redundant = s.nl <= kSmallB && p.n_dom == 1;
@@ -740,7 +832,7 @@ __device__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bufs &B, const Lds
 
 // Apply the argmax results of iteration `stamp` to every utterance of the joint
 // list: src/parakeet_tdt.cpp:936-967 (TDT) and src/parakeet_eou.cpp:275-332 (EOU).
-__device__ void decide(const KParams &p, Ctl &s, unsigned stamp) {
+__device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp) {
     const unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * 2;
     for (int i = threadIdx.x; i < s.nj; i += kBlock) {
         const int ul = s.jst[i], b = s.b[ul];
@@ -848,7 +940,7 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
             q += (size_t)kTile * kp * 2 * 2;
         }
         S.red = reinterpret_cast<f32x4 *>(q);
-        q += (size_t)kWaves * kWave * sizeof(f32x4);
+        q += (size_t)p.red_slots * kWave * sizeof(f32x4);
         S.h0s = reinterpret_cast<float *>(q);
     }
 
