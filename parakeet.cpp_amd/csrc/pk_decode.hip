@@ -233,7 +233,8 @@ int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *
 struct pk_decoder {
     KParams kp{};              // weights + dims (batch fields filled per call)
     pk_decoder_desc desc{};    // host copy of the description (tensor pointers not kept)
-    const float *w_enc = nullptr, *b_enc = nullptr;   // joint.enc dense f32 [J][D], bias
+    const _Float16 *w_enc_hi = nullptr, *w_enc_lo = nullptr;   // joint.enc [J][D] as f16 hi + lo planes
+    const float *b_enc = nullptr;                               // joint.enc bias
     int n_slots = 0;
     int device = 0;
     int n_cu = 0, lds_block = 0;
@@ -369,8 +370,8 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     if (d->kind != PK_KIND_TDT && d->kind != PK_KIND_EOU) return fail(PK_ERR_ARG, "unknown decoder kind %d", d->kind);
     if (H <= 0 || J <= 0 || D <= 0 || L <= 0 || L > PK_MAX_LAYERS || d->vocab_size <= 0)
         return fail(PK_ERR_ARG, "bad dims H=%d L=%d J=%d D=%d V=%d", H, L, J, D, d->vocab_size);
-    if (H % 32 || J % 32 || D % 4)
-        return fail(PK_ERR_UNSUPPORTED, "pred_hidden and joint_hidden must be multiples of 32, d_enc of 4");
+    if (H % 32 || J % 32 || D % 32)
+        return fail(PK_ERR_UNSUPPORTED, "pred_hidden, joint_hidden and d_enc must be multiples of 32");
     if (d->kind == PK_KIND_TDT && (Dn <= 0 || Dn > PK_MAX_DURATIONS))
         return fail(PK_ERR_UNSUPPORTED, "TDT num_durations %d", Dn);
     if (d->kind == PK_KIND_TDT && d->n_duration_values > 0 && d->n_duration_values < Dn)
@@ -439,7 +440,13 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     ar.add(b_pred.data(), b_pred.size() * 4, reinterpret_cast<const void **>(&kp.b_pred));
     ar.add(b_out.data(), b_out.size() * 4, reinterpret_cast<const void **>(&kp.b_out));
     ar.add(b_enc.data(), b_enc.size() * 4, reinterpret_cast<const void **>(&dec->b_enc));
-    ar.add(w_enc.data(), w_enc.size() * 4, reinterpret_cast<const void **>(&dec->w_enc));
+    std::vector<_Float16> w_enc_hi(w_enc.size()), w_enc_lo(w_enc.size());
+    for (size_t i = 0; i < w_enc.size(); ++i) {
+        w_enc_hi[i] = (_Float16)w_enc[i];
+        w_enc_lo[i] = (_Float16)(w_enc[i] - (float)w_enc_hi[i]);
+    }
+    ar.add(w_enc_hi.data(), w_enc_hi.size() * 2, reinterpret_cast<const void **>(&dec->w_enc_hi));
+    ar.add(w_enc_lo.data(), w_enc_lo.size() * 2, reinterpret_cast<const void **>(&dec->w_enc_lo));
     if ((rc = ar.upload(dec->arena))) return cleanup(rc);
 
     // layer-0 input projection of every token: E'[v] = W_ih0 . embed[v] + b_ih0 + b_hh0 (f32)
@@ -661,6 +668,8 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         enc = dec->d_enc.as<float>();
         src_row = dst_row;
     }
+    if (rows > 0 && reinterpret_cast<uintptr_t>(enc) % 16 != 0)
+        return fail(PK_ERR_ARG, "encoder frames must be 16-byte aligned");
     const Plan pl = plan_domains(m, dec->nwg, T);
     const int nwg = pl.n_dom * pl.P;
     for (int d = 0; d < pl.n_dom; ++d)
@@ -696,9 +705,9 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     HIP_TRY(hipEventRecord(dec->ev[0], dec->stream));
     if (rows > 0) {
         if ((rc = dec->d_encp.ensure((size_t)rows * J * 4))) return rc;
-        dim3 grid((max_T + 63) / 64, m, (J + 63) / 64);
-        pkdev::enc_proj_kernel<<<grid, 256, 0, dec->stream>>>(dec->w_enc, J, dec->b_enc, enc, D, d_src, d_dst, d_T,
-                                                              dec->d_encp.as<float>());
+        dim3 grid((max_T + pkdev::kEpTile - 1) / pkdev::kEpTile, m, (J + pkdev::kEpTile - 1) / pkdev::kEpTile);
+        pkdev::enc_proj_kernel<<<grid, 256, 0, dec->stream>>>(dec->w_enc_hi, dec->w_enc_lo, J, dec->b_enc, enc, D,
+                                                              d_src, d_dst, d_T, dec->d_encp.as<float>());
         HIP_TRY(hipGetLastError());
     }
     HIP_TRY(hipEventRecord(dec->ev[1], dec->stream));

@@ -232,53 +232,84 @@ __global__ void __launch_bounds__(256) embed_proj_kernel(const float *__restrict
 
 // ---------------------------------------------------------------- enc_proj
 
-// encp[rows of utterance u] = b_e + W_e . enc[row]  (f32), 64x64 tiles, K step 32.
-// W is dense f32 [J][D] (dequantised at load from the stored bytes).
-__global__ void __launch_bounds__(256) enc_proj_kernel(const float *__restrict w, int J, const float *__restrict bias,
+// encp[rows of utterance u] = b_e + W_e . enc[row] for every frame: an MFMA
+// GEMM with f32 accuracy.  Frames (f32) are split into f16 hi + lo when staged
+// in LDS; W_e arrives as f16 hi / lo planes [J][D] (split once at load).
+// Each 16x16 output tile takes hi.hi + lo.hi + hi.lo (the lo.lo term is below
+// f32 rounding).  Workgroup: 64 frames x 64 outputs, 4 waves of 16 frames;
+// K steps of 32.  d_enc % 32 == 0.
+constexpr int kEpTile = 64, kEpK = 32, kEpStride = kEpK + 8;   // LDS row stride in halves
+__global__ void __launch_bounds__(256) enc_proj_kernel(const _Float16 *__restrict whi, const _Float16 *__restrict wlo,
+                                                       int J, const float *__restrict bias,
                                                        const float *__restrict enc, int d_enc,
                                                        const long long *__restrict src_row,
                                                        const long long *__restrict dst_row,
                                                        const int *__restrict T, float *__restrict out) {
+    __shared__ __attribute__((aligned(16))) _Float16 ah[kEpTile * kEpStride], al[kEpTile * kEpStride];
+    __shared__ __attribute__((aligned(16))) _Float16 bh[kEpTile * kEpStride], bl[kEpTile * kEpStride];
     const int u = blockIdx.y;
     const int Tu = T[u];
-    const int m0 = blockIdx.x * 64;
+    const int m0 = blockIdx.x * kEpTile;
     if (m0 >= Tu) return;
-    const int n0 = blockIdx.z * 64;
-    __shared__ float xs[32][65];
-    __shared__ float ws[32][65];
-    const int tid = threadIdx.x;
-    const int tr = tid / 16, tc = tid % 16;     // 16x16 threads, 4x4 outputs each
-    float acc[4][4] = {};
+    const int n0 = blockIdx.z * kEpTile;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const float *src = enc + (size_t)src_row[u] * d_enc;
-    for (int k0 = 0; k0 < d_enc; k0 += 32) {
-        for (int i = tid; i < 64 * 32; i += 256) {
-            const int r = i / 32, k = i % 32;
-            const int m = m0 + r, n = n0 + r;
-            xs[k][r] = (m < Tu && k0 + k < d_enc) ? src[(size_t)m * d_enc + k0 + k] : 0.0f;
-            ws[k][r] = (n < J && k0 + k < d_enc) ? w[(size_t)n * d_enc + k0 + k] : 0.0f;
+    const int sr = tid / 4, sc = (tid % 4) * 8;   // staging: row / column of this thread's 8 values
+    f32x4 acc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < d_enc; k0 += kEpK) {
+        {
+            const int row = m0 + sr;
+            float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+            if (row < Tu) {
+                v0 = *reinterpret_cast<const float4 *>(src + (size_t)row * d_enc + k0 + sc);
+                v1 = *reinterpret_cast<const float4 *>(src + (size_t)row * d_enc + k0 + sc + 4);
+            }
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            half8 h, l;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                h[i] = (_Float16)v[i];
+                l[i] = (_Float16)(v[i] - (float)h[i]);
+            }
+            *reinterpret_cast<half8 *>(ah + sr * kEpStride + sc) = h;
+            *reinterpret_cast<half8 *>(al + sr * kEpStride + sc) = l;
+            const int j = n0 + sr;
+            half8 wh = half8{}, wl = half8{};
+            if (j < J) {
+                wh = *reinterpret_cast<const half8 *>(whi + (size_t)j * d_enc + k0 + sc);
+                wl = *reinterpret_cast<const half8 *>(wlo + (size_t)j * d_enc + k0 + sc);
+            }
+            *reinterpret_cast<half8 *>(bh + sr * kEpStride + sc) = wh;
+            *reinterpret_cast<half8 *>(bl + sr * kEpStride + sc) = wl;
         }
         __syncthreads();
-#pragma unroll 8
-        for (int k = 0; k < 32; ++k) {
-            float a[4], b[4];
+        const int ao = (wave * 16 + (lane & 15)) * kEpStride + (lane >> 4) * 8;
+        const half8 a_h = *reinterpret_cast<const half8 *>(ah + ao);
+        const half8 a_l = *reinterpret_cast<const half8 *>(al + ao);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) { a[i] = xs[k][tr * 4 + i]; b[i] = ws[k][tc * 4 + i]; }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        for (int t = 0; t < 4; ++t) {
+            const int bo = (t * 16 + (lane & 15)) * kEpStride + (lane >> 4) * 8;
+            const half8 b_h = *reinterpret_cast<const half8 *>(bh + bo);
+            const half8 b_l = *reinterpret_cast<const half8 *>(bl + bo);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, b_h, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_l, b_h, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_h, b_l, acc[t], 0, 0, 0);
         }
         __syncthreads();
     }
+    // D fragment: lane holds output column 16t + lane % 16 of frames 4 (lane / 16) .. +3
     float *dst = out + (size_t)dst_row[u] * J;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = m0 + tr * 4 + i;
-        if (m >= Tu) continue;
+    for (int t = 0; t < 4; ++t) {
+        const int col = n0 + t * 16 + (lane & 15);
+        if (col >= J) continue;
+        const float bc = bias[col];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = n0 + tc * 4 + j;
-            if (n < J) dst[(size_t)m * J + n] = bias[n] + acc[i][j];
+        for (int i = 0; i < 4; ++i) {
+            const int row = m0 + wave * 16 + (lane >> 4) * 4 + i;
+            if (row < Tu) dst[(size_t)row * J + col] = acc[t][i] + bc;
         }
     }
 }
