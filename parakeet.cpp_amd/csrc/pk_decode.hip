@@ -504,7 +504,7 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     // decode-loop launch shape: one workgroup per CU; LDS = activation blocks
     // [hidden | h_0 .. h_{L-1}] of one 16-utterance tile + K-split partials +
     // the redundant layer-0 output
-    const size_t act = (size_t)kTile * ((J + kKPad) + (size_t)(H + kKPad)) * 2 * 2;
+    const size_t act = (size_t)kTile * (std::max(J, H) + kKPad) * 2 * 2;   // shared by the joint and LSTM phases
     if (std::max(J, H) > 4096)
         return cleanup(fail(PK_ERR_UNSUPPORTED, "hidden sizes above 4096"));
     dec->lds_fixed = act + (size_t)kSmallB * H * 4;
@@ -782,10 +782,30 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
             most = std::max(most, items(l + 1 < p.L ? p.w_ih[l + 1] : p.w_pred) + items(p.w_hh[l]));
         p.red_slots = most + kWaves;
     }
-    const size_t lds = dec->lds_fixed + (size_t)p.red_slots * kWave * 16;
+    size_t lds = dec->lds_fixed + (size_t)p.red_slots * kWave * 16;
     if (lds > dec->lds_bytes)
         return fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed for %d workgroups per domain, %zu available", lds, pl.P,
                     dec->lds_bytes);
+    // LDS weight cache: when every workgroup's tiles of all step matrices fit,
+    // they are copied into LDS once per launch and read from there
+    {
+        std::vector<pkdev::TMat *> mats;
+        for (int l = 1; l < p.L; ++l) mats.push_back(&p.w_ih[l]);
+        for (int l = 0; l < p.L; ++l) mats.push_back(&p.w_hh[l]);
+        mats.push_back(&p.w_pred);
+        mats.push_back(&p.w_out);
+        size_t cache = 0;
+        for (auto *m : mats)
+            cache += (size_t)((m->tiles + pl.P - 1) / pl.P) * m->KB * pkdev::cache_block_bytes(m->type);
+        const bool fits = lds + cache <= dec->lds_bytes;
+        size_t off = 0;
+        for (auto *m : mats) {
+            m->lds_off = fits ? (int)off : -1;
+            off += (size_t)((m->tiles + pl.P - 1) / pl.P) * m->KB * pkdev::cache_block_bytes(m->type);
+        }
+        p.wcache_bytes = fits ? (int)cache : 0;
+        if (fits) lds += cache;
+    }
     void *args[] = {&p};
     HIP_TRY(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(pkdev::decode_loop_kernel), dim3(nwg),
                                        dim3(kBlock), args, lds, dec->stream));

@@ -49,7 +49,14 @@ struct TMat {
     const unsigned short *scale;   // q8_0 block scales, f16 bits
     int type;                      // PK_TYPE_Q8_0, PK_TYPE_F16, PK_TYPE_F32
     int rows, tiles, KB;
+    int lds_off;                   // byte offset of this workgroup's tiles in its LDS weight cache, -1: not cached
 };
+
+// Bytes of one cached K block: q8_0 fragment (512) + its 16 scales (32); f16
+// fragment; f32 hi then lo fragment.
+__host__ __device__ constexpr int cache_block_bytes(int type) {
+    return type == PK_TYPE_Q8_0 ? 544 : type == PK_TYPE_F16 ? 1024 : 2048;
+}
 
 struct KParams {
     int kind, H, L, J, V1, Dn, Vo, blank, eou, eob, max_sym, n_dur;
@@ -97,6 +104,7 @@ struct KParams {
     int *status;                 // [0] error code, [1] iterations, [2] overflow, [3] trace overflow
     int max_iter;
     int red_slots;               // LDS partial slots: items of the largest phase + kWaves
+    int wcache_bytes;            // LDS weight cache per workgroup (0: weights are read from L2)
     unsigned long long *prof;    // nullable: per-phase wall-clock totals of workgroup 0 (100 MHz ticks)
 };
 
@@ -183,11 +191,17 @@ __device__ __forceinline__ int key_index(unsigned long long key) {
 }
 __device__ __forceinline__ unsigned key_stamp(unsigned long long key) { return (unsigned)(key >> kStampShift); }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+// Gate nonlinearities from the hardware base-2 exponential (v_exp_f32) and
+// reciprocal (v_rcp_f32), each within about 1 ulp: sigmoid(x) = 1 / (1 + e^-x),
+// tanh(x) = 2 sigmoid(2x) - 1.  Absolute error stays below ~1e-7, far inside
+// the state tolerance, and saturates correctly for large |x| (e^-x -> inf / 0).
+__device__ __forceinline__ float exp_fast(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+__device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.0f + exp_fast(-x)); }
+__device__ __forceinline__ float tanh_fast(float x) { return 2.0f * sigmoidf_(2.0f * x) - 1.0f; }
 
 __device__ __forceinline__ void cell(float gi, float gf, float gg, float go, float c_prev, float &c_new, float &h_new) {
-    c_new = sigmoidf_(gf) * c_prev + sigmoidf_(gi) * tanhf(gg);
-    h_new = sigmoidf_(go) * tanhf(c_new);
+    c_new = sigmoidf_(gf) * c_prev + sigmoidf_(gi) * tanh_fast(gg);
+    h_new = sigmoidf_(go) * tanh_fast(c_new);
 }
 
 // ---------------------------------------------------------------- prepare-time kernels
@@ -442,14 +456,36 @@ __device__ __forceinline__ void stage_act(const Act &x, int K, int n, __amdgpu_b
 // (item, wave) in LDS slot item + wave; phase_reduce sums each item's partials
 // in wave order -- a fixed order, so results do not depend on timing.
 
-constexpr int kUnit = 10;  // K blocks per unit
+constexpr int kUnit = 5;   // K blocks per unit
 
 // Fragments of one unit: blocks sb0 .. sb0+nb-1 of one tile; blocks past nb
 // read as zero (buffer loads past the range return 0).
 template <bool Q8>
-__device__ __forceinline__ void unit_load(const TMat &m, bool two, int tile, int sb0, int nb, int lane,
-                                          uint4 (&f)[kUnit]) {
+__device__ __forceinline__ void unit_load(const TMat &m, bool two, int tile, int li, const unsigned char *wc, int sb0,
+                                          int nb, int lane, uint4 (&f)[kUnit]) {
     const unsigned bad = 0x80000000u;
+    if (wc != nullptr && m.lds_off >= 0) {   // this workgroup's tiles are cached in LDS (local index li)
+        const unsigned char *base = wc + m.lds_off;
+#pragma unroll
+        for (int j = 0; j < kUnit; ++j) {
+            const bool ok = j < nb;
+            const int sb = ok ? sb0 + j : sb0;
+            uint4 v;
+            if (Q8) {
+                const unsigned char *blk = base + ((size_t)li * m.KB + sb) * 544;
+                const uint2 q = *reinterpret_cast<const uint2 *>(blk + lane * 8);
+                const uint2 d = *reinterpret_cast<const uint2 *>(blk + 512 + (lane >> 4) * 8);
+                v = make_uint4(q.x, q.y, d.x, d.y);
+            } else {
+                const int kb = two ? sb >> 1 : sb;
+                const int plane = two ? (sb & 1) : 0;
+                v = *reinterpret_cast<const uint4 *>(base + (((size_t)li * m.KB + kb) * (two ? 2 : 1) + plane) * 1024 +
+                                                     lane * 16);
+            }
+            f[j] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
+        return;
+    }
     if (Q8) {
         const __amdgpu_buffer_rsrc_t rq = rsrc(m.a, (unsigned)m.tiles * m.KB * kWave * 8u);
         const __amdgpu_buffer_rsrc_t rs = rsrc(m.scale, (unsigned)m.tiles * m.KB * kTile * 2u);
@@ -517,7 +553,7 @@ __device__ __forceinline__ int blocks_per_item(const TMat &m) { return m.type ==
 
 template <bool Q8>
 __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
-                                               const Act &x, f32x4 *red) {
+                                               const Act &x, f32x4 *red, const unsigned char *wc) {
     // wave-uniform unit bookkeeping: the weight buffer descriptors stay in SGPRs
     const int lane = threadIdx.x & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const bool two = !Q8 && A.type == PK_TYPE_F32;
@@ -535,7 +571,8 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
     };
     auto fetch = [&](int item, int sb0, int nb, uint4 (&f)[kUnit]) {
         const bool in_a = item < n_a;
-        unit_load<Q8>(in_a ? A : Bm, two, rank + (in_a ? item : item - n_a) * P, sb0, nb, lane, f);
+        const int li = in_a ? item : item - n_a;
+        unit_load<Q8>(in_a ? A : Bm, two, rank + li * P, li, wc, sb0, nb, lane, f);
     };
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int u = c0; u < c1; ++u) {
@@ -572,10 +609,10 @@ __device__ __forceinline__ void phase_reduce(int n_items, int S, const f32x4 *re
 // Products of one phase for this workgroup, then the epilogue per item.
 template <class EpiFn>
 __device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
-                                          const Act &x, f32x4 *red, EpiFn epi) {
+                                          const Act &x, f32x4 *red, const unsigned char *wc, EpiFn epi) {
     if (n_items <= 0) return;
-    if (A.type == PK_TYPE_Q8_0) phase_partials<true>(A, n_a, Bm, n_items, rank, P, x, red);
-    else phase_partials<false>(A, n_a, Bm, n_items, rank, P, x, red);
+    if (A.type == PK_TYPE_Q8_0) phase_partials<true>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+    else phase_partials<false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
     const int KBe = A.type == PK_TYPE_F32 ? 2 * A.KB : A.KB;
     phase_reduce(n_items, (KBe + kUnit - 1) / kUnit, red, epi);
 }
@@ -587,7 +624,32 @@ struct Lds {
     Act act[1 + PK_MAX_LAYERS];   // staged activation blocks
     f32x4 *red;                   // [red_slots][kWave] per-(item, wave) partials
     float *h0s;                   // [kSmallB][H] layer-0 output in redundant mode
+    const unsigned char *wcache;  // weight cache (nullptr when the tiles do not fit)
 };
+
+// Copy this workgroup's tiles of m (rank, rank+P, ...) into its LDS cache:
+// per K block the fragment, then (q8_0) the 16 block scales.
+__device__ __forceinline__ void cache_matrix(const TMat &m, int rank, int P, unsigned char *wc) {
+    if (m.lds_off < 0) return;
+    const int n = owned(m.tiles, rank, P);
+    const int bpb = cache_block_bytes(m.type), chunks = bpb / 16;
+    const size_t nchunk = (size_t)n * m.KB * chunks;
+    for (size_t c = threadIdx.x; c < nchunk; c += kBlock) {
+        const int ch = (int)(c % chunks);
+        const size_t blk = c / chunks;                      // local tile * KB + kb
+        const int li = (int)(blk / m.KB), kb = (int)(blk % m.KB);
+        const size_t f = (size_t)(rank + li * P) * m.KB + kb;   // global fragment index
+        const unsigned char *src;
+        if (m.type == PK_TYPE_Q8_0)
+            src = ch < 32 ? static_cast<const unsigned char *>(m.a) + f * 512 + ch * 16
+                          : reinterpret_cast<const unsigned char *>(m.scale) + f * 32 + (ch - 32) * 16;
+        else if (m.type == PK_TYPE_F16)
+            src = static_cast<const unsigned char *>(m.a) + f * 1024 + ch * 16;
+        else
+            src = static_cast<const unsigned char *>(ch < 64 ? m.a : m.a_lo) + f * 1024 + (ch % 64) * 16;
+        *reinterpret_cast<uint4 *>(wc + m.lds_off + blk * bpb + ch * 16) = *reinterpret_cast<const uint4 *>(src);
+    }
+}
 
 // Joint + argmax for this workgroup's output tiles.  Utterances are processed
 // 16 at a time (one MFMA column tile).
@@ -647,7 +709,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         // each lane keeps its best key per head over all its rows; lanes of one
         // column then combine, and one LDS atomic per column and head follows
         unsigned long long best0 = 0ull, best1 = 0ull;
-        run_phase(p.w_out, n_out, p.w_out, n_out, s.rank, s.P, x, S.red,
+        run_phase(p.w_out, n_out, p.w_out, n_out, s.rank, s.P, x, S.red, S.wcache,
                   [&](int k, f32x4 acc) {
                       if (u >= nc) return;
                       const int tile = s.rank + k * s.P;
@@ -758,7 +820,15 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
         pre_r[k] = pre_b[k] = make_float4(0.f, 0.f, 0.f, 0.f);
         pre_c[k] = 0.0f;
         const int it = wave + k * kWaves, u = lane & 15;
-        if (last || it >= n_c || u >= nc) continue;
+        if (it >= n_c || u >= nc) continue;
+        if (last) {                               // pred projection: the bias rows only
+            const int row0 = (s.rank + it * s.P) * kTile + (lane >> 4) * 4;
+            pre_b[k].x = row0 < p.J ? p.b_pred[row0] : 0.0f;
+            pre_b[k].y = row0 + 1 < p.J ? p.b_pred[row0 + 1] : 0.0f;
+            pre_b[k].z = row0 + 2 < p.J ? p.b_pred[row0 + 2] : 0.0f;
+            pre_b[k].w = row0 + 3 < p.J ? p.b_pred[row0 + 3] : 0.0f;
+            continue;
+        }
         const int j = (s.rank + it * s.P) * 4 + (lane >> 4);
         if (j >= H) continue;
         const int ul = s.lst[c0 + u], b = s.b[ul], cur = s.cur[ul];
@@ -767,7 +837,7 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
         pre_r[k] = ld4_coh(B.rx, (unsigned)((rx_off(p, cur, layer, b) + 4 * j) * 4));
         pre_c[k] = ld_coh(p.cx + hx_off(p, cur, layer, b) + j);
     }
-    run_phase(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red,
+    run_phase(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache,
               [&](int it, f32x4 acc) {
                   const int u = lane & 15;
                   if (u >= nc) return;
@@ -782,10 +852,14 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
                   }
                   const int tile = s.rank + it * s.P;
                   if (last) {               // pred projection
+                      const int kk = (it - wave) / kWaves;
+                      const float4 pb = kk == 0 ? pre_b[0] : pre_b[kPre - 1];
+                      const float bias[4] = {pb.x, pb.y, pb.z, pb.w};
 #pragma unroll
                       for (int i = 0; i < 4; ++i) {
                           const int row = tile * kTile + (lane >> 4) * 4 + i;
-                          if (row < p.J) st_coh(p.ppx + (size_t)b * p.J + row, p.b_pred[row] + acc[i]);
+                          if (row < p.J)
+                              st_coh(p.ppx + (size_t)b * p.J + row, (kk < kPre ? bias[i] : p.b_pred[row]) + acc[i]);
                       }
                       return;
                   }
@@ -958,21 +1032,27 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
     B.ppx = rsrc(p.ppx, (unsigned)((size_t)n_all * J * 4));
     B.rx = rsrc(p.rx, (unsigned)((size_t)2 * L * n_all * 4 * H * 4));
 
-    // LDS: activation blocks [hidden | h_0 .. h_{L-1}], then K-split partials
+    // LDS: one activation block (the joint's hidden block and the LSTM phases'
+    // block are never live together), per-(item, wave) partials, the redundant
+    // layer-0 output, then the weight cache
     Lds S;
+    unsigned char *wcache = nullptr;
     {
         unsigned char *q = lds_raw;
-        for (int a = 0; a <= 1; ++a) {      // [hidden | one layer output]
+        for (int a = 0; a <= 1; ++a) {
             const int K = a == 0 ? J : H;
             const int kp = K + kKPad;
             S.act[a].hi = reinterpret_cast<_Float16 *>(q);
             S.act[a].lo = S.act[a].hi + kTile * kp;
             S.act[a].kp = kp;
-            q += (size_t)kTile * kp * 2 * 2;
         }
+        q += (size_t)kTile * ((J > H ? J : H) + kKPad) * 2 * 2;
         S.red = reinterpret_cast<f32x4 *>(q);
         q += (size_t)p.red_slots * kWave * sizeof(f32x4);
         S.h0s = reinterpret_cast<float *>(q);
+        q += (size_t)kSmallB * H * 4;
+        if (p.wcache_bytes > 0) wcache = q;
+        S.wcache = wcache;
     }
 
     if (threadIdx.x < kPrN) s.prof[threadIdx.x] = 0ull;
@@ -1018,6 +1098,12 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
             const int l = i / (4 * H), k = i - l * 4 * H;
             st_coh(p.rx + rx_off(p, 0, l, b) + k, p.slot_r[(size_t)slot * L * 4 * H + i]);
         }
+    }
+    if (wcache) {      // this workgroup's weight tiles, read from LDS for the whole launch
+        for (int l = 1; l < L; ++l) cache_matrix(p.w_ih[l], s.rank, s.P, wcache);
+        for (int l = 0; l < L; ++l) cache_matrix(p.w_hh[l], s.rank, s.P, wcache);
+        cache_matrix(p.w_pred, s.rank, s.P, wcache);
+        cache_matrix(p.w_out, s.rank, s.P, wcache);
     }
     build_lists(s);
     bool ok = dom_sync(p, s, epoch);
