@@ -750,7 +750,10 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     p.wg_dom = d_wg_dom;
     p.wg_rank = d_wg_rank;
     p.dom_wg = d_dom_wg;
-    const size_t keys_bytes = (size_t)2 * m * 2 * 8;
+    // argmax shards: about 8 ranks per shard
+    p.shards = 1;
+    while (p.shards < pkdev::kShards && p.shards * 8 < pl.P) p.shards *= 2;
+    const size_t keys_bytes = (size_t)2 * m * p.shards * 2 * 8;
     if ((rc = dec->d_keys.ensure(keys_bytes))) return rc;
     if ((rc = dec->d_sync.ensure(64))) return rc;
     if ((rc = dec->d_flags.ensure((size_t)nwg * kFlagStride * 4))) return rc;

@@ -24,6 +24,7 @@ constexpr int kIdxBits = 14;                // argmax key: index field
 constexpr int kStampShift = 46;             // argmax key: 14 index + 32 value bits below the stamp
 constexpr unsigned kMaxStamp = (1u << 18) - 1;
 constexpr int kFlagStride = 64;             // words between barrier flags (256 B)
+constexpr int kShards = 32;                 // argmax keys: most max targets per utterance and head
 constexpr int kKPad = 8;                    // halves of padding per staged row (bank spread)
 
 // Flags in the per-utterance control word.
@@ -100,7 +101,8 @@ struct KParams {
     const int *dom_wg;           // [n_dom][dom_size] workgroup of each rank
     // sync
     unsigned *flags;             // [nwg * kFlagStride]
-    unsigned long long *keys;    // [2][n_utts][2] best keys, by iteration parity
+    unsigned long long *keys;    // [2][n_utts][shards][2] best keys, by iteration parity
+    int shards;                  // power of two <= kShards: ranks per shard ~ 8
     int *status;                 // [0] error code, [1] iterations, [2] overflow, [3] trace overflow
     int max_iter;
     int red_slots;               // LDS partial slots: items of the largest phase + kWaves
@@ -745,14 +747,15 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         __syncthreads();
         pmark(p, s, tlast, kPrJCompute);
     }
-    // one device-scope max per utterance and head: the stamp keeps keys of
-    // iteration `stamp` above every older key in the same parity buffer
-    unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * 2;
+    // one device-scope max per utterance and head into shard rank % kShards
+    // (spreads the atomics of many workgroups over several words); the stamp
+    // keeps keys of iteration `stamp` above every older key in the same parity
+    unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * p.shards * 2;
     if (threadIdx.x < 2 * s.nj) {
         const int u = threadIdx.x / 2, head = threadIdx.x % 2;
         const unsigned long long k = s.wgkey[u][head];
         if (k != 0ull)
-            __hip_atomic_fetch_max(&keys[(size_t)s.b[s.jst[u]] * 2 + head],
+            __hip_atomic_fetch_max(&keys[((size_t)s.b[s.jst[u]] * p.shards + s.rank % p.shards) * 2 + head],
                                    ((unsigned long long)stamp << kStampShift) | k, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -937,13 +940,41 @@ __device__ __forceinline__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bu
 
 // Apply the argmax results of iteration `stamp` to every utterance of the joint
 // list: src/parakeet_tdt.cpp:936-967 (TDT) and src/parakeet_eou.cpp:275-332 (EOU).
+// The domain's best key per joint utterance and head: the maximum over the
+// shards that carry this iteration's stamp (shards no rank wrote this
+// iteration hold older stamps and are skipped).  Lane groups of p.shards
+// reduce one (utterance, head) with shuffles; results go to s.wgkey.
+__device__ __forceinline__ void gather_shards(const KParams &p, Ctl &s, unsigned stamp) {
+    const int G = p.shards;
+    const unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * G * 2;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int n = s.nj * 2 * G;
+    for (int e0 = 0; e0 < n; e0 += kBlock) {      // e = (pair, shard); whole waves stay together
+        const int e = e0 + threadIdx.x;
+        unsigned long long k = 0ull;
+        if (e < n) {
+            const int pair = e / G, sh = e - pair * G;
+            const int b = s.b[s.jst[pair >> 1]];
+            k = __hip_atomic_load(&keys[((size_t)b * G + sh) * 2 + (pair & 1)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (key_stamp(k) != stamp) k = 0ull;
+        }
+        for (int m = 1; m < G; m <<= 1) {
+            const unsigned long long o = __shfl_xor(k, m, kWave);
+            k = o > k ? o : k;
+        }
+        if (e < n && (lane & (G - 1)) == 0) {
+            const int pair = e / G;
+            s.wgkey[pair >> 1][pair & 1] = k;
+        }
+    }
+    __syncthreads();
+}
+
 __device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp) {
-    const unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * 2;
+    gather_shards(p, s, stamp);
     for (int i = threadIdx.x; i < s.nj; i += kBlock) {
         const int ul = s.jst[i], b = s.b[ul];
-        const unsigned long long kt = __hip_atomic_load(&keys[(size_t)b * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned long long kd =
-            __hip_atomic_load(&keys[(size_t)b * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long kt = s.wgkey[i][0], kd = s.wgkey[i][1];
         if (key_stamp(kt) != stamp || (p.Dn > 0 && key_stamp(kd) != stamp)) {
             __hip_atomic_store(p.status, PK_ERR_DEVICE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             s.t[ul] = s.T[ul];
