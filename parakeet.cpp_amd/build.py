@@ -33,7 +33,9 @@ def _run(cmd):
 
 def build_hip():
     out = os.path.join(HERE, "libparakeet_hip.so")
-    _run([HIPCC, *HIP_FLAGS, "-shared", os.path.join(CSRC, "pk_decode.hip"), "-o", out + ".tmp"])
+    # PK_TIMELINE=1 compiles the decode loop's per-wave checkpoint timeline (profiling builds only)
+    extra = ["-DPK_TIMELINE"] if os.environ.get("PK_TIMELINE") else []
+    _run([HIPCC, *HIP_FLAGS, *extra, "-shared", os.path.join(CSRC, "pk_decode.hip"), "-o", out + ".tmp"])
     os.replace(out + ".tmp", out)
     return out
 

@@ -508,9 +508,14 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     if (std::max(J, H) > 4096)
         return cleanup(fail(PK_ERR_UNSUPPORTED, "hidden sizes above 4096"));
     dec->lds_fixed = act + (size_t)kSmallB * H * 4;
-    const size_t need = (size_t)dec->lds_block - sizeof(pkdev::Ctl) - 512;   // upper bound of any launch
+    // dynamic LDS bound of any launch: the block's LDS less the kernel's static LDS
+    hipFuncAttributes fa{};
+    if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(pkdev::decode_loop_kernel)) != hipSuccess)
+        return cleanup(fail(PK_ERR_DEVICE, "hipFuncGetAttributes"));
+    const size_t stat = fa.sharedSizeBytes;
+    const size_t need = (size_t)dec->lds_block > stat ? (size_t)dec->lds_block - stat : 0;
     if (dec->lds_fixed + (size_t)2 * kWaves * kWave * 16 > need)
-        return cleanup(fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed, %d available", dec->lds_fixed + sizeof(pkdev::Ctl),
+        return cleanup(fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed, %d available", dec->lds_fixed + stat,
                             dec->lds_block));
     dec->lds_bytes = need;
     if (hipFuncSetAttribute(reinterpret_cast<const void *>(pkdev::decode_loop_kernel),
@@ -773,8 +778,8 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     const bool prof = getenv("PK_PROFILE_PHASES") != nullptr;
     p.prof = nullptr;
     if (prof) {
-        if ((rc = dec->d_prof.ensure(pkdev::kPrN * 8))) return rc;
-        HIP_TRY(hipMemsetAsync(dec->d_prof.p, 0, pkdev::kPrN * 8, dec->stream));
+        if ((rc = dec->d_prof.ensure((pkdev::kPrN + 9 * pkdev::kTl) * 8))) return rc;
+        HIP_TRY(hipMemsetAsync(dec->d_prof.p, 0, (pkdev::kPrN + 9 * pkdev::kTl) * 8, dec->stream));
         p.prof = dec->d_prof.as<unsigned long long>();
     }
     // LDS partial slots: the most items any phase gives one workgroup, plus one per wave
@@ -859,6 +864,15 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         for (int i = 0; i < pkdev::kPrN; ++i)
             fprintf(stderr, " %s=%.2fus", names[i], status[1] ? t[i] * 1e-2 / status[1] : 0.0);
         fprintf(stderr, "\n");
+        unsigned long long tl[9 * pkdev::kTl];
+        HIP_TRY(hipMemcpy(tl, dec->d_prof.as<unsigned long long>() + pkdev::kPrN, sizeof tl, hipMemcpyDeviceToHost));
+        for (int k = 0; k < pkdev::kTl; ++k) {
+            const unsigned long long cnt = tl[8 * pkdev::kTl + k];
+            if (!cnt) continue;
+            fprintf(stderr, "[pk tl] %2d n=%4llu", k, cnt);
+            for (int w = 0; w < 8; ++w) fprintf(stderr, " %6.2f", tl[w * pkdev::kTl + k] * 1e-2 / cnt);
+            fprintf(stderr, "\n");
+        }
     }
     if (status[0]) return fail(status[0], "device decode failed (status %d)", status[0]);
     if (status[2]) return fail(PK_ERR_OVERFLOW, "token or segment capacity exceeded");

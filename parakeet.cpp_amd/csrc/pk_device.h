@@ -141,6 +141,18 @@ __device__ __forceinline__ void st_coh(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Workgroup barrier for LDS traffic only: each wave waits for its own LDS
+// operations (lgkmcnt 0) but not for its global loads and stores, which stay
+// in flight across it (s_barrier carries no implicit wait on gfx950).  Every
+// exchange between workgroups goes through dom_sync, which drains them.  The
+// signal fences keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_sync() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // gfx9 encoding: lgkmcnt(0), vmcnt and expcnt unconstrained
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // ---------------------------------------------------------------- MFMA tiles
 
 // 8 int8 (two dwords) -> 8 exact f16: byte q ^ 0x80 = q + 128 becomes the low
@@ -337,6 +349,8 @@ struct Ctl {                      // per-workgroup copy of its domain's control 
     int t[kDomCap], T[kDomCap], sym[kDomCap], pend[kDomCap], flags[kDomCap];
     int ntok[kDomCap], steps[kDomCap], nseg[kDomCap], segst[kDomCap], last[kDomCap], cur[kDomCap];
     int lst[kDomCap], jst[kDomCap];
+    long long erow[kDomCap];      // first encp row of each utterance
+    float bbias[kDomCap];         // blank logit offset of each utterance
     int n, nl, nj;
     int dom, rank, P;
     unsigned long long wgkey[kDomCap][2];   // this workgroup's best key per utterance and head
@@ -345,13 +359,35 @@ struct Ctl {                      // per-workgroup copy of its domain's control 
 
 __device__ __forceinline__ void pmark(const KParams &p, Ctl &s, unsigned long long &last, int k) {
     if (!p.prof) return;
-    __syncthreads();
+    lds_sync();
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         const unsigned long long now = __builtin_amdgcn_s_memrealtime();
         s.prof[k] += now - last;
         last = now;
     }
 }
+
+// Checkpoint timeline (built with -DPK_TIMELINE, read with PK_PROFILE_PHASES=1):
+// workgroup 0 sums, per wave and checkpoint, the time since the start of the
+// iteration over iterations 40 .. 295; the host prints the per-wave means.
+// TL(k) is relative to the phase base set by TLBASE, TLA(k) absolute.  The
+// checkpoints add LDS traffic and waits of their own, so their times are
+// upper bounds.
+constexpr int kTl = 32;
+#ifdef PK_TIMELINE
+__device__ __forceinline__ unsigned long long *tl_sum() { __shared__ unsigned long long b[kWaves * kTl]; return b; }
+__device__ __forceinline__ int *tl_ctl() { __shared__ int c[2 + kTl]; return c; }
+__device__ __forceinline__ unsigned long long *tl_t0() { __shared__ unsigned long long t; return &t; }
+#define TLX(k, rel) do { int *c_ = tl_ctl(); if (c_[0]) { const int w_ = threadIdx.x >> 6; \
+    if ((threadIdx.x & 63) == 0) { const int kk_ = ((rel) ? c_[1] : 0) + (k); \
+    tl_sum()[w_ * kTl + kk_] += __builtin_amdgcn_s_memrealtime() - *tl_t0(); if (w_ == 0) c_[2 + kk_]++; } } } while (0)
+#define TLBASE(b) do { if (threadIdx.x == 0) tl_ctl()[1] = (b); } while (0)
+#else
+#define TLX(k, rel) do { } while (0)
+#define TLBASE(b) do { } while (0)
+#endif
+#define TL(k) TLX(k, 1)
+#define TLA(k) TLX(k, 0)
 
 // Compact the LSTM list (pending token) and the joint list (frames left).
 __device__ __forceinline__ void build_lists(Ctl &s) {
@@ -368,7 +404,7 @@ __device__ __forceinline__ void build_lists(Ctl &s) {
             s.nj = __popcll(bj);
         }
     }
-    __syncthreads();
+    lds_sync();
 }
 
 // Domain barrier: every member publishes its epoch in its own flag word and
@@ -462,11 +498,23 @@ constexpr int kUnit = 5;   // K blocks per unit
 
 // Fragments of one unit: blocks sb0 .. sb0+nb-1 of one tile; blocks past nb
 // read as zero (buffer loads past the range return 0).
-template <bool Q8>
-__device__ __forceinline__ void unit_load(const TMat &m, bool two, int tile, int li, const unsigned char *wc, int sb0,
+// The fields of a TMat that the unit loop reads, held in registers.
+struct WView {
+    const void *a, *a_lo;
+    const unsigned short *scale;
+    int tiles, KB, lds_off;
+};
+__device__ __forceinline__ WView wview(const TMat &m) { return WView{m.a, m.a_lo, m.scale, m.tiles, m.KB, m.lds_off}; }
+__device__ __forceinline__ WView pick(bool first, const WView &x, const WView &y) {
+    return WView{first ? x.a : y.a, first ? x.a_lo : y.a_lo, first ? x.scale : y.scale,
+                 first ? x.tiles : y.tiles, first ? x.KB : y.KB, first ? x.lds_off : y.lds_off};
+}
+
+template <bool Q8, bool CACHED>
+__device__ __forceinline__ void unit_load(const WView m, bool two, int tile, int li, const unsigned char *wc, int sb0,
                                           int nb, int lane, uint4 (&f)[kUnit]) {
     const unsigned bad = 0x80000000u;
-    if (wc != nullptr && m.lds_off >= 0) {   // this workgroup's tiles are cached in LDS (local index li)
+    if (CACHED) {   // this workgroup's tiles are cached in LDS (local index li)
         const unsigned char *base = wc + m.lds_off;
 #pragma unroll
         for (int j = 0; j < kUnit; ++j) {
@@ -521,12 +569,18 @@ __device__ __forceinline__ void unit_load(const TMat &m, bool two, int tile, int
 template <bool Q8>
 __device__ __forceinline__ f32x4 unit_mma(const uint4 (&f)[kUnit], const Act &x, int xo, bool two, int sb0, int nb,
                                           f32x4 acc) {
+    // every activation read of the unit is issued before the first product
+    half8 ah[kUnit], al[kUnit];
 #pragma unroll
     for (int j = 0; j < kUnit; ++j) {
         const int sb = min(sb0 + j, sb0 + nb - 1);
         const int kb = two ? sb >> 1 : sb;
-        const half8 bh = *reinterpret_cast<const half8 *>(x.hi + xo + kb * 32);
-        const half8 bl = *reinterpret_cast<const half8 *>(x.lo + xo + kb * 32);
+        ah[j] = *reinterpret_cast<const half8 *>(x.hi + xo + kb * 32);
+        al[j] = *reinterpret_cast<const half8 *>(x.lo + xo + kb * 32);
+    }
+#pragma unroll
+    for (int j = 0; j < kUnit; ++j) {
+        const half8 bh = ah[j], bl = al[j];
         if (Q8) {
             const half8 w = q8_to_half8(make_uint2(f[j].x, f[j].y));
             f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bh, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
@@ -553,7 +607,7 @@ __device__ __forceinline__ int wave_cut(int N, int w) { return (int)(((long long
 
 __device__ __forceinline__ int blocks_per_item(const TMat &m) { return m.type == PK_TYPE_F32 ? 2 * m.KB : m.KB; }
 
-template <bool Q8>
+template <bool Q8, bool CACHED>
 __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
                                                const Act &x, f32x4 *red, const unsigned char *wc) {
     // wave-uniform unit bookkeeping: the weight buffer descriptors stay in SGPRs
@@ -565,29 +619,27 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
     const int c0 = wave_cut(N, wave), c1 = wave_cut(N, wave + 1);
     if (c0 >= c1) return;
     const int xo = (lane & 15) * x.kp + (lane >> 4) * 8;
-    auto unit = [&](int u, int &item, int &sb0, int &nb) {
-        item = u / S;
-        const int c = u - item * S;
-        sb0 = c * kUnit;
-        nb = min(kUnit, KBe - sb0);
-    };
-    auto fetch = [&](int item, int sb0, int nb, uint4 (&f)[kUnit]) {
-        const bool in_a = item < n_a;
-        const int li = in_a ? item : item - n_a;
-        unit_load<Q8>(in_a ? A : Bm, two, rank + li * P, li, wc, sb0, nb, lane, f);
-    };
+    // the two matrices' descriptors, read once (not per unit from the kernel arguments)
+    const WView vA = wview(A), vB = wview(Bm);
+    int item = c0 / S, c = c0 - item * S;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int u = c0; u < c1; ++u) {
-        int item, sb0, nb;
-        unit(u, item, sb0, nb);
+        const int sb0 = c * kUnit, nb = min(kUnit, KBe - sb0);
+        const bool in_a = item < n_a;
+        const int li = in_a ? item : item - n_a;
         uint4 f[kUnit];
-        fetch(item, sb0, nb, f);
+        unit_load<Q8, CACHED>(pick(in_a, vA, vB), two, rank + li * P, li, wc, sb0, nb, lane, f);
         acc = unit_mma<Q8>(f, x, xo, two, sb0, nb, acc);
-        if (u + 1 == c1 || (u + 1) / S != item) {
+        if (++c == S || u + 1 == c1) {   // this item's last unit in this wave
             red[(item + wave) * kWave + lane] = acc;
             acc = f32x4{0.f, 0.f, 0.f, 0.f};
         }
+        if (c == S) {
+            c = 0;
+            ++item;
+        }
     }
+    TL(2);
 }
 
 // Sum each item's partials in wave order and run epi(item, acc); items are
@@ -596,7 +648,8 @@ template <class EpiFn>
 __device__ __forceinline__ void phase_reduce(int n_items, int S, const f32x4 *red, EpiFn epi) {
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int N = n_items * S;
-    __syncthreads();
+    lds_sync();
+    TL(3);
     for (int it = wave; it < n_items; it += kWaves) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         for (int w = 0; w < kWaves; ++w) {
@@ -605,7 +658,9 @@ __device__ __forceinline__ void phase_reduce(int n_items, int S, const f32x4 *re
         }
         epi(it, acc);
     }
-    __syncthreads();
+    TL(4);
+    lds_sync();
+    TL(5);
 }
 
 // Products of one phase for this workgroup, then the epilogue per item.
@@ -613,8 +668,15 @@ template <class EpiFn>
 __device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
                                           const Act &x, f32x4 *red, const unsigned char *wc, EpiFn epi) {
     if (n_items <= 0) return;
-    if (A.type == PK_TYPE_Q8_0) phase_partials<true>(A, n_a, Bm, n_items, rank, P, x, red, wc);
-    else phase_partials<false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+    // the LDS weight cache holds every step matrix or none
+    const bool cached = wc != nullptr && A.lds_off >= 0;
+    if (A.type == PK_TYPE_Q8_0) {
+        if (cached) phase_partials<true, true>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+        else phase_partials<true, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+    } else {
+        if (cached) phase_partials<false, true>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+        else phase_partials<false, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+    }
     const int KBe = A.type == PK_TYPE_F32 ? 2 * A.KB : A.KB;
     phase_reduce(n_items, (KBe + kUnit - 1) / kUnit, red, epi);
 }
@@ -674,7 +736,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
                 e[j] = q[j] = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (i < kTile * per && u < nc) {
                     const int ul = s.jst[c0 + u], b = s.b[ul];
-                    e[j] = *reinterpret_cast<const float4 *>(p.encp + (size_t)(p.encp_row[b] + s.t[ul]) * J + k);
+                    e[j] = *reinterpret_cast<const float4 *>(p.encp + (size_t)(s.erow[ul] + s.t[ul]) * J + k);
                     q[j] = ld4_coh(B.ppx, (unsigned)(((size_t)b * J + k) * 4));
                 }
             }
@@ -692,13 +754,14 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
                 }
             }
         }
-        __syncthreads();
+        TLBASE(21);
+        lds_sync();
+        TL(0);
         pmark(p, s, tlast, kPrJStage);
         // bias rows of this wave's first two items and the blank offset of this
         // lane's utterance, loaded before the products
         const int u = lane & 15, wave = threadIdx.x / kWave;
-        const int b_u = u < nc ? s.b[s.jst[c0 + u]] : 0;
-        const float bb = (u < nc && p.blank_bias) ? p.blank_bias[b_u] : 0.0f;
+        const float bb = u < nc ? s.bbias[s.jst[c0 + u]] : 0.0f;
         float4 pre_b[2];
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
@@ -708,6 +771,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
             pre_b[k].z = row0 + 2 < p.Vo ? p.b_out[row0 + 2] : 0.0f;
             pre_b[k].w = row0 + 3 < p.Vo ? p.b_out[row0 + 3] : 0.0f;
         }
+        TL(1);
         // each lane keeps its best key per head over all its rows; lanes of one
         // column then combine, and one LDS atomic per column and head follows
         unsigned long long best0 = 0ull, best1 = 0ull;
@@ -744,7 +808,8 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
             if (best0) atomicMax(&s.wgkey[c0 + u][0], best0);
             if (best1) atomicMax(&s.wgkey[c0 + u][1], best1);
         }
-        __syncthreads();
+        lds_sync();
+        TLA(27);
         pmark(p, s, tlast, kPrJCompute);
     }
     // one device-scope max per utterance and head into shard rank % kShards
@@ -759,39 +824,55 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
                                    ((unsigned long long)stamp << kStampShift) | k, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
     }
+    TLA(28);
 }
 
 // Layer 0 from the precomputed input projection: gates = E'[token] + R0,
 // elementwise per unit.  redundant: every unit for every listed utterance,
 // h' kept in LDS (h0s) as well; otherwise only this workgroup's unit tiles.
 // Owners store h', c' coherently.
-__device__ __forceinline__ void lstm_layer0(const KParams &p, Ctl &s, const Lds &S, bool redundant) {
+// Each thread issues the loads of up to kL0 units before computing any.
+constexpr int kL0 = 3;
+__device__ __forceinline__ void lstm_layer0(const KParams &p, Ctl &s, const Lds &S, const Bufs &B, bool redundant) {
     const int H = p.H;
     const int groups = p.w_hh[0].tiles;                 // unit groups of 4
     const int n_own = owned(groups, s.rank, s.P);
     const int nunits = redundant ? H : 4 * n_own;
-    for (int i = threadIdx.x; i < s.nl * nunits; i += kBlock) {
-        const int u = i / nunits, jj = i - u * nunits;
-        const int j = redundant ? jj : 4 * (s.rank + (jj / 4) * s.P) + (jj & 3);
-        if (j >= H) continue;
-        const int ul = s.lst[u], b = s.b[ul];
-        const bool zero = s.flags[ul] & kFlagZeroHC;
-        const int cur = s.cur[ul];
-        const float4 e = *reinterpret_cast<const float4 *>(p.eproj + (size_t)s.pend[ul] * 4 * H + 4 * j);
-        float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
-        float c_prev = 0.0f;
-        if (!zero) {
-            const float *rp = p.rx + rx_off(p, cur, 0, b) + 4 * j;
-            r = make_float4(ld_coh(rp), ld_coh(rp + 1), ld_coh(rp + 2), ld_coh(rp + 3));
-            c_prev = ld_coh(p.cx + hx_off(p, cur, 0, b) + j);
+    const int n_work = s.nl * nunits;
+    for (int base = 0; base < n_work; base += kL0 * kBlock) {
+        float4 e[kL0], r[kL0];
+        float c_prev[kL0];
+#pragma unroll
+        for (int q = 0; q < kL0; ++q) {
+            const int i = base + threadIdx.x + q * kBlock;
+            e[q] = r[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+            c_prev[q] = 0.0f;
+            if (i >= n_work) continue;
+            const int u = i / nunits, jj = i - u * nunits;
+            const int j = redundant ? jj : 4 * (s.rank + (jj / 4) * s.P) + (jj & 3);
+            if (j >= H) continue;
+            const int ul = s.lst[u], b = s.b[ul], cur = s.cur[ul];
+            e[q] = *reinterpret_cast<const float4 *>(p.eproj + (size_t)s.pend[ul] * 4 * H + 4 * j);
+            if (!(s.flags[ul] & kFlagZeroHC)) {
+                r[q] = ld4_coh(B.rx, (unsigned)((rx_off(p, cur, 0, b) + 4 * j) * 4));
+                c_prev[q] = ld_coh(p.cx + hx_off(p, cur, 0, b) + j);
+            }
         }
-        float c_new, h_new;
-        cell(e.x + r.x, e.y + r.y, e.z + r.z, e.w + r.w, c_prev, c_new, h_new);
-        if (redundant) S.h0s[u * H + j] = h_new;
-        const bool mine = ((j >> 2) % s.P) == s.rank;
-        if (mine) {
-            st_coh(p.cx + hx_off(p, cur ^ 1, 0, b) + j, c_new);
-            st_coh(p.hx + hx_off(p, cur ^ 1, 0, b) + j, h_new);
+#pragma unroll
+        for (int q = 0; q < kL0; ++q) {
+            const int i = base + threadIdx.x + q * kBlock;
+            if (i >= n_work) continue;
+            const int u = i / nunits, jj = i - u * nunits;
+            const int j = redundant ? jj : 4 * (s.rank + (jj / 4) * s.P) + (jj & 3);
+            if (j >= H) continue;
+            const int ul = s.lst[u], b = s.b[ul], cur = s.cur[ul];
+            float c_new, h_new;
+            cell(e[q].x + r[q].x, e[q].y + r[q].y, e[q].z + r[q].z, e[q].w + r[q].w, c_prev[q], c_new, h_new);
+            if (redundant) S.h0s[u * H + j] = h_new;
+            if (((j >> 2) % s.P) == s.rank) {
+                st_coh(p.cx + hx_off(p, cur ^ 1, 0, b) + j, c_new);
+                st_coh(p.hx + hx_off(p, cur ^ 1, 0, b) + j, h_new);
+            }
         }
     }
 }
@@ -840,6 +921,7 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
         pre_r[k] = ld4_coh(B.rx, (unsigned)((rx_off(p, cur, layer, b) + 4 * j) * 4));
         pre_c[k] = ld_coh(p.cx + hx_off(p, cur, layer, b) + j);
     }
+    TL(1);
     run_phase(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache,
               [&](int it, f32x4 acc) {
                   const int u = lane & 15;
@@ -901,18 +983,20 @@ __device__ __forceinline__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bu
     const int H = p.H, L = p.L;
     const bool redundant = s.nl <= kSmallB && p.n_dom == 1;
     const Act &x = S.act[1];
-    lstm_layer0(p, s, S, redundant);
+    lstm_layer0(p, s, S, B, redundant);
+    TLA(1);
     pmark(p, s, tlast, kPrL0);
     for (int lc = 0; lc < L; ++lc) {
         const bool local = lc == 0 && redundant;     // h_0' is in LDS already
         if (!local) {
             if (!dom_sync(p, s, epoch)) return false;
+            TLA(18 + lc);
             pmark(p, s, tlast, lc == 0 ? kPrSync0 : kPrSync1);
         }
         for (int c0 = 0; c0 < s.nl; c0 += kTile) {
             const int nc = min(kTile, s.nl - c0);
             if (local) {
-                __syncthreads();
+                lds_sync();
                 for (int i = threadIdx.x; i < kTile * (H / 4); i += kBlock) {
                     const int u = i / (H / 4), k = (i - u * (H / 4)) * 4;
                     put4(x, u, k, u < nc ? *reinterpret_cast<const float4 *>(S.h0s + u * H + k) : make_float4(0.f, 0.f, 0.f, 0.f));
@@ -920,10 +1004,13 @@ __device__ __forceinline__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bu
             } else {
                 stage_act(x, H, nc, B.hx, [&](int u) { const int ul = s.lst[c0 + u]; return hx_off(p, s.cur[ul] ^ 1, lc, s.b[ul]); });
             }
-            __syncthreads();
+            TLBASE(2 + 8 * lc);
+            lds_sync();
+            TL(0);
             pmark(p, s, tlast, kPrStageL);
             consume_layer(p, s, S, B, x, lc, c0, nc);
-            __syncthreads();
+            lds_sync();
+            TL(6);
         }
         pmark(p, s, tlast, lc == L - 1 ? kPrPred : kPrL1);
     }
@@ -934,6 +1021,7 @@ __device__ __forceinline__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bu
         s.flags[ul] &= ~kFlagZeroHC;
     }
     const bool ok = dom_sync(p, s, epoch);
+    TLA(20);
     pmark(p, s, tlast, kPrSync2);
     return ok;
 }
@@ -967,11 +1055,12 @@ __device__ __forceinline__ void gather_shards(const KParams &p, Ctl &s, unsigned
             s.wgkey[pair >> 1][pair & 1] = k;
         }
     }
-    __syncthreads();
+    lds_sync();
 }
 
 __device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp) {
     gather_shards(p, s, stamp);
+    TLA(30);
     for (int i = threadIdx.x; i < s.nj; i += kBlock) {
         const int ul = s.jst[i], b = s.b[ul];
         const unsigned long long kt = s.wgkey[i][0], kd = s.wgkey[i][1];
@@ -1087,6 +1176,10 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
     }
 
     if (threadIdx.x < kPrN) s.prof[threadIdx.x] = 0ull;
+#ifdef PK_TIMELINE
+    if (threadIdx.x < kWaves * kTl) tl_sum()[threadIdx.x] = 0ull;
+    if (threadIdx.x < 2 + kTl) tl_ctl()[threadIdx.x] = 0;
+#endif
     if (threadIdx.x == 0) {
         s.dom = p.wg_dom[wg];
         s.rank = p.wg_rank[wg];
@@ -1101,6 +1194,8 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         const bool init = ctrl[PK_CTRL_INIT] != 0;
         s.b[ul] = b;
         s.T[ul] = p.T[b];
+        s.erow[ul] = p.encp_row[b];
+        s.bbias[ul] = p.blank_bias ? p.blank_bias[b] : 0.0f;
         s.ntok[ul] = 0;
         s.steps[ul] = 0;
         s.nseg[ul] = 0;
@@ -1150,6 +1245,15 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
             break;
         }
         ++iter;
+#ifdef PK_TIMELINE
+        if (p.prof) {
+            if (threadIdx.x == 0) {
+                tl_ctl()[0] = (blockIdx.x == 0 && iter >= 40 && iter < 40 + 256) ? 1 : 0;
+                *tl_t0() = __builtin_amdgcn_s_memrealtime();
+            }
+            lds_sync();
+        }
+#endif
         if (s.nl > 0) {
             ok = lstm_and_pred(p, s, B, S, epoch, tlast);
             if (!ok) break;
@@ -1157,15 +1261,21 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         if (s.nj > 0) {
             joint_phase(p, s, B, S, iter, tlast);
             ok = dom_sync(p, s, epoch);
+            TLA(29);
             pmark(p, s, tlast, kPrJSync);
             if (!ok) break;
             decide(p, s, iter);
         }
-        __syncthreads();
+        lds_sync();
         build_lists(s);
+        TLA(31);
         pmark(p, s, tlast, kPrDecide);
     }
     if (p.prof && wg == 0 && threadIdx.x < kPrN) p.prof[threadIdx.x] = s.prof[threadIdx.x];
+#ifdef PK_TIMELINE
+    if (p.prof && wg == 0 && threadIdx.x < kWaves * kTl) p.prof[kPrN + threadIdx.x] = tl_sum()[threadIdx.x];
+    if (p.prof && wg == 0 && threadIdx.x < kTl) p.prof[kPrN + kWaves * kTl + threadIdx.x] = tl_ctl()[2 + threadIdx.x];
+#endif
     if (!ok) return;
 
     for (int ul = s.rank; ul < s.n; ul += s.P) {
