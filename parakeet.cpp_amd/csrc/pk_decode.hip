@@ -437,6 +437,8 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     if ((rc = vec_f32(d->joint_out_b, Vo, nullptr, b_out, "joint.out.bias"))) return cleanup(rc);
     if ((rc = vec_f32(d->joint_enc_b, J, nullptr, b_enc, "joint.enc.bias"))) return cleanup(rc);
     if ((rc = dense_f32(d->joint_enc_w, J, D, nullptr, w_enc, "joint.enc.weight"))) return cleanup(rc);
+    // joint.out bias padded with zeros to whole 16-row tiles (read a float4 per lane)
+    b_out.resize((size_t)(Vo + kTile - 1) / kTile * kTile, 0.0f);
     ar.add(b_pred.data(), b_pred.size() * 4, reinterpret_cast<const void **>(&kp.b_pred));
     ar.add(b_out.data(), b_out.size() * 4, reinterpret_cast<const void **>(&kp.b_out));
     ar.add(b_enc.data(), b_enc.size() * 4, reinterpret_cast<const void **>(&dec->b_enc));
@@ -465,6 +467,8 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
             hipMemcpy(dbi, bi.data(), 16 * (size_t)H, hipMemcpyHostToDevice) != hipSuccess ||
             hipMemcpy(dbh, bh.data(), 16 * (size_t)H, hipMemcpyHostToDevice) != hipSuccess)
             return cleanup(fail(PK_ERR_DEVICE, "embedding projection upload"));
+        if ((size_t)V1 * 4 * H * 4 >= (1ull << 31))   // the loop reads E' rows with 32-bit buffer offsets
+            return cleanup(fail(PK_ERR_UNSUPPORTED, "vocabulary x 4 x pred_hidden too large (%d x %d)", V1, H));
         if ((rc = dec->eproj.ensure((size_t)V1 * 4 * H * 4))) return cleanup(rc);
         dim3 grid((V1 + 15) / 16, (4 * H + 63) / 64);
         pkdev::embed_proj_kernel<<<grid, 256>>>(dw, de, 4 * H, V1, H, dbi, dbh, dec->eproj.as<float>());
@@ -660,6 +664,9 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         base[i] = bt->tokens_base ? bt->tokens_base[u] : 0;
     }
     const int max_iter = max_T * (std::max(bt->max_symbols, 1) + 1) + 4;
+    // the loop addresses encp with 32-bit buffer offsets below 2^31
+    if (rows * (long long)p.J * 4 >= (1ll << 31))
+        return fail(PK_ERR_UNSUPPORTED, "%lld frames in one call; at most %lld", rows, ((1ll << 31) - 1) / (p.J * 4ll));
     if ((unsigned)max_iter >= kMaxStamp) return fail(PK_ERR_UNSUPPORTED, "window too long for the iteration stamp");
     const int D = dec->desc.d_enc, J = p.J, L = p.L, H = p.H;
     int rc;
@@ -736,6 +743,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     }
     p.n_utts = m;
     p.encp = dec->d_encp.as<float>();
+    p.encp_rows = rows;
     p.encp_row = d_dst;
     p.T = d_T;
     p.slot = d_slot;

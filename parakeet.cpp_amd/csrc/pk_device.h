@@ -78,6 +78,7 @@ struct KParams {
     // batch
     int n_utts;
     const float *encp;           // [rows][J] b_e + W_e . enc
+    long long encp_rows;
     const long long *encp_row;   // [n_utts]
     const int *T;
     const int *slot;
@@ -133,6 +134,14 @@ __device__ __forceinline__ float4 ld4_coh(__amdgpu_buffer_rsrc_t r, unsigned byt
 __device__ __forceinline__ void st4_coh(__amdgpu_buffer_rsrc_t r, unsigned byte_off, float4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), r,
                                            byte_off, 0, kSC1);
+}
+// Offset past every buffer range: loads return 0 and stores are dropped.
+constexpr unsigned kBad = 0x80000000u;
+__device__ __forceinline__ float4 ld4(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+__device__ __forceinline__ float ld1_coh(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, kSC1));
 }
 __device__ __forceinline__ float ld_coh(const float *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -451,7 +460,7 @@ __device__ __forceinline__ size_t rx_off(const KParams &p, int buf, int layer, i
 }
 
 struct Bufs {
-    __amdgpu_buffer_rsrc_t hx, cx, ppx, rx;
+    __amdgpu_buffer_rsrc_t hx, cx, ppx, rx, ep, encp;
 };
 
 // Stage vectors of length K for n <= 16 utterances into an activation block:
@@ -467,7 +476,8 @@ __device__ __forceinline__ void stage_act(const Act &x, int K, int n, __amdgpu_b
         for (int j = 0; j < kStageMax; ++j) {
             const int i = base + threadIdx.x + j * kBlock;
             const int u = i / per, k = (i - u * per) * 4;
-            v[j] = (i < kTile * per && u < n) ? ld4_coh(r, (unsigned)((off(u) + k) * 4)) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const bool ok = i < kTile * per && u < n;
+            v[j] = ld4_coh(r, ok ? (unsigned)((off(min(u, n - 1)) + k) * 4) : kBad);
         }
 #pragma unroll
         for (int j = 0; j < kStageMax; ++j) {
@@ -733,12 +743,10 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
             for (int j = 0; j < kStageMax; ++j) {
                 const int i = base + threadIdx.x + j * kBlock;
                 const int u = i / per, k = (i - u * per) * 4;
-                e[j] = q[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (i < kTile * per && u < nc) {
-                    const int ul = s.jst[c0 + u], b = s.b[ul];
-                    e[j] = *reinterpret_cast<const float4 *>(p.encp + (size_t)(s.erow[ul] + s.t[ul]) * J + k);
-                    q[j] = ld4_coh(B.ppx, (unsigned)(((size_t)b * J + k) * 4));
-                }
+                const bool ok = i < kTile * per && u < nc;
+                const int ul = s.jst[c0 + min(u, nc - 1)], b = s.b[ul];
+                e[j] = ld4(B.encp, ok ? (unsigned)(((size_t)(s.erow[ul] + s.t[ul]) * J + k) * 4) : kBad);
+                q[j] = ld4_coh(B.ppx, ok ? (unsigned)(((size_t)b * J + k) * 4) : kBad);
             }
 #pragma unroll
             for (int j = 0; j < kStageMax; ++j) {
@@ -762,14 +770,14 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         // lane's utterance, loaded before the products
         const int u = lane & 15, wave = threadIdx.x / kWave;
         const float bb = u < nc ? s.bbias[s.jst[c0 + u]] : 0.0f;
+        // (b_out is zero-padded to whole tiles)
+        const __amdgpu_buffer_rsrc_t rbo = rsrc(p.b_out, (unsigned)p.w_out.tiles * kTile * 4u);
         float4 pre_b[2];
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            const int row0 = (s.rank + (wave + k * kWaves) * s.P) * kTile + (lane >> 4) * 4;
-            pre_b[k].x = row0 < p.Vo ? p.b_out[row0] : 0.0f;
-            pre_b[k].y = row0 + 1 < p.Vo ? p.b_out[row0 + 1] : 0.0f;
-            pre_b[k].z = row0 + 2 < p.Vo ? p.b_out[row0 + 2] : 0.0f;
-            pre_b[k].w = row0 + 3 < p.Vo ? p.b_out[row0 + 3] : 0.0f;
+            const int it = wave + k * kWaves;
+            const int row0 = (s.rank + it * s.P) * kTile + (lane >> 4) * 4;
+            pre_b[k] = ld4(rbo, it < n_out ? (unsigned)row0 * 4u : kBad);
         }
         TL(1);
         // each lane keeps its best key per head over all its rows; lanes of one
@@ -780,13 +788,13 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
                       if (u >= nc) return;
                       const int tile = s.rank + k * s.P;
                       const int kk = (k - wave) / kWaves;
-                      const float4 bias4 = kk == 0 ? pre_b[0] : pre_b[1];
+                      const float4 bias4 = kk == 0 ? pre_b[0] : kk == 1 ? pre_b[1]
+                                                   : ld4(rbo, (unsigned)(tile * kTile + (lane >> 4) * 4) * 4u);
 #pragma unroll
                       for (int i = 0; i < 4; ++i) {
                           const int row = tile * kTile + (lane >> 4) * 4 + i;
                           if (row >= p.Vo) continue;
-                          const float bias = kk < 2 ? (i == 0 ? bias4.x : i == 1 ? bias4.y : i == 2 ? bias4.z : bias4.w)
-                                                    : p.b_out[row];
+                          const float bias = i == 0 ? bias4.x : i == 1 ? bias4.y : i == 2 ? bias4.z : bias4.w;
                           float v = acc[i] + bias;
                           if (row == p.blank) v += bb;
                           if (row < p.V1) {
@@ -843,20 +851,16 @@ __device__ __forceinline__ void lstm_layer0(const KParams &p, Ctl &s, const Lds 
         float4 e[kL0], r[kL0];
         float c_prev[kL0];
 #pragma unroll
-        for (int q = 0; q < kL0; ++q) {
+        for (int q = 0; q < kL0; ++q) {   // no branches: unused loads take kBad and return 0
             const int i = base + threadIdx.x + q * kBlock;
-            e[q] = r[q] = make_float4(0.f, 0.f, 0.f, 0.f);
-            c_prev[q] = 0.0f;
-            if (i >= n_work) continue;
-            const int u = i / nunits, jj = i - u * nunits;
+            const int u = min(i, n_work - 1) / nunits, jj = min(i, n_work - 1) - u * nunits;
             const int j = redundant ? jj : 4 * (s.rank + (jj / 4) * s.P) + (jj & 3);
-            if (j >= H) continue;
+            const bool ok = i < n_work && j < H;
             const int ul = s.lst[u], b = s.b[ul], cur = s.cur[ul];
-            e[q] = *reinterpret_cast<const float4 *>(p.eproj + (size_t)s.pend[ul] * 4 * H + 4 * j);
-            if (!(s.flags[ul] & kFlagZeroHC)) {
-                r[q] = ld4_coh(B.rx, (unsigned)((rx_off(p, cur, 0, b) + 4 * j) * 4));
-                c_prev[q] = ld_coh(p.cx + hx_off(p, cur, 0, b) + j);
-            }
+            const bool st = ok && !(s.flags[ul] & kFlagZeroHC);
+            e[q] = ld4(B.ep, ok ? (unsigned)(((size_t)s.pend[ul] * 4 * H + 4 * j) * 4) : kBad);
+            r[q] = ld4_coh(B.rx, st ? (unsigned)((rx_off(p, cur, 0, b) + 4 * j) * 4) : kBad);
+            c_prev[q] = ld1_coh(B.cx, st ? (unsigned)((hx_off(p, cur, 0, b) + j) * 4) : kBad);
         }
 #pragma unroll
         for (int q = 0; q < kL0; ++q) {
@@ -892,78 +896,59 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
     const TMat &wc = last ? p.w_pred : p.w_ih[lc + 1];
     const TMat &wr = p.w_hh[lc];
     const int n_c = owned(wc.tiles, s.rank, s.P), n_r = owned(wr.tiles, s.rank, s.P);
-    // Cell-update operands (R, c_prev, bias) of this wave's first kPre consumer
-    // items: they were written one step earlier, so they are loaded before the
-    // products rather than after them.
-    constexpr int kPre = 2;
-    const int wave = threadIdx.x / kWave, layer = lc + 1;
+    const int wave = threadIdx.x / kWave, layer = lc + 1, u = lane & 15;
+    // this lane's utterance (a valid index for every lane; lanes u >= nc store nothing)
+    const int ul = s.lst[c0 + min(u, nc - 1)], b = s.b[ul], cur = s.cur[ul];
+    const bool zero = s.flags[ul] & kFlagZeroHC;
+    // Epilogue operands of this wave's first kPre consumer items -- the bias
+    // rows and, for an LSTM layer, R and c_prev, written one step earlier --
+    // loaded before the products.  Lane rows row0 .. row0+3 are the pred rows,
+    // or the four gates of unit j = row0 / 4.  Unused loads take an offset past
+    // the buffer and return 0: no branches, so nothing waits for them early.
+    constexpr int kPre = 3;
+    const __amdgpu_buffer_rsrc_t rb = rsrc(last ? p.b_pred : p.b_lstm[layer], (unsigned)(last ? p.J : 4 * H) * 4u);
     float4 pre_r[kPre], pre_b[kPre];
     float pre_c[kPre];
 #pragma unroll
     for (int k = 0; k < kPre; ++k) {
-        pre_r[k] = pre_b[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        pre_c[k] = 0.0f;
-        const int it = wave + k * kWaves, u = lane & 15;
-        if (it >= n_c || u >= nc) continue;
-        if (last) {                               // pred projection: the bias rows only
-            const int row0 = (s.rank + it * s.P) * kTile + (lane >> 4) * 4;
-            pre_b[k].x = row0 < p.J ? p.b_pred[row0] : 0.0f;
-            pre_b[k].y = row0 + 1 < p.J ? p.b_pred[row0 + 1] : 0.0f;
-            pre_b[k].z = row0 + 2 < p.J ? p.b_pred[row0 + 2] : 0.0f;
-            pre_b[k].w = row0 + 3 < p.J ? p.b_pred[row0 + 3] : 0.0f;
-            continue;
-        }
-        const int j = (s.rank + it * s.P) * 4 + (lane >> 4);
-        if (j >= H) continue;
-        const int ul = s.lst[c0 + u], b = s.b[ul], cur = s.cur[ul];
-        pre_b[k] = *reinterpret_cast<const float4 *>(p.b_lstm[layer] + 4 * j);
-        if (s.flags[ul] & kFlagZeroHC) continue;
-        pre_r[k] = ld4_coh(B.rx, (unsigned)((rx_off(p, cur, layer, b) + 4 * j) * 4));
-        pre_c[k] = ld_coh(p.cx + hx_off(p, cur, layer, b) + j);
+        const int it = wave + k * kWaves;
+        const int row0 = (s.rank + it * s.P) * kTile + (lane >> 4) * 4;
+        const bool ok = it < n_c && u < nc;
+        const bool st = ok && !last && !zero;
+        pre_b[k] = ld4(rb, ok ? (unsigned)row0 * 4u : kBad);
+        pre_r[k] = ld4_coh(B.rx, st ? (unsigned)((rx_off(p, cur, layer, b) + row0) * 4) : kBad);
+        pre_c[k] = ld1_coh(B.cx, st ? (unsigned)((hx_off(p, cur, layer, b) + row0 / 4) * 4) : kBad);
     }
     TL(1);
     run_phase(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache,
               [&](int it, f32x4 acc) {
-                  const int u = lane & 15;
                   if (u >= nc) return;
-                  const int ul = s.lst[c0 + u], b = s.b[ul];
-                  const int cur = s.cur[ul];
                   if (it >= n_c) {          // recurrent product for the next step
                       const int row0 = (s.rank + (it - n_c) * s.P) * kTile + (lane >> 4) * 4;
-                      if (row0 < 4 * H)
-                          st4_coh(B.rx, (unsigned)((rx_off(p, cur ^ 1, lc, b) + row0) * 4),
-                                  make_float4(acc[0], acc[1], acc[2], acc[3]));
+                      st4_coh(B.rx, (unsigned)((rx_off(p, cur ^ 1, lc, b) + row0) * 4),
+                              make_float4(acc[0], acc[1], acc[2], acc[3]));
                       return;
                   }
-                  const int tile = s.rank + it * s.P;
-                  if (last) {               // pred projection
-                      const int kk = (it - wave) / kWaves;
-                      const float4 pb = kk == 0 ? pre_b[0] : pre_b[kPre - 1];
-                      const float bias[4] = {pb.x, pb.y, pb.z, pb.w};
-#pragma unroll
-                      for (int i = 0; i < 4; ++i) {
-                          const int row = tile * kTile + (lane >> 4) * 4 + i;
-                          if (row < p.J)
-                              st_coh(p.ppx + (size_t)b * p.J + row, (kk < kPre ? bias[i] : p.b_pred[row]) + acc[i]);
-                      }
-                      return;
-                  }
-                  const int j = tile * 4 + (lane >> 4);
-                  if (j >= H) return;
+                  const int row0 = (s.rank + it * s.P) * kTile + (lane >> 4) * 4;
                   const int k = (it - wave) / kWaves;
-                  float4 r, bias;
+                  float4 bias, r;
                   float c_prev;
                   if (k < kPre) {
-                      r = k == 0 ? pre_r[0] : pre_r[kPre - 1];
-                      bias = k == 0 ? pre_b[0] : pre_b[kPre - 1];
-                      c_prev = k == 0 ? pre_c[0] : pre_c[kPre - 1];
+                      bias = k == 0 ? pre_b[0] : k == 1 ? pre_b[1] : pre_b[2];
+                      r = k == 0 ? pre_r[0] : k == 1 ? pre_r[1] : pre_r[2];
+                      c_prev = k == 0 ? pre_c[0] : k == 1 ? pre_c[1] : pre_c[2];
                   } else {
-                      const bool zero = s.flags[ul] & kFlagZeroHC;
-                      bias = *reinterpret_cast<const float4 *>(p.b_lstm[layer] + 4 * j);
-                      r = zero ? make_float4(0.f, 0.f, 0.f, 0.f)
-                               : ld4_coh(B.rx, (unsigned)((rx_off(p, cur, layer, b) + 4 * j) * 4));
-                      c_prev = zero ? 0.0f : ld_coh(p.cx + hx_off(p, cur, layer, b) + j);
+                      const bool st = !last && !zero;
+                      bias = ld4(rb, (unsigned)row0 * 4u);
+                      r = ld4_coh(B.rx, st ? (unsigned)((rx_off(p, cur, layer, b) + row0) * 4) : kBad);
+                      c_prev = ld1_coh(B.cx, st ? (unsigned)((hx_off(p, cur, layer, b) + row0 / 4) * 4) : kBad);
                   }
+                  if (last) {               // pred projection: rows row0 .. row0+3 of pp
+                      st4_coh(B.ppx, (unsigned)(((size_t)b * p.J + row0) * 4),
+                              make_float4(acc[0] + bias.x, acc[1] + bias.y, acc[2] + bias.z, acc[3] + bias.w));
+                      return;
+                  }
+                  const int j = row0 / 4;
                   float c_new, h_new;
                   cell((acc[0] + r.x) + bias.x, (acc[1] + r.y) + bias.y, (acc[2] + r.z) + bias.z,
                        (acc[3] + r.w) + bias.w, c_prev, c_new, h_new);
@@ -1151,6 +1136,8 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
     B.cx = rsrc(p.cx, (unsigned)((size_t)2 * L * n_all * H * 4));
     B.ppx = rsrc(p.ppx, (unsigned)((size_t)n_all * J * 4));
     B.rx = rsrc(p.rx, (unsigned)((size_t)2 * L * n_all * 4 * H * 4));
+    B.ep = rsrc(p.eproj, (unsigned)((size_t)p.V1 * 4 * H * 4));
+    B.encp = rsrc(p.encp, (unsigned)(p.encp_rows * J * 4));
 
     // LDS: one activation block (the joint's hidden block and the LSTM phases'
     // block are never live together), per-(item, wave) partials, the redundant
