@@ -181,10 +181,12 @@ __device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo) {
     lo = (_Float16)(x - (float)hi);
 }
 
-// Staged activation block: NT*16 utterance rows of K values as f16 (hi, lo).
+// Staged activation block: 16 utterance rows of K values as f16 (hi, lo).
+// Only rows 0 .. n-1 are staged; product columns n .. 15 are not used.
 struct Act {
     _Float16 *hi, *lo;
     int kp;     // row stride in halves (K + kKPad)
+    int n;      // live rows
 };
 
 __device__ __forceinline__ void put4(const Act &x, int row, int k, float4 v) {
@@ -470,19 +472,19 @@ constexpr int kStageMax = 5;    // float4 per thread per round: one round covers
 template <class OffFn>
 __device__ __forceinline__ void stage_act(const Act &x, int K, int n, __amdgpu_buffer_rsrc_t r, OffFn off) {
     const int per = K / 4;
-    for (int base = 0; base < kTile * per; base += kStageMax * kBlock) {
+    for (int base = 0; base < n * per; base += kStageMax * kBlock) {
         float4 v[kStageMax];
 #pragma unroll
         for (int j = 0; j < kStageMax; ++j) {
             const int i = base + threadIdx.x + j * kBlock;
             const int u = i / per, k = (i - u * per) * 4;
-            const bool ok = i < kTile * per && u < n;
+            const bool ok = i < n * per;
             v[j] = ld4_coh(r, ok ? (unsigned)((off(min(u, n - 1)) + k) * 4) : kBad);
         }
 #pragma unroll
         for (int j = 0; j < kStageMax; ++j) {
             const int i = base + threadIdx.x + j * kBlock;
-            if (i < kTile * per) {
+            if (i < n * per) {
                 const int u = i / per, k = (i - u * per) * 4;
                 put4(x, u, k, v[j]);
             }
@@ -504,7 +506,7 @@ __device__ __forceinline__ void stage_act(const Act &x, int K, int n, __amdgpu_b
 // (item, wave) in LDS slot item + wave; phase_reduce sums each item's partials
 // in wave order -- a fixed order, so results do not depend on timing.
 
-constexpr int kUnit = 5;   // K blocks per unit
+constexpr int kUnit = 5;   // K blocks per unit (measured: 5 beats 8 and 10 with fragments from L2 or LDS)
 
 // Fragments of one unit: blocks sb0 .. sb0+nb-1 of one tile; blocks past nb
 // read as zero (buffer loads past the range return 0).
@@ -628,6 +630,9 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
     const int N = n_items * S;
     const int c0 = wave_cut(N, wave), c1 = wave_cut(N, wave + 1);
     if (c0 >= c1) return;
+    // Column c of the product depends only on column c of the activations;
+    // rows past x.n are not staged (they hold older values) and the columns
+    // they feed are never read.
     const int xo = (lane & 15) * x.kp + (lane >> 4) * 8;
     // the two matrices' descriptors, read once (not per unit from the kernel arguments)
     const WView vA = wview(A), vB = wview(Bm);
@@ -732,18 +737,19 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
     const int J = p.J, lane = threadIdx.x & (kWave - 1);
     if (threadIdx.x < 2 * kDomCap) s.wgkey[threadIdx.x / 2][threadIdx.x % 2] = 0ull;
     const int n_out = owned(p.w_out.tiles, s.rank, s.P);
-    const Act &x = S.act[0];
     for (int c0 = 0; c0 < s.nj; c0 += kTile) {
         const int nc = min(kTile, s.nj - c0);
+        Act x = S.act[0];
+        x.n = nc;
         // stage hidden = relu(encp[t] + pp) for this column tile
-        for (int base = 0; base < kTile * (J / 4); base += kStageMax * kBlock) {
+        for (int base = 0; base < nc * (J / 4); base += kStageMax * kBlock) {
             const int per = J / 4;
             float4 e[kStageMax], q[kStageMax];
 #pragma unroll
             for (int j = 0; j < kStageMax; ++j) {
                 const int i = base + threadIdx.x + j * kBlock;
                 const int u = i / per, k = (i - u * per) * 4;
-                const bool ok = i < kTile * per && u < nc;
+                const bool ok = i < nc * per;
                 const int ul = s.jst[c0 + min(u, nc - 1)], b = s.b[ul];
                 e[j] = ld4(B.encp, ok ? (unsigned)(((size_t)(s.erow[ul] + s.t[ul]) * J + k) * 4) : kBad);
                 q[j] = ld4_coh(B.ppx, ok ? (unsigned)(((size_t)b * J + k) * 4) : kBad);
@@ -751,7 +757,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
 #pragma unroll
             for (int j = 0; j < kStageMax; ++j) {
                 const int i = base + threadIdx.x + j * kBlock;
-                if (i < kTile * per) {
+                if (i < nc * per) {
                     const int u = i / per, k = (i - u * per) * 4;
                     float4 v = make_float4(e[j].x + q[j].x, e[j].y + q[j].y, e[j].z + q[j].z, e[j].w + q[j].w);
                     v.x = (0.0f < v.x) ? v.x : 0.0f;
@@ -967,7 +973,6 @@ __device__ __forceinline__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bu
                               unsigned long long &tlast) {
     const int H = p.H, L = p.L;
     const bool redundant = s.nl <= kSmallB && p.n_dom == 1;
-    const Act &x = S.act[1];
     lstm_layer0(p, s, S, B, redundant);
     TLA(1);
     pmark(p, s, tlast, kPrL0);
@@ -980,11 +985,13 @@ __device__ __forceinline__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bu
         }
         for (int c0 = 0; c0 < s.nl; c0 += kTile) {
             const int nc = min(kTile, s.nl - c0);
+            Act x = S.act[1];
+            x.n = nc;
             if (local) {
                 lds_sync();
-                for (int i = threadIdx.x; i < kTile * (H / 4); i += kBlock) {
+                for (int i = threadIdx.x; i < nc * (H / 4); i += kBlock) {
                     const int u = i / (H / 4), k = (i - u * (H / 4)) * 4;
-                    put4(x, u, k, u < nc ? *reinterpret_cast<const float4 *>(S.h0s + u * H + k) : make_float4(0.f, 0.f, 0.f, 0.f));
+                    put4(x, u, k, *reinterpret_cast<const float4 *>(S.h0s + u * H + k));
                 }
             } else {
                 stage_act(x, H, nc, B.hx, [&](int u) { const int ul = s.lst[c0 + u]; return hx_off(p, s.cur[ul] ^ 1, lc, s.b[ul]); });
@@ -1152,6 +1159,7 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
             S.act[a].hi = reinterpret_cast<_Float16 *>(q);
             S.act[a].lo = S.act[a].hi + kTile * kp;
             S.act[a].kp = kp;
+            S.act[a].n = kTile;
         }
         q += (size_t)kTile * ((J > H ? J : H) + kKPad) * 2 * 2;
         S.red = reinterpret_cast<f32x4 *>(q);
