@@ -505,13 +505,13 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     kp.slot_r = dec->slots_r.as<float>();
     kp.slot_ctrl = dec->slots_ctrl.as<int>();
 
-    // decode-loop launch shape: one workgroup per CU; LDS = activation blocks
-    // [hidden | h_0 .. h_{L-1}] of one 16-utterance tile + K-split partials +
-    // the redundant layer-0 output
+    // decode-loop launch shape: one workgroup per CU; LDS = one activation
+    // block (16 utterance rows, hidden or h_l) + per-wave partials + the
+    // optional weight cache
     const size_t act = (size_t)kTile * (std::max(J, H) + kKPad) * 2 * 2;   // shared by the joint and LSTM phases
     if (std::max(J, H) > 4096)
         return cleanup(fail(PK_ERR_UNSUPPORTED, "hidden sizes above 4096"));
-    dec->lds_fixed = act + (size_t)kSmallB * H * 4;
+    dec->lds_fixed = act;
     // dynamic LDS bound of any launch: the block's LDS less the kernel's static LDS
     hipFuncAttributes fa{};
     if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(pkdev::decode_loop_kernel)) != hipSuccess)

@@ -702,7 +702,6 @@ __device__ __forceinline__ int owned(int tiles, int r, int P) { return tiles > r
 struct Lds {
     Act act[1 + PK_MAX_LAYERS];   // staged activation blocks
     f32x4 *red;                   // [red_slots][kWave] per-(item, wave) partials
-    float *h0s;                   // [kSmallB][H] layer-0 output in redundant mode
     const unsigned char *wcache;  // weight cache (nullptr when the tiles do not fit)
 };
 
@@ -843,7 +842,8 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
 
 // Layer 0 from the precomputed input projection: gates = E'[token] + R0,
 // elementwise per unit.  redundant: every unit for every listed utterance,
-// h' kept in LDS (h0s) as well; otherwise only this workgroup's unit tiles.
+// h' also written into the layer-1 activation block; otherwise only this
+// workgroup's unit tiles.
 // Owners store h', c' coherently.
 // Each thread issues the loads of up to kL0 units before computing any.
 constexpr int kL0 = 3;
@@ -878,7 +878,10 @@ __device__ __forceinline__ void lstm_layer0(const KParams &p, Ctl &s, const Lds 
             const int ul = s.lst[u], b = s.b[ul], cur = s.cur[ul];
             float c_new, h_new;
             cell(e[q].x + r[q].x, e[q].y + r[q].y, e[q].z + r[q].z, e[q].w + r[q].w, c_prev[q], c_new, h_new);
-            if (redundant) S.h0s[u * H + j] = h_new;
+            if (redundant) {   // straight into the layer-1 activation block
+                const Act &x = S.act[1];
+                split_f16(h_new, x.hi[u * x.kp + j], x.lo[u * x.kp + j]);
+            }
             if (((j >> 2) % s.P) == s.rank) {
                 st_coh(p.cx + hx_off(p, cur ^ 1, 0, b) + j, c_new);
                 st_coh(p.hx + hx_off(p, cur ^ 1, 0, b) + j, h_new);
@@ -987,13 +990,7 @@ __device__ __forceinline__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bu
             const int nc = min(kTile, s.nl - c0);
             Act x = S.act[1];
             x.n = nc;
-            if (local) {
-                lds_sync();
-                for (int i = threadIdx.x; i < nc * (H / 4); i += kBlock) {
-                    const int u = i / (H / 4), k = (i - u * (H / 4)) * 4;
-                    put4(x, u, k, *reinterpret_cast<const float4 *>(S.h0s + u * H + k));
-                }
-            } else {
+            if (!local) {   // (redundant layer 0 wrote h_0' into the block itself)
                 stage_act(x, H, nc, B.hx, [&](int u) { const int ul = s.lst[c0 + u]; return hx_off(p, s.cur[ul] ^ 1, lc, s.b[ul]); });
             }
             TLBASE(2 + 8 * lc);
@@ -1147,8 +1144,8 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
     B.encp = rsrc(p.encp, (unsigned)(p.encp_rows * J * 4));
 
     // LDS: one activation block (the joint's hidden block and the LSTM phases'
-    // block are never live together), per-(item, wave) partials, the redundant
-    // layer-0 output, then the weight cache
+    // block are never live together), per-(item, wave) partials, then the
+    // weight cache
     Lds S;
     unsigned char *wcache = nullptr;
     {
@@ -1164,8 +1161,6 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         q += (size_t)kTile * ((J > H ? J : H) + kKPad) * 2 * 2;
         S.red = reinterpret_cast<f32x4 *>(q);
         q += (size_t)p.red_slots * kWave * sizeof(f32x4);
-        S.h0s = reinterpret_cast<float *>(q);
-        q += (size_t)kSmallB * H * 4;
         if (p.wcache_bytes > 0) wcache = q;
         S.wcache = wcache;
     }
