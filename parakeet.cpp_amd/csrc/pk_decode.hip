@@ -790,13 +790,24 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         HIP_TRY(hipMemsetAsync(dec->d_prof.p, 0, (pkdev::kPrN + 9 * pkdev::kTl) * 8, dec->stream));
         p.prof = dec->d_prof.as<unsigned long long>();
     }
-    // LDS partial slots: the most items any phase gives one workgroup, plus one per wave
+    // LDS partial slots.  K-major unit order (activation fragments reused
+    // across a workgroup's tiles) needs one slot per unit of the largest
+    // phase; item-major needs the most items of any phase plus one per wave.
+    // K-major whenever its slots fit.
     {
         auto items = [&](const pkdev::TMat &m) { return (m.tiles + pl.P - 1) / pl.P; };
-        int most = items(p.w_out);
-        for (int l = 0; l < p.L; ++l)
-            most = std::max(most, items(l + 1 < p.L ? p.w_ih[l + 1] : p.w_pred) + items(p.w_hh[l]));
-        p.red_slots = most + kWaves;
+        auto units = [&](const pkdev::TMat &m) {
+            const int kbe = m.type == PK_TYPE_F32 ? 2 * m.KB : m.KB;
+            return (kbe + pkdev::kUnit - 1) / pkdev::kUnit;
+        };
+        int most = items(p.w_out), kslots = items(p.w_out) * units(p.w_out);
+        for (int l = 0; l < p.L; ++l) {
+            const pkdev::TMat &c = l + 1 < p.L ? p.w_ih[l + 1] : p.w_pred;
+            most = std::max(most, items(c) + items(p.w_hh[l]));
+            kslots = std::max(kslots, (items(c) + items(p.w_hh[l])) * units(c));
+        }
+        p.kmajor = dec->lds_fixed + (size_t)kslots * kWave * 16 <= dec->lds_bytes ? 1 : 0;
+        p.red_slots = p.kmajor ? kslots : most + kWaves;
     }
     size_t lds = dec->lds_fixed + (size_t)p.red_slots * kWave * 16;
     if (lds > dec->lds_bytes)

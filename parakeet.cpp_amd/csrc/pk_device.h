@@ -106,7 +106,8 @@ struct KParams {
     int shards;                  // power of two <= kShards: ranks per shard ~ 8
     int *status;                 // [0] error code, [1] iterations, [2] overflow, [3] trace overflow
     int max_iter;
-    int red_slots;               // LDS partial slots: items of the largest phase + kWaves
+    int red_slots;               // LDS partial slots (K-major: items x units per item of the largest phase)
+    int kmajor;                  // unit order of every phase: 1 K-major, 0 item-major
     int wcache_bytes;            // LDS weight cache per workgroup (0: weights are read from L2)
     unsigned long long *prof;    // nullable: per-phase wall-clock totals of workgroup 0 (100 MHz ticks)
 };
@@ -576,13 +577,9 @@ __device__ __forceinline__ void unit_load(const WView m, bool two, int tile, int
     }
 }
 
-// acc += (unit's weight blocks) . (activation blocks); xo = this lane's
-// activation offset.  Zero blocks past nb add nothing.
-template <bool Q8>
-__device__ __forceinline__ f32x4 unit_mma(const uint4 (&f)[kUnit], const Act &x, int xo, bool two, int sb0, int nb,
-                                          f32x4 acc) {
-    // every activation read of the unit is issued before the first product
-    half8 ah[kUnit], al[kUnit];
+// The activation fragments of a unit's K blocks (all reads issued at once).
+__device__ __forceinline__ void unit_act(const Act &x, int xo, bool two, int sb0, int nb, half8 (&ah)[kUnit],
+                                         half8 (&al)[kUnit]) {
 #pragma unroll
     for (int j = 0; j < kUnit; ++j) {
         const int sb = min(sb0 + j, sb0 + nb - 1);
@@ -590,6 +587,13 @@ __device__ __forceinline__ f32x4 unit_mma(const uint4 (&f)[kUnit], const Act &x,
         ah[j] = *reinterpret_cast<const half8 *>(x.hi + xo + kb * 32);
         al[j] = *reinterpret_cast<const half8 *>(x.lo + xo + kb * 32);
     }
+}
+
+// acc += (unit's weight blocks) . (activation blocks).  Zero blocks past nb
+// add nothing.
+template <bool Q8>
+__device__ __forceinline__ f32x4 unit_mma(const uint4 (&f)[kUnit], const half8 (&ah)[kUnit], const half8 (&al)[kUnit],
+                                          bool two, int sb0, f32x4 acc) {
 #pragma unroll
     for (int j = 0; j < kUnit; ++j) {
         const half8 bh = ah[j], bl = al[j];
@@ -619,7 +623,7 @@ __device__ __forceinline__ int wave_cut(int N, int w) { return (int)(((long long
 
 __device__ __forceinline__ int blocks_per_item(const TMat &m) { return m.type == PK_TYPE_F32 ? 2 * m.KB : m.KB; }
 
-template <bool Q8, bool CACHED>
+template <bool Q8, bool CACHED, bool KMAJ>
 __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
                                                const Act &x, f32x4 *red, const unsigned char *wc) {
     // wave-uniform unit bookkeeping: the weight buffer descriptors stay in SGPRs
@@ -636,30 +640,58 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
     const int xo = (lane & 15) * x.kp + (lane >> 4) * 8;
     // the two matrices' descriptors, read once (not per unit from the kernel arguments)
     const WView vA = wview(A), vB = wview(Bm);
-    int item = c0 / S, c = c0 - item * S;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int u = c0; u < c1; ++u) {
-        const int sb0 = c * kUnit, nb = min(kUnit, KBe - sb0);
-        const bool in_a = item < n_a;
-        const int li = in_a ? item : item - n_a;
-        uint4 f[kUnit];
-        unit_load<Q8, CACHED>(pick(in_a, vA, vB), two, rank + li * P, li, wc, sb0, nb, lane, f);
-        acc = unit_mma<Q8>(f, x, xo, two, sb0, nb, acc);
-        if (++c == S || u + 1 == c1) {   // this item's last unit in this wave
-            red[(item + wave) * kWave + lane] = acc;
-            acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    half8 ah[kUnit], al[kUnit];
+    if (KMAJ) {
+        // unit u = c * n_items + item: a wave's range runs over items at one K
+        // chunk c, so its activation fragments are read once per chunk; one
+        // partial per unit, in slot item * S + c
+        int c = c0 / n_items, item = c0 - c * n_items, have = -1;
+        for (int u = c0; u < c1; ++u) {
+            const int sb0 = c * kUnit, nb = min(kUnit, KBe - sb0);
+            if (c != have) {
+                unit_act(x, xo, two, sb0, nb, ah, al);
+                have = c;
+            }
+            const bool in_a = item < n_a;
+            const int li = in_a ? item : item - n_a;
+            uint4 f[kUnit];
+            unit_load<Q8, CACHED>(pick(in_a, vA, vB), two, rank + li * P, li, wc, sb0, nb, lane, f);
+            red[(item * S + c) * kWave + lane] = unit_mma<Q8>(f, ah, al, two, sb0, f32x4{0.f, 0.f, 0.f, 0.f});
+            if (++item == n_items) {
+                item = 0;
+                ++c;
+            }
         }
-        if (c == S) {
-            c = 0;
-            ++item;
+    } else {
+        // unit u = item * S + c: a wave keeps one running partial per item, in
+        // slot item + wave
+        int item = c0 / S, c = c0 - item * S;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int u = c0; u < c1; ++u) {
+            const int sb0 = c * kUnit, nb = min(kUnit, KBe - sb0);
+            const bool in_a = item < n_a;
+            const int li = in_a ? item : item - n_a;
+            uint4 f[kUnit];
+            unit_load<Q8, CACHED>(pick(in_a, vA, vB), two, rank + li * P, li, wc, sb0, nb, lane, f);
+            unit_act(x, xo, two, sb0, nb, ah, al);
+            acc = unit_mma<Q8>(f, ah, al, two, sb0, acc);
+            if (++c == S || u + 1 == c1) {   // this item's last unit in this wave
+                red[(item + wave) * kWave + lane] = acc;
+                acc = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+            if (c == S) {
+                c = 0;
+                ++item;
+            }
         }
     }
     TL(2);
 }
 
-// Sum each item's partials in wave order and run epi(item, acc); items are
-// dealt round robin over the waves.  Brackets the LDS traffic with barriers.
-template <class EpiFn>
+// Sum each item's partials (K-major: in K order; item-major: in wave order)
+// and run epi(item, acc); items are dealt round robin over the waves.
+// Brackets the LDS traffic with barriers.
+template <bool KMAJ, class EpiFn>
 __device__ __forceinline__ void phase_reduce(int n_items, int S, const f32x4 *red, EpiFn epi) {
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int N = n_items * S;
@@ -667,9 +699,13 @@ __device__ __forceinline__ void phase_reduce(int n_items, int S, const f32x4 *re
     TL(3);
     for (int it = wave; it < n_items; it += kWaves) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int w = 0; w < kWaves; ++w) {
-            const int a0 = wave_cut(N, w), a1 = wave_cut(N, w + 1);
-            if (a0 < a1 && a0 < (it + 1) * S && a1 > it * S) acc += red[(it + w) * kWave + lane];
+        if (KMAJ) {
+            for (int c = 0; c < S; ++c) acc += red[(it * S + c) * kWave + lane];
+        } else {
+            for (int w = 0; w < kWaves; ++w) {
+                const int a0 = wave_cut(N, w), a1 = wave_cut(N, w + 1);
+                if (a0 < a1 && a0 < (it + 1) * S && a1 > it * S) acc += red[(it + w) * kWave + lane];
+            }
         }
         epi(it, acc);
     }
@@ -679,21 +715,27 @@ __device__ __forceinline__ void phase_reduce(int n_items, int S, const f32x4 *re
 }
 
 // Products of one phase for this workgroup, then the epilogue per item.
-template <class EpiFn>
-__device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
-                                          const Act &x, f32x4 *red, const unsigned char *wc, EpiFn epi) {
-    if (n_items <= 0) return;
+template <bool KMAJ, class EpiFn>
+__device__ __forceinline__ void run_phase_(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
+                                           const Act &x, f32x4 *red, const unsigned char *wc, EpiFn epi) {
     // the LDS weight cache holds every step matrix or none
     const bool cached = wc != nullptr && A.lds_off >= 0;
     if (A.type == PK_TYPE_Q8_0) {
-        if (cached) phase_partials<true, true>(A, n_a, Bm, n_items, rank, P, x, red, wc);
-        else phase_partials<true, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+        if (cached) phase_partials<true, true, KMAJ>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+        else phase_partials<true, false, KMAJ>(A, n_a, Bm, n_items, rank, P, x, red, wc);
     } else {
-        if (cached) phase_partials<false, true>(A, n_a, Bm, n_items, rank, P, x, red, wc);
-        else phase_partials<false, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+        if (cached) phase_partials<false, true, KMAJ>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+        else phase_partials<false, false, KMAJ>(A, n_a, Bm, n_items, rank, P, x, red, wc);
     }
     const int KBe = A.type == PK_TYPE_F32 ? 2 * A.KB : A.KB;
-    phase_reduce(n_items, (KBe + kUnit - 1) / kUnit, red, epi);
+    phase_reduce<KMAJ>(n_items, (KBe + kUnit - 1) / kUnit, red, epi);
+}
+template <class EpiFn>
+__device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
+                                          const Act &x, f32x4 *red, const unsigned char *wc, bool kmajor, EpiFn epi) {
+    if (n_items <= 0) return;
+    if (kmajor) run_phase_<true>(A, n_a, Bm, n_items, rank, P, x, red, wc, epi);
+    else run_phase_<false>(A, n_a, Bm, n_items, rank, P, x, red, wc, epi);
 }
 
 // Tiles of a matrix with `tiles` row tiles owned by rank r of P: t = r, r+P, ...
@@ -777,23 +819,20 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         const float bb = u < nc ? s.bbias[s.jst[c0 + u]] : 0.0f;
         // (b_out is zero-padded to whole tiles)
         const __amdgpu_buffer_rsrc_t rbo = rsrc(p.b_out, (unsigned)p.w_out.tiles * kTile * 4u);
-        float4 pre_b[2];
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int it = wave + k * kWaves;
-            const int row0 = (s.rank + it * s.P) * kTile + (lane >> 4) * 4;
-            pre_b[k] = ld4(rbo, it < n_out ? (unsigned)row0 * 4u : kBad);
-        }
+        const int row_b0 = (s.rank + wave * s.P) * kTile + (lane >> 4) * 4;
+        const int row_b1 = (s.rank + (wave + kWaves) * s.P) * kTile + (lane >> 4) * 4;
+        const float4 pre_b0 = ld4(rbo, wave < n_out ? (unsigned)row_b0 * 4u : kBad);
+        const float4 pre_b1 = ld4(rbo, wave + kWaves < n_out ? (unsigned)row_b1 * 4u : kBad);
         TL(1);
         // each lane keeps its best key per head over all its rows; lanes of one
         // column then combine, and one LDS atomic per column and head follows
         unsigned long long best0 = 0ull, best1 = 0ull;
-        run_phase(p.w_out, n_out, p.w_out, n_out, s.rank, s.P, x, S.red, S.wcache,
+        run_phase(p.w_out, n_out, p.w_out, n_out, s.rank, s.P, x, S.red, S.wcache, p.kmajor != 0,
                   [&](int k, f32x4 acc) {
                       if (u >= nc) return;
                       const int tile = s.rank + k * s.P;
                       const int kk = (k - wave) / kWaves;
-                      const float4 bias4 = kk == 0 ? pre_b[0] : kk == 1 ? pre_b[1]
+                      const float4 bias4 = kk == 0 ? pre_b0 : kk == 1 ? pre_b1
                                                    : ld4(rbo, (unsigned)(tile * kTile + (lane >> 4) * 4) * 4u);
 #pragma unroll
                       for (int i = 0; i < 4; ++i) {
@@ -909,27 +948,22 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
     // this lane's utterance (a valid index for every lane; lanes u >= nc store nothing)
     const int ul = s.lst[c0 + min(u, nc - 1)], b = s.b[ul], cur = s.cur[ul];
     const bool zero = s.flags[ul] & kFlagZeroHC;
-    // Epilogue operands of this wave's first kPre consumer items -- the bias
-    // rows and, for an LSTM layer, R and c_prev, written one step earlier --
-    // loaded before the products.  Lane rows row0 .. row0+3 are the pred rows,
-    // or the four gates of unit j = row0 / 4.  Unused loads take an offset past
-    // the buffer and return 0: no branches, so nothing waits for them early.
-    constexpr int kPre = 3;
+    // Epilogue operands of this wave's first consumer item -- the bias rows
+    // and, for an LSTM layer, R and c_prev, written one step earlier -- loaded
+    // before the products (one item per wave covers every workgroup count of
+    // 32 and more; later items load theirs in the epilogue).  Lane rows
+    // row0 .. row0+3 are the pred rows, or the four gates of unit j = row0 / 4.
+    // Unused loads take an offset past the buffer and return 0: no branches,
+    // so nothing waits for them early.
     const __amdgpu_buffer_rsrc_t rb = rsrc(last ? p.b_pred : p.b_lstm[layer], (unsigned)(last ? p.J : 4 * H) * 4u);
-    float4 pre_r[kPre], pre_b[kPre];
-    float pre_c[kPre];
-#pragma unroll
-    for (int k = 0; k < kPre; ++k) {
-        const int it = wave + k * kWaves;
-        const int row0 = (s.rank + it * s.P) * kTile + (lane >> 4) * 4;
-        const bool ok = it < n_c && u < nc;
-        const bool st = ok && !last && !zero;
-        pre_b[k] = ld4(rb, ok ? (unsigned)row0 * 4u : kBad);
-        pre_r[k] = ld4_coh(B.rx, st ? (unsigned)((rx_off(p, cur, layer, b) + row0) * 4) : kBad);
-        pre_c[k] = ld1_coh(B.cx, st ? (unsigned)((hx_off(p, cur, layer, b) + row0 / 4) * 4) : kBad);
-    }
+    const unsigned r_base = (unsigned)rx_off(p, cur, layer, b), c_base = (unsigned)hx_off(p, cur, layer, b);
+    const unsigned w0 = (unsigned)((s.rank + wave * s.P) * kTile + (lane >> 4) * 4);
+    const bool ok0 = wave < n_c && u < nc, st0 = ok0 && !last && !zero;
+    const float4 pb0 = ld4(rb, ok0 ? w0 * 4u : kBad);
+    const float4 pr0 = ld4_coh(B.rx, st0 ? (r_base + w0) * 4u : kBad);
+    const float pc0 = ld1_coh(B.cx, st0 ? (c_base + w0 / 4) * 4u : kBad);
     TL(1);
-    run_phase(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache,
+    run_phase(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache, p.kmajor != 0,
               [&](int it, f32x4 acc) {
                   if (u >= nc) return;
                   if (it >= n_c) {          // recurrent product for the next step
@@ -939,18 +973,17 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
                       return;
                   }
                   const int row0 = (s.rank + it * s.P) * kTile + (lane >> 4) * 4;
-                  const int k = (it - wave) / kWaves;
                   float4 bias, r;
                   float c_prev;
-                  if (k < kPre) {
-                      bias = k == 0 ? pre_b[0] : k == 1 ? pre_b[1] : pre_b[2];
-                      r = k == 0 ? pre_r[0] : k == 1 ? pre_r[1] : pre_r[2];
-                      c_prev = k == 0 ? pre_c[0] : k == 1 ? pre_c[1] : pre_c[2];
+                  if (it == wave) {
+                      bias = pb0;
+                      r = pr0;
+                      c_prev = pc0;
                   } else {
                       const bool st = !last && !zero;
                       bias = ld4(rb, (unsigned)row0 * 4u);
-                      r = ld4_coh(B.rx, st ? (unsigned)((rx_off(p, cur, layer, b) + row0) * 4) : kBad);
-                      c_prev = ld1_coh(B.cx, st ? (unsigned)((hx_off(p, cur, layer, b) + row0 / 4) * 4) : kBad);
+                      r = ld4_coh(B.rx, st ? (r_base + row0) * 4u : kBad);
+                      c_prev = ld1_coh(B.cx, st ? (c_base + row0 / 4) * 4u : kBad);
                   }
                   if (last) {               // pred projection: rows row0 .. row0+3 of pp
                       st4_coh(B.ppx, (unsigned)(((size_t)b * p.J + row0) * 4),
