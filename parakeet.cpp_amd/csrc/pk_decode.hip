@@ -790,6 +790,11 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         HIP_TRY(hipMemsetAsync(dec->d_prof.p, 0, (pkdev::kPrN + 9 * pkdev::kTl) * 8, dec->stream));
         p.prof = dec->d_prof.as<unsigned long long>();
     }
+    // LDS state of layers >= 1 (R and c of each workgroup's unit tiles)
+    p.st_n = *std::max_element(pl.dom_n.begin(), pl.dom_n.end());
+    p.st_k = p.L > 1 ? (p.w_hh[1].tiles + pl.P - 1) / pl.P : 0;
+    const size_t st_bytes = (size_t)(p.L - 1) * p.st_n * p.st_k * pkdev::kStFloats * 4;
+    const size_t lds_base = dec->lds_fixed + st_bytes;
     // LDS partial slots.  K-major unit order (activation fragments reused
     // across a workgroup's tiles) needs one slot per unit of the largest
     // phase; item-major needs the most items of any phase plus one per wave.
@@ -806,10 +811,10 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
             most = std::max(most, items(c) + items(p.w_hh[l]));
             kslots = std::max(kslots, (items(c) + items(p.w_hh[l])) * units(c));
         }
-        p.kmajor = dec->lds_fixed + (size_t)kslots * kWave * 16 <= dec->lds_bytes ? 1 : 0;
+        p.kmajor = lds_base + (size_t)kslots * kWave * 16 <= dec->lds_bytes ? 1 : 0;
         p.red_slots = p.kmajor ? kslots : most + kWaves;
     }
-    size_t lds = dec->lds_fixed + (size_t)p.red_slots * kWave * 16;
+    size_t lds = lds_base + (size_t)p.red_slots * kWave * 16;
     if (lds > dec->lds_bytes)
         return fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed for %d workgroups per domain, %zu available", lds, pl.P,
                     dec->lds_bytes);

@@ -108,6 +108,7 @@ struct KParams {
     int max_iter;
     int red_slots;               // LDS partial slots (K-major: items x units per item of the largest phase)
     int kmajor;                  // unit order of every phase: 1 K-major, 0 item-major
+    int st_n, st_k;              // LDS state of layers >= 1: utterance and owned-tile capacity
     int wcache_bytes;            // LDS weight cache per workgroup (0: weights are read from L2)
     unsigned long long *prof;    // nullable: per-phase wall-clock totals of workgroup 0 (100 MHz ticks)
 };
@@ -741,8 +742,17 @@ __device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm
 // Tiles of a matrix with `tiles` row tiles owned by rank r of P: t = r, r+P, ...
 __device__ __forceinline__ int owned(int tiles, int r, int P) { return tiles > r ? (tiles - r + P - 1) / P : 0; }
 
+// LSTM state of layers >= 1 kept in LDS by the workgroup that owns the units:
+// for layer l, utterance ul (domain index) and owned tile k (tile rank + kP,
+// units 4t .. 4t+3): R_l rows 16t .. 16t+15 (W_hh_l . h_l, unit-major), then
+// c_l of the 4 units.  Those units' gates are produced (the recurrent product
+// of the phase that consumes h_l) and consumed (the cell update) by the same
+// workgroup, so they never travel through memory inside a launch.
+constexpr int kStFloats = kTile + 4;
+
 struct Lds {
     Act act[1 + PK_MAX_LAYERS];   // staged activation blocks
+    float *st;                    // [L-1][st_n][st_k][kStFloats] LDS state of layers >= 1
     f32x4 *red;                   // [red_slots][kWave] per-(item, wave) partials
     const unsigned char *wcache;  // weight cache (nullptr when the tiles do not fit)
 };
@@ -937,6 +947,11 @@ __device__ __forceinline__ void lstm_layer0(const KParams &p, Ctl &s, const Lds 
 //                    (stored in the other ping-pong half of rx).
 // Column tile: utterances lst[c0 .. c0+nc).
 // Both matrices have K = H and the same storage type.
+// LDS state of layer l (>= 1), utterance ul, owned tile k.
+__device__ __forceinline__ float *st_at(const KParams &p, const Lds &S, int l, int ul, int k) {
+    return S.st + ((size_t)((l - 1) * p.st_n + ul) * p.st_k + k) * kStFloats;
+}
+
 __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Lds &S, const Bufs &B, const Act &x,
                                               int lc, int c0, int nc) {
     const int lane = threadIdx.x & (kWave - 1), H = p.H;
@@ -944,58 +959,53 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
     const TMat &wc = last ? p.w_pred : p.w_ih[lc + 1];
     const TMat &wr = p.w_hh[lc];
     const int n_c = owned(wc.tiles, s.rank, s.P), n_r = owned(wr.tiles, s.rank, s.P);
-    const int wave = threadIdx.x / kWave, layer = lc + 1, u = lane & 15;
+    const int wave = threadIdx.x / kWave, layer = lc + 1, u = lane & 15, g = lane >> 4;
     // this lane's utterance (a valid index for every lane; lanes u >= nc store nothing)
     const int ul = s.lst[c0 + min(u, nc - 1)], b = s.b[ul], cur = s.cur[ul];
     const bool zero = s.flags[ul] & kFlagZeroHC;
-    // Epilogue operands of this wave's first consumer item -- the bias rows
-    // and, for an LSTM layer, R and c_prev, written one step earlier -- loaded
-    // before the products (one item per wave covers every workgroup count of
-    // 32 and more; later items load theirs in the epilogue).  Lane rows
+    // The bias rows of this wave's first consumer item, loaded before the
+    // products (later items load theirs in the epilogue).  Lane rows
     // row0 .. row0+3 are the pred rows, or the four gates of unit j = row0 / 4.
-    // Unused loads take an offset past the buffer and return 0: no branches,
-    // so nothing waits for them early.
+    // Unused loads take an offset past the buffer and return 0.
     const __amdgpu_buffer_rsrc_t rb = rsrc(last ? p.b_pred : p.b_lstm[layer], (unsigned)(last ? p.J : 4 * H) * 4u);
-    const unsigned r_base = (unsigned)rx_off(p, cur, layer, b), c_base = (unsigned)hx_off(p, cur, layer, b);
-    const unsigned w0 = (unsigned)((s.rank + wave * s.P) * kTile + (lane >> 4) * 4);
-    const bool ok0 = wave < n_c && u < nc, st0 = ok0 && !last && !zero;
-    const float4 pb0 = ld4(rb, ok0 ? w0 * 4u : kBad);
-    const float4 pr0 = ld4_coh(B.rx, st0 ? (r_base + w0) * 4u : kBad);
-    const float pc0 = ld1_coh(B.cx, st0 ? (c_base + w0 / 4) * 4u : kBad);
+    const unsigned w0 = (unsigned)((s.rank + wave * s.P) * kTile + g * 4);
+    const float4 pb0 = ld4(rb, wave < n_c && u < nc ? w0 * 4u : kBad);
     TL(1);
     run_phase(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache, p.kmajor != 0,
               [&](int it, f32x4 acc) {
                   if (u >= nc) return;
                   if (it >= n_c) {          // recurrent product for the next step
-                      const int row0 = (s.rank + (it - n_c) * s.P) * kTile + (lane >> 4) * 4;
-                      st4_coh(B.rx, (unsigned)((rx_off(p, cur ^ 1, lc, b) + row0) * 4),
-                              make_float4(acc[0], acc[1], acc[2], acc[3]));
+                      const int k = it - n_c;
+                      if (lc == 0) {        // R_0: read by the layer-0 update of every workgroup (global)
+                          const int row0 = (s.rank + k * s.P) * kTile + g * 4;
+                          st4_coh(B.rx, (unsigned)((rx_off(p, cur ^ 1, 0, b) + row0) * 4),
+                                  make_float4(acc[0], acc[1], acc[2], acc[3]));
+                      } else {              // R_lc: LDS state of this workgroup
+                          *reinterpret_cast<float4 *>(st_at(p, S, lc, ul, k) + g * 4) =
+                              make_float4(acc[0], acc[1], acc[2], acc[3]);
+                      }
                       return;
                   }
-                  const int row0 = (s.rank + it * s.P) * kTile + (lane >> 4) * 4;
-                  float4 bias, r;
-                  float c_prev;
-                  if (it == wave) {
-                      bias = pb0;
-                      r = pr0;
-                      c_prev = pc0;
-                  } else {
-                      const bool st = !last && !zero;
-                      bias = ld4(rb, (unsigned)row0 * 4u);
-                      r = ld4_coh(B.rx, st ? (r_base + row0) * 4u : kBad);
-                      c_prev = ld1_coh(B.cx, st ? (c_base + row0 / 4) * 4u : kBad);
-                  }
+                  const int row0 = (s.rank + it * s.P) * kTile + g * 4;
+                  const float4 bias = it == wave ? pb0 : ld4(rb, (unsigned)row0 * 4u);
                   if (last) {               // pred projection: rows row0 .. row0+3 of pp
                       st4_coh(B.ppx, (unsigned)(((size_t)b * p.J + row0) * 4),
                               make_float4(acc[0] + bias.x, acc[1] + bias.y, acc[2] + bias.z, acc[3] + bias.w));
                       return;
                   }
-                  const int j = row0 / 4;
+                  // cell update of unit j = row0 / 4 of layer `layer`: R and c_prev from the LDS state
+                  float *st = st_at(p, S, layer, ul, it);
+                  float4 r = *reinterpret_cast<const float4 *>(st + g * 4);
+                  float c_prev = st[kTile + g];
+                  if (zero) {
+                      r = make_float4(0.f, 0.f, 0.f, 0.f);
+                      c_prev = 0.0f;
+                  }
                   float c_new, h_new;
                   cell((acc[0] + r.x) + bias.x, (acc[1] + r.y) + bias.y, (acc[2] + r.z) + bias.z,
                        (acc[3] + r.w) + bias.w, c_prev, c_new, h_new);
-                  st_coh(p.cx + hx_off(p, cur ^ 1, layer, b) + j, c_new);
-                  st_coh(p.hx + hx_off(p, cur ^ 1, layer, b) + j, h_new);
+                  st[kTile + g] = c_new;
+                  st_coh(p.hx + hx_off(p, cur ^ 1, layer, b) + row0 / 4, h_new);
               });
 }
 
@@ -1192,6 +1202,8 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
             S.act[a].n = kTile;
         }
         q += (size_t)kTile * ((J > H ? J : H) + kKPad) * 2 * 2;
+        S.st = reinterpret_cast<float *>(q);
+        q += (size_t)(L - 1) * p.st_n * p.st_k * kStFloats * 4;
         S.red = reinterpret_cast<f32x4 *>(q);
         q += (size_t)p.red_slots * kWave * sizeof(f32x4);
         if (p.wcache_bytes > 0) wcache = q;
@@ -1240,12 +1252,23 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         for (int i = threadIdx.x; i < L * H; i += kBlock) {
             const int l = i / H, k = i - l * H;
             st_coh(p.hx + hx_off(p, 0, l, b) + k, p.slot_h[(size_t)slot * L * H + i]);
-            st_coh(p.cx + hx_off(p, 0, l, b) + k, p.slot_c[(size_t)slot * L * H + i]);
         }
+        for (int i = threadIdx.x; i < H; i += kBlock)   // layer 0; layers >= 1 go to the LDS state
+            st_coh(p.cx + hx_off(p, 0, 0, b) + i, p.slot_c[(size_t)slot * L * H + i]);
         for (int i = threadIdx.x; i < J; i += kBlock) st_coh(p.ppx + (size_t)b * J + i, p.slot_pp[(size_t)slot * J + i]);
-        for (int i = threadIdx.x; i < L * 4 * H; i += kBlock) {
-            const int l = i / (4 * H), k = i - l * 4 * H;
-            st_coh(p.rx + rx_off(p, 0, l, b) + k, p.slot_r[(size_t)slot * L * 4 * H + i]);
+        for (int i = threadIdx.x; i < 4 * H; i += kBlock)
+            st_coh(p.rx + rx_off(p, 0, 0, b) + i, p.slot_r[(size_t)slot * L * 4 * H + i]);
+    }
+    // LDS state of layers >= 1: R and c of this workgroup's unit tiles for every utterance of the domain
+    if (L > 1) {
+        const int n_own = owned(p.w_hh[1].tiles, s.rank, s.P);
+        const int n_st = (L - 1) * s.n * n_own * kStFloats;
+        for (int i = threadIdx.x; i < n_st; i += kBlock) {
+            const int e = i % kStFloats, k = (i / kStFloats) % n_own, ul = (i / kStFloats / n_own) % s.n;
+            const int l = 1 + i / (kStFloats * n_own * s.n);
+            const int slot = p.slot[s.b[ul]], t = s.rank + k * s.P;
+            st_at(p, S, l, ul, k)[e] = e < kTile ? p.slot_r[((size_t)slot * L + l) * 4 * H + t * kTile + e]
+                                                 : p.slot_c[((size_t)slot * L + l) * H + t * 4 + (e - kTile)];
         }
     }
     if (wcache) {      // this workgroup's weight tiles, read from LDS for the whole launch
@@ -1301,19 +1324,30 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
 #endif
     if (!ok) return;
 
+    if (L > 1) {       // layers >= 1: R and c of this workgroup's unit tiles, from its LDS state
+        const int n_own = owned(p.w_hh[1].tiles, s.rank, s.P);
+        const int n_st = (L - 1) * s.n * n_own * kStFloats;
+        for (int i = threadIdx.x; i < n_st; i += kBlock) {
+            const int e = i % kStFloats, k = (i / kStFloats) % n_own, ul = (i / kStFloats / n_own) % s.n;
+            const int l = 1 + i / (kStFloats * n_own * s.n);
+            const int slot = p.slot[s.b[ul]], t = s.rank + k * s.P;
+            const float v = st_at(p, S, l, ul, k)[e];
+            if (e < kTile) p.slot_r[((size_t)slot * L + l) * 4 * H + t * kTile + e] = v;
+            else p.slot_c[((size_t)slot * L + l) * H + t * 4 + (e - kTile)] = v;
+        }
+    }
     for (int ul = s.rank; ul < s.n; ul += s.P) {
         const int b = s.b[ul], slot = p.slot[b];
         const int cur = s.cur[ul];
         for (int i = threadIdx.x; i < L * H; i += kBlock) {
             const int l = i / H, k = i - l * H;
             p.slot_h[(size_t)slot * L * H + i] = ld_coh(p.hx + hx_off(p, cur, l, b) + k);
-            p.slot_c[(size_t)slot * L * H + i] = ld_coh(p.cx + hx_off(p, cur, l, b) + k);
         }
+        for (int i = threadIdx.x; i < H; i += kBlock)   // layer 0; layers >= 1 come from the LDS state
+            p.slot_c[(size_t)slot * L * H + i] = ld_coh(p.cx + hx_off(p, cur, 0, b) + i);
         for (int i = threadIdx.x; i < J; i += kBlock) p.slot_pp[(size_t)slot * J + i] = ld_coh(p.ppx + (size_t)b * J + i);
-        for (int i = threadIdx.x; i < L * 4 * H; i += kBlock) {
-            const int l = i / (4 * H), k = i - l * 4 * H;
-            p.slot_r[(size_t)slot * L * 4 * H + i] = ld_coh(p.rx + rx_off(p, cur, l, b) + k);
-        }
+        for (int i = threadIdx.x; i < 4 * H; i += kBlock)
+            p.slot_r[(size_t)slot * L * 4 * H + i] = ld_coh(p.rx + rx_off(p, cur, 0, b) + i);
         if (threadIdx.x == 0) {
             int *ctrl = p.slot_ctrl + (size_t)slot * PK_CTRL_N;
             ctrl[PK_CTRL_INIT] = 1;
