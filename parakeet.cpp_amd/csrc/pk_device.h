@@ -690,8 +690,9 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
 }
 
 // Sum each item's partials (K-major: in K order; item-major: in wave order)
-// and run epi(item, acc); items are dealt round robin over the waves.
-// Brackets the LDS traffic with barriers.
+// and run epi(item, acc); items are dealt round robin over the waves.  Opens
+// with a barrier (all partials written); the caller's next barrier (before any
+// new partials or staging) closes it.
 template <bool KMAJ, class EpiFn>
 __device__ __forceinline__ void phase_reduce(int n_items, int S, const f32x4 *red, EpiFn epi) {
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
@@ -711,8 +712,6 @@ __device__ __forceinline__ void phase_reduce(int n_items, int S, const f32x4 *re
         epi(it, acc);
     }
     TL(4);
-    lds_sync();
-    TL(5);
 }
 
 // Products of one phase for this workgroup, then the epilogue per item.
@@ -1041,7 +1040,6 @@ __device__ __forceinline__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bu
             TL(0);
             pmark(p, s, tlast, kPrStageL);
             consume_layer(p, s, S, B, x, lc, c0, nc);
-            lds_sync();
             TL(6);
         }
         pmark(p, s, tlast, lc == L - 1 ? kPrPred : kPrL1);
