@@ -794,7 +794,14 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     p.st_n = *std::max_element(pl.dom_n.begin(), pl.dom_n.end());
     p.st_k = p.L > 1 ? (p.w_hh[1].tiles + pl.P - 1) / pl.P : 0;
     const size_t st_bytes = (size_t)(p.L - 1) * p.st_n * p.st_k * pkdev::kStFloats * 4;
-    const size_t lds_base = dec->lds_fixed + st_bytes;
+    // LDS bias table: 16 rows per owned tile of W_ih_l (l >= 1), W_p and W_o
+    {
+        auto own = [&](const pkdev::TMat &m) { return (m.tiles + pl.P - 1) / pl.P; };
+        int rows = own(p.w_pred) + own(p.w_out);
+        for (int l = 1; l < p.L; ++l) rows += own(p.w_ih[l]);
+        p.bias_floats = rows * kTile;
+    }
+    const size_t lds_base = dec->lds_fixed + st_bytes + (size_t)p.bias_floats * 4;
     // LDS partial slots.  K-major unit order (activation fragments reused
     // across a workgroup's tiles) needs one slot per unit of the largest
     // phase; item-major needs the most items of any phase plus one per wave.

@@ -109,6 +109,7 @@ struct KParams {
     int red_slots;               // LDS partial slots (K-major: items x units per item of the largest phase)
     int kmajor;                  // unit order of every phase: 1 K-major, 0 item-major
     int st_n, st_k;              // LDS state of layers >= 1: utterance and owned-tile capacity
+    int bias_floats;             // LDS bias table size (floats)
     int wcache_bytes;            // LDS weight cache per workgroup (0: weights are read from L2)
     unsigned long long *prof;    // nullable: per-phase wall-clock totals of workgroup 0 (100 MHz ticks)
 };
@@ -752,9 +753,40 @@ constexpr int kStFloats = kTile + 4;
 struct Lds {
     Act act[1 + PK_MAX_LAYERS];   // staged activation blocks
     float *st;                    // [L-1][st_n][st_k][kStFloats] LDS state of layers >= 1
+    float *bias;                  // epilogue bias rows of this workgroup's tiles (see bias_table)
     f32x4 *red;                   // [red_slots][kWave] per-(item, wave) partials
     const unsigned char *wcache;  // weight cache (nullptr when the tiles do not fit)
 };
+
+// Epilogue bias rows of this workgroup's tiles, in LDS for the whole launch:
+// the 16 rows of each owned tile of W_ih_l (b_ih_l + b_hh_l, l = 1 .. L-1;
+// 4H/16 tiles each), then of W_p (b_p; J/16 tiles), then of W_o (b_o).
+// bias_base gives the table offset (floats) of matrix index m (0 .. L-2
+// LSTM, L-1 pred, L joint).
+__device__ __forceinline__ int bias_base(const KParams &p, int rank, int P, int m) {
+    const int n_lstm = owned(p.H / 4, rank, P), n_pred = owned(p.J / kTile, rank, P);   // 4H/16 and J/16 tiles
+    return kTile * (m < p.L ? m * n_lstm : (p.L - 1) * n_lstm + n_pred);
+}
+__device__ __forceinline__ void bias_table(const KParams &p, int rank, int P, float *tab) {
+    const int n_lstm = owned(p.H / 4, rank, P), n_pred = owned(p.J / kTile, rank, P);
+    const int n_out = owned(p.w_out.tiles, rank, P);
+    const int nl = (p.L - 1) * n_lstm * kTile, np = n_pred * kTile, no = n_out * kTile;
+    for (int i = threadIdx.x; i < nl + np + no; i += kBlock) {
+        float v;
+        if (i < nl) {
+            const int l = 1 + i / (n_lstm * kTile), r = i % (n_lstm * kTile);
+            v = p.b_lstm[l][(rank + (r / kTile) * P) * kTile + r % kTile];
+        } else if (i < nl + np) {
+            const int r = i - nl;
+            v = p.b_pred[(rank + (r / kTile) * P) * kTile + r % kTile];
+        } else {
+            const int r = i - nl - np;
+            const int row = (rank + (r / kTile) * P) * kTile + r % kTile;
+            v = row < p.Vo ? p.b_out[row] : 0.0f;
+        }
+        tab[i] = v;
+    }
+}
 
 // Copy this workgroup's tiles of m (rank, rank+P, ...) into its LDS cache:
 // per K block the fragment, then (q8_0) the 16 block scales.
@@ -827,11 +859,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         const int u = lane & 15, wave = threadIdx.x / kWave;
         const float bb = u < nc ? s.bbias[s.jst[c0 + u]] : 0.0f;
         // (b_out is zero-padded to whole tiles)
-        const __amdgpu_buffer_rsrc_t rbo = rsrc(p.b_out, (unsigned)p.w_out.tiles * kTile * 4u);
-        const int row_b0 = (s.rank + wave * s.P) * kTile + (lane >> 4) * 4;
-        const int row_b1 = (s.rank + (wave + kWaves) * s.P) * kTile + (lane >> 4) * 4;
-        const float4 pre_b0 = ld4(rbo, wave < n_out ? (unsigned)row_b0 * 4u : kBad);
-        const float4 pre_b1 = ld4(rbo, wave + kWaves < n_out ? (unsigned)row_b1 * 4u : kBad);
+        const float *btab = S.bias + bias_base(p, s.rank, s.P, p.L);
         TL(1);
         // each lane keeps its best key per head over all its rows; lanes of one
         // column then combine, and one LDS atomic per column and head follows
@@ -840,9 +868,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
                   [&](int k, f32x4 acc) {
                       if (u >= nc) return;
                       const int tile = s.rank + k * s.P;
-                      const int kk = (k - wave) / kWaves;
-                      const float4 bias4 = kk == 0 ? pre_b0 : kk == 1 ? pre_b1
-                                                   : ld4(rbo, (unsigned)(tile * kTile + (lane >> 4) * 4) * 4u);
+                      const float4 bias4 = *reinterpret_cast<const float4 *>(btab + k * kTile + (lane >> 4) * 4);
 #pragma unroll
                       for (int i = 0; i < 4; ++i) {
                           const int row = tile * kTile + (lane >> 4) * 4 + i;
@@ -962,13 +988,9 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
     // this lane's utterance (a valid index for every lane; lanes u >= nc store nothing)
     const int ul = s.lst[c0 + min(u, nc - 1)], b = s.b[ul], cur = s.cur[ul];
     const bool zero = s.flags[ul] & kFlagZeroHC;
-    // The bias rows of this wave's first consumer item, loaded before the
-    // products (later items load theirs in the epilogue).  Lane rows
-    // row0 .. row0+3 are the pred rows, or the four gates of unit j = row0 / 4.
-    // Unused loads take an offset past the buffer and return 0.
-    const __amdgpu_buffer_rsrc_t rb = rsrc(last ? p.b_pred : p.b_lstm[layer], (unsigned)(last ? p.J : 4 * H) * 4u);
-    const unsigned w0 = (unsigned)((s.rank + wave * s.P) * kTile + g * 4);
-    const float4 pb0 = ld4(rb, wave < n_c && u < nc ? w0 * 4u : kBad);
+    // bias rows of the consumer tiles (LDS table): lane rows row0 .. row0+3 are
+    // the pred rows, or the four gates of unit j = row0 / 4
+    const float *btab = S.bias + bias_base(p, s.rank, s.P, layer - 1);
     TL(1);
     run_phase(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache, p.kmajor != 0,
               [&](int it, f32x4 acc) {
@@ -986,7 +1008,7 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
                       return;
                   }
                   const int row0 = (s.rank + it * s.P) * kTile + g * 4;
-                  const float4 bias = it == wave ? pb0 : ld4(rb, (unsigned)row0 * 4u);
+                  const float4 bias = *reinterpret_cast<const float4 *>(btab + it * kTile + g * 4);
                   if (last) {               // pred projection: rows row0 .. row0+3 of pp
                       st4_coh(B.ppx, (unsigned)(((size_t)b * p.J + row0) * 4),
                               make_float4(acc[0] + bias.x, acc[1] + bias.y, acc[2] + bias.z, acc[3] + bias.w));
@@ -1202,6 +1224,8 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         q += (size_t)kTile * ((J > H ? J : H) + kKPad) * 2 * 2;
         S.st = reinterpret_cast<float *>(q);
         q += (size_t)(L - 1) * p.st_n * p.st_k * kStFloats * 4;
+        S.bias = reinterpret_cast<float *>(q);
+        q += (size_t)p.bias_floats * 4;
         S.red = reinterpret_cast<f32x4 *>(q);
         q += (size_t)p.red_slots * kWave * sizeof(f32x4);
         if (p.wcache_bytes > 0) wcache = q;
@@ -1257,6 +1281,7 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         for (int i = threadIdx.x; i < 4 * H; i += kBlock)
             st_coh(p.rx + rx_off(p, 0, 0, b) + i, p.slot_r[(size_t)slot * L * 4 * H + i]);
     }
+    bias_table(p, s.rank, s.P, S.bias);
     // LDS state of layers >= 1: R and c of this workgroup's unit tiles for every utterance of the domain
     if (L > 1) {
         const int n_own = owned(p.w_hh[1].tiles, s.rank, s.P);
