@@ -825,25 +825,29 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     if (lds > dec->lds_bytes)
         return fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed for %d workgroups per domain, %zu available", lds, pl.P,
                     dec->lds_bytes);
-    // LDS weight cache: when every workgroup's tiles of all step matrices fit,
-    // they are copied into LDS once per launch and read from there
+    // LDS weight cache, phase by phase: the matrices of a phase (the two that
+    // consume one layer's output, or W_o) are copied into LDS once per launch
+    // when the workgroup's tiles of both fit; the LSTM phases are tried first
+    // (smaller), then the joint.  A phase whose tiles do not fit reads them from L2.
     {
-        std::vector<pkdev::TMat *> mats;
-        for (int l = 1; l < p.L; ++l) mats.push_back(&p.w_ih[l]);
-        for (int l = 0; l < p.L; ++l) mats.push_back(&p.w_hh[l]);
-        mats.push_back(&p.w_pred);
-        mats.push_back(&p.w_out);
-        size_t cache = 0;
-        for (auto *m : mats)
-            cache += (size_t)((m->tiles + pl.P - 1) / pl.P) * m->KB * pkdev::cache_block_bytes(m->type);
-        const bool fits = lds + cache <= dec->lds_bytes;
+        std::vector<std::vector<pkdev::TMat *>> phases;
+        for (int lc = 0; lc < p.L; ++lc) phases.push_back({lc + 1 < p.L ? &p.w_ih[lc + 1] : &p.w_pred, &p.w_hh[lc]});
+        phases.push_back({&p.w_out});
+        auto bytes = [&](const pkdev::TMat *m) {
+            return (size_t)((m->tiles + pl.P - 1) / pl.P) * m->KB * pkdev::cache_block_bytes(m->type);
+        };
         size_t off = 0;
-        for (auto *m : mats) {
-            m->lds_off = fits ? (int)off : -1;
-            off += (size_t)((m->tiles + pl.P - 1) / pl.P) * m->KB * pkdev::cache_block_bytes(m->type);
+        for (auto &ph : phases) {
+            size_t need = 0;
+            for (auto *m : ph) need += bytes(m);
+            const bool fits = lds + off + need <= dec->lds_bytes;
+            for (auto *m : ph) {
+                m->lds_off = fits ? (int)off : -1;
+                if (fits) off += bytes(m);
+            }
         }
-        p.wcache_bytes = fits ? (int)cache : 0;
-        if (fits) lds += cache;
+        p.wcache_bytes = (int)off;
+        lds += off;
     }
     void *args[] = {&p};
     HIP_TRY(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(pkdev::decode_loop_kernel), dim3(nwg),

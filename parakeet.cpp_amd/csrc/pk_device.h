@@ -719,7 +719,7 @@ __device__ __forceinline__ void phase_reduce(int n_items, int S, const f32x4 *re
 template <bool KMAJ, class EpiFn>
 __device__ __forceinline__ void run_phase_(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
                                            const Act &x, f32x4 *red, const unsigned char *wc, EpiFn epi) {
-    // the LDS weight cache holds every step matrix or none
+    // both matrices of a phase are in the LDS weight cache or neither
     const bool cached = wc != nullptr && A.lds_off >= 0;
     if (A.type == PK_TYPE_Q8_0) {
         if (cached) phase_partials<true, true, KMAJ>(A, n_a, Bm, n_items, rank, P, x, red, wc);
