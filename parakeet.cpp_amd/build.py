@@ -4,6 +4,7 @@
   libparakeet_decoder.so  C++ decoder API           (csrc/parakeet_decoder.cpp, csrc/gguf_reader.cpp)
   libpk_calib.so          copy kernel of known size (csrc/pk_calib.hip), used by bench.py to scale
                           hardware byte counters
+  tests/cpp/decoder_api_main  test driver of the C++ API (tests/cpp/decoder_api_main.cpp)
 
 Called by __graft_entry__.build(); every call recompiles.
 """
@@ -58,8 +59,20 @@ def build_decoder():
     return out
 
 
+def build_api_test():
+    """tests/cpp/decoder_api_main: drives the C++ API for the GPU tests (not part of the library)."""
+    src = os.path.join(ROOT, "tests", "cpp", "decoder_api_main.cpp")
+    if not os.path.exists(src) or not os.path.exists(os.path.join(HERE, "libparakeet_decoder.so")):
+        return None
+    out = os.path.join(ROOT, "tests", "cpp", "decoder_api_main")
+    _run(["g++", "-O2", "-std=c++17", "-Wall", f"-I{INC}", src, f"-L{HERE}", "-lparakeet_decoder", "-lparakeet_hip",
+          "-Wl,-rpath,$ORIGIN/../../parakeet.cpp_amd", "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build_all():
-    return [build_hip(), build_decoder(), build_calib()]
+    return [build_hip(), build_decoder(), build_calib(), build_api_test()]
 
 
 if __name__ == "__main__":

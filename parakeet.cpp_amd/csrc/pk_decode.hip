@@ -9,7 +9,8 @@
 //                       the same projection as a ggml graph; the CPU path
 //                       recomputes it per step at :167-168).
 //   decode_loop_kernel  all lockstep iterations of all utterances in one
-//                       cooperative launch.  The batch is split into
+//                       launch (cooperative where the runtime grants it;
+//                       see launch_loop).  The batch is split into
 //                       independent domains (16 or 32 utterances, each on
 //                       nwg/C workgroups with its own barrier); one iteration
 //                       of a domain is
@@ -36,6 +37,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <numeric>
 #include <string>
 #include <vector>
@@ -614,6 +617,46 @@ PK_API int pk_decode(pk_decoder *dec, const pk_batch *bt) {
 
 namespace {
 
+// Decode-loop launches of this process, per device: the loop's workgroups
+// wait on one another, so two loops must never share a device.  Every launch
+// waits for the previous one on the same device, whatever stream it was on.
+struct LoopOrder {
+    std::mutex mu;
+    std::map<int, hipEvent_t> last;       // per device: recorded after the latest loop launch
+    std::map<int, bool> coop_refused;     // per device: cooperative launches refused once
+};
+LoopOrder g_loops;
+
+// A cooperative launch guarantees that the whole grid (one workgroup per CU,
+// checked at create) is resident at once.  The runtime refuses it
+// (hipErrorIllegalState) while another process holds the device's
+// cooperative queue.  The loop is then an ordinary dispatch: on a device with
+// no other loop running the grid fits, and the ordering above keeps this
+// process's loops apart.  If a loop of another process overlaps it, the
+// barrier's 2 s limit ends both launches with PK_ERR_TIMEOUT.
+int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds) {
+    std::lock_guard<std::mutex> lk(g_loops.mu);
+    hipEvent_t &last = g_loops.last[dec->device];
+    if (!last) HIP_TRY(hipEventCreateWithFlags(&last, hipEventDisableTiming));
+    HIP_TRY(hipStreamWaitEvent(dec->stream, last, 0));
+    void *args[] = {&p};
+    const void *fn = reinterpret_cast<const void *>(pkdev::decode_loop_kernel);
+    bool &refused = g_loops.coop_refused[dec->device];
+    if (!refused) {
+        const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(nwg), dim3(kBlock), args, lds, dec->stream);
+        if (e != hipErrorIllegalState) {
+            HIP_TRY(e);
+            HIP_TRY(hipEventRecord(last, dec->stream));
+            return 0;
+        }
+        (void)hipGetLastError();
+        refused = true;
+    }
+    HIP_TRY(hipLaunchKernel(fn, dim3(nwg), dim3(kBlock), args, lds, dec->stream));
+    HIP_TRY(hipEventRecord(last, dec->stream));
+    return 0;
+}
+
 int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     if (!dec || !bt) return fail(PK_ERR_ARG, "pk_decode: null argument");
     KParams &p = dec->kp;
@@ -849,9 +892,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         p.wcache_bytes = (int)off;
         lds += off;
     }
-    void *args[] = {&p};
-    HIP_TRY(hipLaunchCooperativeKernel(reinterpret_cast<const void *>(pkdev::decode_loop_kernel), dim3(nwg),
-                                       dim3(kBlock), args, lds, dec->stream));
+    if ((rc = launch_loop(dec, nwg, p, lds))) return rc;
     HIP_TRY(hipEventRecord(dec->ev[2], dec->stream));
     int status[4] = {0, 0, 0, 0};
     HIP_TRY(hipMemcpyAsync(status, p.status, sizeof status, hipMemcpyDeviceToHost, dec->stream));

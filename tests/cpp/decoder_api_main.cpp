@@ -1,0 +1,211 @@
+// Drives the reference-shaped C++ decoder API (include/parakeet_decoder.h) the
+// way parakeet.cpp's callers do, and prints what it returns as one JSON object:
+//   - tdt_greedy_decode per utterance (src/parakeet_engine.cpp:273-297);
+//   - tdt_init_state + tdt_decode_window over fixed-size windows (Mode 2,
+//     src/parakeet_engine.cpp:409-452);
+//   - tdt_decode_batch over all utterances;
+//   - the same three for EOU, with segment boundaries;
+//   - Engine::transcribe_features on the first TDT utterance.
+// Usage: decoder_api_main TDT.gguf TDT_FRAMES EOU.gguf EOU_FRAMES WINDOW
+// Frame files: int32 n, T, D, then n*T*D float32 (utterance-major).
+#include <cstdio>
+#include <algorithm>
+#include <cstdlib>
+#include <string>
+#include <vector>
+
+#include "parakeet_decoder.h"
+
+namespace {
+
+struct Frames {
+    int n = 0, T = 0, D = 0;
+    std::vector<float> data;
+    const float *utt(int u) const { return data.data() + (size_t)u * T * D; }
+};
+
+bool read_frames(const char *path, Frames &f) {
+    FILE *fp = fopen(path, "rb");
+    if (!fp) return false;
+    int hdr[3];
+    bool ok = fread(hdr, 4, 3, fp) == 3;
+    if (ok) {
+        f.n = hdr[0];
+        f.T = hdr[1];
+        f.D = hdr[2];
+        f.data.resize((size_t)f.n * f.T * f.D);
+        ok = fread(f.data.data(), 4, f.data.size(), fp) == f.data.size();
+    }
+    fclose(fp);
+    return ok;
+}
+
+void ints(const std::vector<int32_t> &v) {
+    printf("[");
+    for (size_t i = 0; i < v.size(); ++i) printf(i ? ",%d" : "%d", v[i]);
+    printf("]");
+}
+
+void str(const std::string &s) {
+    printf("\"");
+    for (char c : s) {
+        if (c == '"' || c == '\\') printf("\\%c", c);
+        else printf("%c", c);
+    }
+    printf("\"");
+}
+
+int fail(const char *what, int rc) {
+    fprintf(stderr, "%s failed: rc=%d\n", what, rc);
+    return 1;
+}
+
+}  // namespace
+
+int main(int argc, char **argv) {
+    if (argc != 6) {
+        fprintf(stderr, "usage: %s TDT.gguf TDT_FRAMES EOU.gguf EOU_FRAMES WINDOW\n", argv[0]);
+        return 2;
+    }
+    const int W = atoi(argv[5]);
+    Frames ft, fe;
+    if (!read_frames(argv[2], ft) || !read_frames(argv[4], fe)) return fail("read frames", -1);
+    using namespace parakeet;
+    int rc;
+
+    // ---- TDT ----
+    ParakeetCtcModel tdt;
+    if ((rc = load_from_gguf(argv[1], tdt)) != 0) return fail("load_from_gguf(tdt)", rc);
+    TdtRuntimeWeights tw;
+    if ((rc = tdt_prepare_runtime(tdt, tw, 2 * ft.n + 4)) != 0) return fail("tdt_prepare_runtime", rc);
+    TdtDecodeOptions topt;
+    printf("{\"tdt\":{\"greedy\":[");
+    std::vector<int> steps;
+    std::vector<std::string> texts;
+    for (int u = 0; u < ft.n; ++u) {
+        TdtDecodeResult r;
+        if ((rc = tdt_greedy_decode(tdt, tw, ft.utt(u), ft.T, ft.D, topt, r)) != 0) return fail("tdt_greedy_decode", rc);
+        if (u) printf(",");
+        ints(r.token_ids);
+        steps.push_back(r.steps);
+        texts.push_back(r.text);
+    }
+    printf("],\"steps\":");
+    ints(std::vector<int32_t>(steps.begin(), steps.end()));
+    printf(",\"text\":[");
+    for (size_t i = 0; i < texts.size(); ++i) {
+        if (i) printf(",");
+        str(texts[i]);
+    }
+    printf("],\"chunked\":[");
+    for (int u = 0; u < ft.n; ++u) {
+        TdtDecodeState st;
+        tdt_init_state(tw, tdt.blank_id, st);
+        std::vector<int32_t> all;
+        for (int t0 = 0; t0 < ft.T; t0 += W) {
+            const int n = std::min(W, ft.T - t0);
+            std::vector<int32_t> toks;
+            int s = 0;
+            if ((rc = tdt_decode_window(tdt, tw, ft.utt(u) + (size_t)t0 * ft.D, n, ft.D, topt, st, toks, s)) != 0)
+                return fail("tdt_decode_window", rc);
+            all.insert(all.end(), toks.begin(), toks.end());
+        }
+        if (u) printf(",");
+        ints(all);
+    }
+    printf("],\"batch\":[");
+    {
+        std::vector<TdtDecodeState> sts(ft.n);
+        std::vector<TdtDecodeState *> ps;
+        std::vector<const float *> enc;
+        std::vector<int> nf;
+        for (int u = 0; u < ft.n; ++u) {
+            tdt_init_state(tw, tdt.blank_id, sts[u]);
+            ps.push_back(&sts[u]);
+            enc.push_back(ft.utt(u));
+            nf.push_back(ft.T);
+        }
+        std::vector<std::vector<int32_t>> toks;
+        std::vector<int> bs;
+        if ((rc = tdt_decode_batch(tdt, tw, enc, nf, ft.D, topt, ps, toks, bs)) != 0) return fail("tdt_decode_batch", rc);
+        for (int u = 0; u < ft.n; ++u) {
+            if (u) printf(",");
+            ints(toks[u]);
+        }
+    }
+    printf("],\"bad_dim_rc\":");
+    {
+        TdtDecodeResult r;
+        printf("%d", tdt_greedy_decode(tdt, tw, ft.utt(0), ft.T, ft.D + 1, topt, r));
+    }
+    printf("},");
+
+    // ---- EOU ----
+    ParakeetCtcModel eou;
+    if ((rc = load_from_gguf(argv[3], eou)) != 0) return fail("load_from_gguf(eou)", rc);
+    EouRuntimeWeights ew;
+    if ((rc = eou_prepare_runtime(eou, ew, 2 * fe.n + 4)) != 0) return fail("eou_prepare_runtime", rc);
+    EouDecodeOptions eopt;
+    eopt.max_symbols_per_step = eou.encoder_cfg.eou_max_symbols_per_step;
+    printf("\"eou\":{\"greedy\":[");
+    std::vector<std::vector<int32_t>> segs;
+    for (int u = 0; u < fe.n; ++u) {
+        EouDecodeResult r;
+        if ((rc = eou_greedy_decode(eou, ew, fe.utt(u), fe.T, fe.D, eopt, r)) != 0) return fail("eou_greedy_decode", rc);
+        if (u) printf(",");
+        ints(r.token_ids);
+        std::vector<int32_t> b;
+        for (auto &sb : r.segments) b.push_back(sb.token_index);
+        segs.push_back(b);
+    }
+    printf("],\"segments\":[");
+    for (size_t u = 0; u < segs.size(); ++u) {
+        if (u) printf(",");
+        ints(segs[u]);
+    }
+    printf("],\"chunked\":[");
+    std::vector<std::vector<int32_t>> csegs;
+    for (int u = 0; u < fe.n; ++u) {
+        EouDecodeState st;
+        eou_init_state(ew, st);
+        std::vector<int32_t> all, bounds;
+        for (int t0 = 0; t0 < fe.T; t0 += W) {
+            const int n = std::min(W, fe.T - t0);
+            std::vector<int32_t> toks;
+            std::vector<EouSegmentBoundary> sb;
+            int s = 0;
+            if ((rc = eou_decode_window(eou, ew, fe.utt(u) + (size_t)t0 * fe.D, n, fe.D, eopt, st, toks, sb, s)) != 0)
+                return fail("eou_decode_window", rc);
+            all.insert(all.end(), toks.begin(), toks.end());
+            for (auto &x : sb) bounds.push_back(x.token_index);
+        }
+        if (u) printf(",");
+        ints(all);
+        csegs.push_back(bounds);
+    }
+    printf("],\"chunked_segments\":[");
+    for (size_t u = 0; u < csegs.size(); ++u) {
+        if (u) printf(",");
+        ints(csegs[u]);
+    }
+    printf("]},");
+
+    // ---- Engine ----
+    try {
+        EngineOptions eo;
+        eo.model_gguf_path = argv[1];
+        eo.n_slots = 4;
+        Engine engine(eo);
+        EngineResult er = engine.transcribe_features(ft.utt(0), ft.T, ft.D);
+        printf("\"engine\":{\"tokens\":");
+        ints(er.token_ids);
+        printf(",\"text\":");
+        str(er.text);
+        printf(",\"steps\":%d}", er.steps);
+    } catch (const std::exception &e) {
+        fprintf(stderr, "Engine: %s\n", e.what());
+        return 1;
+    }
+    printf("}\n");
+    return 0;
+}

@@ -132,6 +132,43 @@ def test_deterministic(tmp_path):
         assert np.array_equal(x["tokens"], y["tokens"])
 
 
+def test_concurrent_decoders(tmp_path):
+    """Two decoders, each on its own stream, driven from two threads at once:
+    the loop launches are ordered on the device (a loop needs every CU), and
+    each thread gets the results of a sequential run."""
+    import threading
+    from parakeet_amd import pk, synth
+    small_tdt(str(tmp_path / "t.gguf"))
+    small_eou(str(tmp_path / "e.gguf"))
+    dt = pk.Decoder.from_gguf(str(tmp_path / "t.gguf"), n_slots=4)
+    de = pk.Decoder.from_gguf(str(tmp_path / "e.gguf"), n_slots=4)
+    et = [synth.encoder_frames(900 + u, 30, 128) for u in range(4)]
+    ee = [synth.encoder_frames(950 + u, 30, 64) for u in range(4)]
+
+    def run(dec, encs, out, rounds, start=None):
+        if start is not None:
+            start.wait()
+        for _ in range(rounds):
+            for u in range(len(encs)):
+                dec.reset_state(u)
+            out.append([r["tokens"].tolist() for r in dec.decode(encs)])
+
+    want_t, want_e = [], []
+    run(dt, et, want_t, 1)
+    run(de, ee, want_e, 1)
+    got_t, got_e = [], []
+    start = threading.Barrier(2)
+    th = [threading.Thread(target=run, args=(dt, et, got_t, 6, start)),
+          threading.Thread(target=run, args=(de, ee, got_e, 6, start))]
+    for t in th:
+        t.start()
+    for t in th:
+        t.join(60)
+    assert len(got_t) == 6 and len(got_e) == 6
+    assert all(g == want_t[0] for g in got_t)
+    assert all(g == want_e[0] for g in got_e)
+
+
 def test_error_codes(tmp_path):
     from parakeet_amd import pk, synth
     path = str(tmp_path / "m.gguf")
