@@ -17,6 +17,7 @@
 #pragma once
 
 #include <cstdint>
+#include <functional>
 #include <memory>
 #include <string>
 #include <vector>
@@ -33,17 +34,26 @@ struct BpeVocab {
     int32_t blank_id = -1, unk_id = -1, bos_id = -1, eos_id = -1, pad_id = -1;
 };
 
-// The decoder fields of the reference's EncoderConfig (src/parakeet_ctc.h).
+// The decoder fields of the reference's EncoderConfig (src/parakeet_ctc.h), plus the
+// subsampling factor that sets the encoder frame stride.
 struct EncoderConfig {
     int d_model = 1024;
+    int subsampling_factor = 8;
     int tdt_pred_hidden = 640, tdt_pred_rnn_layers = 2, tdt_joint_hidden = 640, tdt_num_durations = 5;
     int eou_pred_hidden = 640, eou_pred_rnn_layers = 1, eou_joint_hidden = 640;
     int eou_max_symbols_per_step = 5;
 };
 
+// The MelConfig fields that set the encoder frame stride (src/parakeet_ctc.cpp:470-473).
+struct MelConfig {
+    int sample_rate = 16000;
+    int hop_length = 160;
+};
+
 struct ParakeetCtcModel {
     ParakeetModelType model_type = ParakeetModelType::CTC;
     EncoderConfig encoder_cfg;
+    MelConfig mel_cfg;
     BpeVocab vocab;
     int32_t blank_id = 1024;
     int32_t vocab_size = 1025;
@@ -159,6 +169,91 @@ int eou_decode_batch(const ParakeetCtcModel &model, const EouRuntimeWeights &W, 
 // leading spaces trimmed.
 std::string detokenize(const BpeVocab &vocab, const std::vector<int32_t> &ids);
 
+// ---- Streaming types (include/parakeet/streaming.h) ----
+
+enum class VadState : int { Unknown = 0, Speaking = 1, Silent = 2 };
+enum class StreamEventType : int { VadStateChanged = 1, EndOfTurn = 2 };
+
+struct StreamEvent {
+    StreamEventType type = StreamEventType::VadStateChanged;
+    double timestamp_s = 0.0;     // end of the chunk that produced the event
+    int chunk_index = -1;
+    VadState vad_state = VadState::Unknown;
+    int speaker_id = -1;
+    float vad_score = 0.0f;
+    float eot_confidence = 0.0f;  // 1.0 when <EOU> fired
+};
+using StreamEventCallback = std::function<void(const StreamEvent &)>;
+
+struct StreamingSegment {
+    std::string text;             // new text of this chunk (cumulative detokenize, minus the previous text)
+    std::vector<int32_t> token_ids;
+    double start_s = 0.0, end_s = 0.0;
+    int chunk_index = 0;
+    bool is_final = true;
+    bool is_eou_boundary = false; // EOU: the chunk recorded at least one segment boundary
+    float eot_confidence = 0.0f;
+    double encoder_ms = 0.0;
+    double decode_ms = 0.0;
+};
+using StreamingCallback = std::function<void(const StreamingSegment &)>;
+
+// Streaming over encoder features.  The reference's StreamingOptions (chunk_ms,
+// left context, lookahead) also drive mel and encoder windows, which are
+// outside this library: a caller hands the frames of each chunk that are to
+// be decoded (the reference drops the context frames first,
+// src/parakeet_engine.cpp:796-818).
+struct FeatureStreamOptions {
+    int chunk_ms = 1000;             // StreamingOptions::chunk_ms
+    int chunk_frames = 0;            // frames per window of transcribe_features_stream;
+                                     // 0: floor(chunk_ms / frame stride), at least 1
+    StreamEventCallback on_event = nullptr;
+};
+
+class Engine;
+
+// The decode half of StreamSession (src/parakeet_engine.cpp:753-864): each fed
+// chunk is decoded with the session's carried state (its own device slot),
+// then one StreamingSegment and, for EOU boundaries, EndOfTurn events are
+// delivered.  Each chunk is decoded into a fresh token vector, as the
+// reference does, so EOU boundary indices count from the chunk's first token
+// while segment_start_token carries over (src/parakeet_eou.cpp:293-299).
+// Not thread-safe; one Engine may hold many sessions; a session must not
+// outlive its Engine.
+class FeatureStreamSession {
+public:
+    struct Impl;
+    explicit FeatureStreamSession(std::unique_ptr<Impl> impl);
+    ~FeatureStreamSession();
+    FeatureStreamSession(const FeatureStreamSession &) = delete;
+    FeatureStreamSession &operator=(const FeatureStreamSession &) = delete;
+
+    // One chunk of encoder frames [n_frames][D_enc].  Throws std::runtime_error on
+    // a decode failure; does nothing after cancel().
+    void feed_frames(const float *encoder_out, int n_frames, int D_enc);
+    // Sessions of one Engine fed in one lockstep launch: sessions[i] gets
+    // encoder_out[i][0 .. n_frames[i]).  Callbacks run afterwards, in session order.
+    static void feed_frames_batch(const std::vector<FeatureStreamSession *> &sessions,
+                                  const std::vector<const float *> &encoder_out, const std::vector<int> &n_frames,
+                                  int D_enc);
+    // No more chunks (the reference flushes its sample remainder here; feature
+    // chunks have none).  Later feeds throw.
+    void finalize();
+    void cancel();
+    const FeatureStreamOptions &options() const;
+    int chunks_emitted() const;
+    const std::vector<int32_t> &token_ids() const;   // every token so far
+    const std::string &text() const;                 // detokenize(token_ids())
+    int steps() const;                               // decode steps so far
+
+private:
+    std::unique_ptr<Impl> pimpl_;
+};
+
+// Encoder frame stride in ms: 1000 * hop_length * subsampling / sample_rate
+// (src/parakeet_engine.cpp:35-41).
+double encoder_frame_stride_ms(const ParakeetCtcModel &model);
+
 // ---- Engine-shaped front (include/parakeet/engine.h) over encoder features ----
 
 struct EngineOptions {
@@ -183,10 +278,17 @@ public:
     EngineResult transcribe_features(const float *encoder_out, int T_enc, int D_enc);
     std::vector<EngineResult> transcribe_features_batch(const std::vector<const float *> &encoder_out,
                                                         const std::vector<int> &T_enc, int D_enc);
+    // The decode half of Engine::transcribe_samples_stream (src/parakeet_engine.cpp:389-489):
+    // the encoder output in windows of opts.chunk_frames frames, one segment per window.
+    EngineResult transcribe_features_stream(const float *encoder_out, int T_enc, int D_enc,
+                                            const FeatureStreamOptions &opts, StreamingCallback on_segment);
+    // The decode half of Engine::stream_start (src/parakeet_engine.cpp:1013-1059).
+    std::unique_ptr<FeatureStreamSession> stream_start(const FeatureStreamOptions &opts,
+                                                       StreamingCallback on_segment);
     const ParakeetCtcModel &model() const;
+    struct Impl;
 
 private:
-    struct Impl;
     std::unique_ptr<Impl> pimpl_;
 };
 

@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -201,6 +202,9 @@ int load_from_gguf(const std::string &gguf_path, ParakeetCtcModel &out, int, int
     }
     out = ParakeetCtcModel{};
     out.encoder_cfg.d_model = (int)g.get_u32("parakeet.encoder.d_model", 1024);
+    out.encoder_cfg.subsampling_factor = (int)g.get_u32("parakeet.encoder.subsampling_factor", 8);
+    out.mel_cfg.sample_rate = (int)g.get_u32("parakeet.preproc.sample_rate", 16000);
+    out.mel_cfg.hop_length = (int)g.get_u32("parakeet.preproc.hop_length", 160);
     const std::string mt = g.get_str("parakeet.model.type", "ctc");
     out.model_type = mt == "tdt" ? ParakeetModelType::TDT
                    : mt == "eou" ? ParakeetModelType::EOU
@@ -601,6 +605,168 @@ std::vector<EngineResult> Engine::transcribe_features_batch(const std::vector<co
         out[u].encoder_frames = T_enc[u];
     }
     return out;
+}
+
+// ------------------------------------------------------------------ streaming over features
+
+double encoder_frame_stride_ms(const ParakeetCtcModel &m) {
+    const int sub = m.encoder_cfg.subsampling_factor > 0 ? m.encoder_cfg.subsampling_factor : 8;
+    const int sr = m.mel_cfg.sample_rate > 0 ? m.mel_cfg.sample_rate : 16000;
+    return 1000.0 * (double)(m.mel_cfg.hop_length * sub) / (double)sr;
+}
+
+struct FeatureStreamSession::Impl {
+    Engine::Impl *engine = nullptr;
+    FeatureStreamOptions opts;
+    StreamingCallback on_segment;
+    double stride_ms = 80.0;
+    TdtDecodeState tdt;
+    EouDecodeState eou;
+    std::vector<int32_t> cum_ids;     // every token of the session so far
+    std::string cum_text;             // detokenize(cum_ids)
+    long long emitted_frames = 0;
+    int chunk_index = 0;
+    int steps = 0;
+    bool cancelled = false, finalized = false;
+
+    // Segment and events of one decoded chunk (src/parakeet_engine.cpp:838-864).
+    void emit(const std::vector<int32_t> &win_tokens, int n_boundaries, int n_frames, double decode_ms);
+};
+
+FeatureStreamSession::FeatureStreamSession(std::unique_ptr<Impl> impl) : pimpl_(std::move(impl)) {}
+FeatureStreamSession::~FeatureStreamSession() = default;
+const FeatureStreamOptions &FeatureStreamSession::options() const { return pimpl_->opts; }
+int FeatureStreamSession::chunks_emitted() const { return pimpl_->chunk_index; }
+const std::vector<int32_t> &FeatureStreamSession::token_ids() const { return pimpl_->cum_ids; }
+const std::string &FeatureStreamSession::text() const { return pimpl_->cum_text; }
+int FeatureStreamSession::steps() const { return pimpl_->steps; }
+void FeatureStreamSession::cancel() { pimpl_->cancelled = true; }
+void FeatureStreamSession::finalize() { pimpl_->finalized = true; }
+
+void FeatureStreamSession::Impl::emit(const std::vector<int32_t> &win_tokens, int n_boundaries, int n_frames,
+                                      double decode_ms) {
+    const ParakeetCtcModel &m = engine->model;
+    const size_t prev = cum_text.size();
+    cum_ids.insert(cum_ids.end(), win_tokens.begin(), win_tokens.end());
+    cum_text = detokenize(m.vocab, cum_ids);
+    const double start_s = (double)emitted_frames * stride_ms / 1000.0;
+    const double end_s = (double)(emitted_frames + n_frames) * stride_ms / 1000.0;
+    if (on_segment) {
+        StreamingSegment seg;
+        seg.text = cum_text.substr(prev);
+        seg.token_ids = win_tokens;
+        seg.start_s = start_s;
+        seg.end_s = end_s;
+        seg.chunk_index = chunk_index;
+        seg.is_final = true;
+        seg.is_eou_boundary = n_boundaries > 0;
+        seg.decode_ms = decode_ms;
+        on_segment(seg);
+    }
+    if (opts.on_event && n_boundaries > 0) {   // one EndOfTurn per boundary, confidence 1
+        StreamEvent ev;
+        ev.type = StreamEventType::EndOfTurn;
+        ev.timestamp_s = end_s;
+        ev.chunk_index = chunk_index;
+        ev.eot_confidence = 1.0f;
+        for (int i = 0; i < n_boundaries; ++i) opts.on_event(ev);
+    }
+    emitted_frames += n_frames;
+    ++chunk_index;
+}
+
+void FeatureStreamSession::feed_frames(const float *enc, int n_frames, int D_enc) {
+    feed_frames_batch({this}, {enc}, {n_frames}, D_enc);
+}
+
+void FeatureStreamSession::feed_frames_batch(const std::vector<FeatureStreamSession *> &sessions,
+                                             const std::vector<const float *> &enc, const std::vector<int> &n_frames,
+                                             int D_enc) {
+    if (enc.size() != sessions.size() || n_frames.size() != sessions.size())
+        throw std::invalid_argument("FeatureStreamSession::feed_frames_batch: size mismatch");
+    std::vector<Impl *> live;
+    std::vector<const float *> e;
+    std::vector<int> nf;
+    for (size_t i = 0; i < sessions.size(); ++i) {
+        Impl *s = sessions[i]->pimpl_.get();
+        if (s->cancelled) continue;
+        if (s->finalized) throw std::logic_error("FeatureStreamSession: feed after finalize()");
+        if (!live.empty() && s->engine != live[0]->engine)
+            throw std::invalid_argument("FeatureStreamSession::feed_frames_batch: sessions of different engines");
+        if (n_frames[i] < 0) throw std::invalid_argument("FeatureStreamSession: negative n_frames");
+        for (Impl *o : live)
+            if (o == s) throw std::invalid_argument("FeatureStreamSession::feed_frames_batch: repeated session");
+        live.push_back(s);
+        e.push_back(enc[i]);
+        nf.push_back(n_frames[i]);
+    }
+    if (live.empty()) return;
+    Engine::Impl &E = *live[0]->engine;
+    const ParakeetCtcModel &m = E.model;
+    const int n = (int)live.size();
+    const auto t0 = std::chrono::steady_clock::now();
+    std::vector<std::vector<int32_t>> toks;
+    std::vector<int> steps, nb(n, 0);
+    if (m.model_type == ParakeetModelType::TDT) {
+        std::vector<TdtDecodeState *> st(n);
+        for (int i = 0; i < n; ++i) st[i] = &live[i]->tdt;
+        if (int rc = tdt_decode_batch(m, E.tdt, e, nf, D_enc, TdtDecodeOptions{}, st, toks, steps))
+            throw std::runtime_error("FeatureStreamSession: tdt_decode_window failed (rc=" + std::to_string(rc) + ")");
+    } else {
+        EouDecodeOptions o;
+        o.max_symbols_per_step = m.encoder_cfg.eou_max_symbols_per_step;
+        std::vector<EouDecodeState *> st(n);
+        for (int i = 0; i < n; ++i) st[i] = &live[i]->eou;
+        std::vector<std::vector<EouSegmentBoundary>> segs;
+        if (int rc = eou_decode_batch(m, E.eou, e, nf, D_enc, o, st, toks, segs, steps))
+            throw std::runtime_error("FeatureStreamSession: eou_decode_window failed (rc=" + std::to_string(rc) + ")");
+        for (int i = 0; i < n; ++i) nb[i] = (int)segs[i].size();
+    }
+    const double ms =
+        std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::steady_clock::now() - t0).count() / 1000.0;
+    for (int i = 0; i < n; ++i) {
+        live[i]->steps += steps[i];
+        live[i]->emit(toks[i], nb[i], nf[i], ms);
+    }
+}
+
+std::unique_ptr<FeatureStreamSession> Engine::stream_start(const FeatureStreamOptions &opts,
+                                                           StreamingCallback on_segment) {
+    if (opts.chunk_ms <= 0 && opts.chunk_frames <= 0)
+        throw std::runtime_error("Engine::stream_start: chunk_ms must be > 0");
+    auto impl = std::make_unique<FeatureStreamSession::Impl>();
+    impl->engine = pimpl_.get();
+    impl->opts = opts;
+    impl->on_segment = std::move(on_segment);
+    impl->stride_ms = encoder_frame_stride_ms(pimpl_->model);
+    if (pimpl_->model.model_type == ParakeetModelType::TDT)
+        tdt_init_state(pimpl_->tdt, pimpl_->model.blank_id, impl->tdt);
+    else
+        eou_init_state(pimpl_->eou, impl->eou);
+    return std::make_unique<FeatureStreamSession>(std::move(impl));
+}
+
+EngineResult Engine::transcribe_features_stream(const float *enc, int T_enc, int D_enc,
+                                                const FeatureStreamOptions &opts, StreamingCallback on_segment) {
+    if (!enc || T_enc <= 0) throw std::runtime_error("parakeet::Engine::transcribe_features_stream: empty input");
+    const auto t0 = std::chrono::steady_clock::now();
+    const double stride = encoder_frame_stride_ms(pimpl_->model);
+    int fpw = opts.chunk_frames > 0 ? opts.chunk_frames : (int)std::floor(opts.chunk_ms / stride);
+    if (fpw < 1) fpw = 1;
+    auto session = stream_start(opts, std::move(on_segment));
+    EngineResult result;
+    result.encoder_frames = T_enc;
+    for (int start = 0; start < T_enc; start += fpw) {
+        const int end = std::min(T_enc, start + fpw);
+        session->feed_frames(enc + (size_t)start * D_enc, end - start, D_enc);
+    }
+    session->finalize();
+    result.token_ids = session->token_ids();
+    result.text = session->text();
+    result.steps = session->steps();
+    result.decode_ms =
+        std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::steady_clock::now() - t0).count() / 1000.0;
+    return result;
 }
 
 }  // namespace parakeet

@@ -58,10 +58,11 @@ def vocab_pieces(kind: str, vocab: int, eou_id: int = -1, eob_id: int = -1) -> l
 def make_decoder_gguf(path: str, kind: str, H: int, L: int, J: int, D: int, vocab: int,
                       durations=None, eou_id: int = -1, eob_id: int = -1, max_symbols: int = 5,
                       quant: str = "q8_0", seed: int = WEIGHT_SEED, scale: float = 1.0,
-                      overrides: dict | None = None) -> dict:
+                      overrides: dict | None = None, meta_u32: dict | None = None) -> dict:
     """Write a decoder GGUF and return its float32 weights (dequantised from
     the stored bytes) keyed by tensor name.  ``overrides`` replaces named
-    tensors (PyTorch layout) before quantisation -- used by scripted models."""
+    tensors (PyTorch layout) before quantisation -- used by scripted models;
+    ``meta_u32`` adds u32 metadata keys (e.g. parakeet.preproc.hop_length)."""
     rng = np.random.default_rng(seed)
     p = "tdt" if kind == "tdt" else "eou"
     V1 = vocab + 1
@@ -113,6 +114,8 @@ def make_decoder_gguf(path: str, kind: str, H: int, L: int, J: int, D: int, voca
         w.add_u32("parakeet.eou.max_symbols_per_step", max_symbols)
     w.add_arr("tokenizer.ggml.tokens", G.T_STR, vocab_pieces(kind, vocab, eou_id, eob_id))
     w.add_bool("parakeet.decoder_only", True)
+    for k, v in (meta_u32 or {}).items():
+        w.add_u32(k, int(v))
 
     for name, arr in tensors.items():
         if arr.ndim == 2:

@@ -5,12 +5,16 @@
 //     src/parakeet_engine.cpp:409-452);
 //   - tdt_decode_batch over all utterances;
 //   - the same three for EOU, with segment boundaries;
-//   - Engine::transcribe_features on the first TDT utterance.
+//   - Engine::transcribe_features on the first TDT utterance;
+//   - Engine::transcribe_features_stream (Mode 2) on the first TDT utterance, and
+//     EOU FeatureStreamSessions (Mode 3) fed chunk by chunk: all sessions in one
+//     launch per chunk, and one session per launch.
 // Usage: decoder_api_main TDT.gguf TDT_FRAMES EOU.gguf EOU_FRAMES WINDOW
 // Frame files: int32 n, T, D, then n*T*D float32 (utterance-major).
 #include <cstdio>
 #include <algorithm>
 #include <cstdlib>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -53,6 +57,33 @@ void str(const std::string &s) {
         else printf("%c", c);
     }
     printf("\"");
+}
+
+struct SegLog {
+    std::vector<parakeet::StreamingSegment> segs;
+    std::vector<parakeet::StreamEvent> events;
+};
+
+void print_log(const SegLog &l) {
+    printf("{\"segments\":[");
+    for (size_t i = 0; i < l.segs.size(); ++i) {
+        const auto &g = l.segs[i];
+        printf(i ? ",{" : "{");
+        printf("\"chunk\":%d,\"tokens\":", g.chunk_index);
+        ints(g.token_ids);
+        printf(",\"text\":");
+        str(g.text);
+        printf(",\"start\":%.6f,\"end\":%.6f,\"eou\":%d,\"final\":%d}", g.start_s, g.end_s,
+               g.is_eou_boundary ? 1 : 0, g.is_final ? 1 : 0);
+    }
+    printf("],\"events\":[");
+    for (size_t i = 0; i < l.events.size(); ++i) {
+        const auto &e = l.events[i];
+        printf(i ? ",{" : "{");
+        printf("\"type\":%d,\"chunk\":%d,\"t\":%.6f,\"conf\":%.3f}", (int)e.type, e.chunk_index, e.timestamp_s,
+               e.eot_confidence);
+    }
+    printf("]}");
 }
 
 int fail(const char *what, int rc) {
@@ -202,6 +233,58 @@ int main(int argc, char **argv) {
         printf(",\"text\":");
         str(er.text);
         printf(",\"steps\":%d}", er.steps);
+
+        // ---- streaming over features ----
+        printf(",\"stream\":{\"tdt\":");
+        SegLog tl;
+        FeatureStreamOptions so;
+        so.chunk_frames = W;
+        EngineResult sr = engine.transcribe_features_stream(
+            ft.utt(0), ft.T, ft.D, so, [&](const StreamingSegment &g) { tl.segs.push_back(g); });
+        print_log(tl);
+        printf(",\"tdt_tokens\":");
+        ints(sr.token_ids);
+        printf(",\"tdt_text\":");
+        str(sr.text);
+        printf(",\"tdt_steps\":%d,\"stride_ms\":%.6f", sr.steps, encoder_frame_stride_ms(engine.model()));
+
+        EngineOptions eeo;
+        eeo.model_gguf_path = argv[3];
+        eeo.n_slots = 2 * fe.n + 4;
+        Engine eng(eeo);
+        for (int mode = 0; mode < 2; ++mode) {   // 0: all sessions per launch, 1: one per launch
+            std::vector<SegLog> logs(fe.n);
+            std::vector<std::unique_ptr<FeatureStreamSession>> ss;
+            for (int u = 0; u < fe.n; ++u) {
+                FeatureStreamOptions o;
+                o.on_event = [&logs, u](const StreamEvent &ev) { logs[u].events.push_back(ev); };
+                ss.push_back(eng.stream_start(o, [&logs, u](const StreamingSegment &g) { logs[u].segs.push_back(g); }));
+            }
+            for (int t0 = 0; t0 < fe.T; t0 += W) {
+                const int n = std::min(W, fe.T - t0);
+                if (mode == 0) {
+                    std::vector<FeatureStreamSession *> ps;
+                    std::vector<const float *> en;
+                    std::vector<int> nf;
+                    for (int u = 0; u < fe.n; ++u) {
+                        ps.push_back(ss[u].get());
+                        en.push_back(fe.utt(u) + (size_t)t0 * fe.D);
+                        nf.push_back(n);
+                    }
+                    FeatureStreamSession::feed_frames_batch(ps, en, nf, fe.D);
+                } else {
+                    for (int u = 0; u < fe.n; ++u) ss[u]->feed_frames(fe.utt(u) + (size_t)t0 * fe.D, n, fe.D);
+                }
+            }
+            printf(mode == 0 ? ",\"eou_batch\":[" : ",\"eou_single\":[");
+            for (int u = 0; u < fe.n; ++u) {
+                ss[u]->finalize();
+                if (u) printf(",");
+                print_log(logs[u]);
+            }
+            printf("]");
+        }
+        printf("}");
     } catch (const std::exception &e) {
         fprintf(stderr, "Engine: %s\n", e.what());
         return 1;
