@@ -183,3 +183,49 @@ def test_error_codes(tmp_path):
     with pytest.raises(pk.PkError) as e:
         dev.decode([synth.encoder_frames(0, 5, 128)] * 2, slots=[1, 1])
     assert e.value.rc == 3
+
+
+@pytest.mark.parametrize("kind", ["tdt", "eou"])
+def test_device_memory_batch_matches_host(tmp_path, kind):
+    """Encoder frames already resident in HBM (PK_MEM_DEVICE): a ragged batch
+    whose utterances sit at scattered row offsets of one device array, outputs
+    written to device arrays, gives the host-memory batch's results."""
+    from parakeet_amd import hipmem, pk, synth
+    path = str(tmp_path / "m.gguf")
+    (small_tdt if kind == "tdt" else small_eou)(path)
+    dec = pk.Decoder.from_gguf(path, n_slots=12)
+    D = dec.info.D
+    Ts = [17, 0, 33, 5, 24] if kind == "eou" else [17, 1, 33, 5, 24]
+    encs = [synth.encoder_frames(500 + u, T, D) for u, T in enumerate(Ts)]
+    # rows: utterance u at offset rows[u], with unused rows between utterances
+    rows = np.zeros(len(Ts), np.int64)
+    at = 3
+    for u, T in enumerate(Ts):
+        rows[u] = at
+        at += T + 2
+    frames = np.full((at, D), np.nan, np.float32)     # gaps hold NaN: never read
+    for u, T in enumerate(Ts):
+        frames[rows[u]:rows[u] + T] = encs[u]
+    bias = np.array([0.0, 2.0, 0.0, 4.0, 1.0], np.float32)
+    ms = dec.info.max_symbols
+    want = dec.decode(encs, slots=list(range(5)), blank_bias=bias)
+    n = len(Ts)
+    cap = max(Ts) * max(1, ms) + 1
+    enc_d = hipmem.DeviceArray.from_numpy(frames)
+    out = dict(tokens=hipmem.DeviceArray(4 * n * cap), n_tokens=hipmem.DeviceArray(4 * n),
+               steps=hipmem.DeviceArray(4 * n), segments=hipmem.DeviceArray(4 * n * cap),
+               n_segments=hipmem.DeviceArray(4 * n))
+    ptrs = {k: v.ptr for k, v in out.items()}
+    ptrs["seg_cap"] = cap
+    dec.decode_device(enc_d.ptr, rows, Ts, np.arange(5, 10, dtype=np.int32), ms, ptrs, cap, blank_bias=bias)
+    hipmem.synchronize()
+    toks = out["tokens"].to_numpy(np.int32, n * cap).reshape(n, cap)
+    ntok = out["n_tokens"].to_numpy(np.int32, n)
+    steps = out["steps"].to_numpy(np.int32, n)
+    segs = out["segments"].to_numpy(np.int32, n * cap).reshape(n, cap)
+    nseg = out["n_segments"].to_numpy(np.int32, n)
+    for u in range(n):
+        assert toks[u, :ntok[u]].tolist() == want[u]["tokens"].tolist(), u
+        assert steps[u] == want[u]["steps"], u
+        if kind == "eou":
+            assert segs[u, :nseg[u]].tolist() == want[u]["segments"].tolist(), u
