@@ -59,12 +59,12 @@ def build_decoder():
     return out
 
 
-def build_api_test():
-    """tests/cpp/decoder_api_main: drives the C++ API for the GPU tests (not part of the library)."""
-    src = os.path.join(ROOT, "tests", "cpp", "decoder_api_main.cpp")
+def build_api_test(name="decoder_api_main"):
+    """tests/cpp/<name>: drivers of the C++ API for the tests (not part of the library)."""
+    src = os.path.join(ROOT, "tests", "cpp", name + ".cpp")
     if not os.path.exists(src) or not os.path.exists(os.path.join(HERE, "libparakeet_decoder.so")):
         return None
-    out = os.path.join(ROOT, "tests", "cpp", "decoder_api_main")
+    out = os.path.join(ROOT, "tests", "cpp", name)
     _run(["g++", "-O2", "-std=c++17", "-Wall", f"-I{INC}", src, f"-L{HERE}", "-lparakeet_decoder", "-lparakeet_hip",
           "-Wl,-rpath,$ORIGIN/../../parakeet.cpp_amd", "-o", out + ".tmp"])
     os.replace(out + ".tmp", out)
@@ -72,7 +72,8 @@ def build_api_test():
 
 
 def build_all():
-    return [build_hip(), build_decoder(), build_calib(), build_api_test()]
+    return [build_hip(), build_decoder(), build_calib(), build_api_test("decoder_api_main"),
+            build_api_test("loader_main")]
 
 
 if __name__ == "__main__":
