@@ -579,6 +579,90 @@ __device__ __forceinline__ void unit_load(const WView m, bool two, int tile, int
     }
 }
 
+// One matrix's fragment sources for a phase: buffer descriptors (q8_0: the
+// quants and the block scales; f16: the plane twice; f32: the hi and lo
+// planes) and the base of this workgroup's LDS-cached tiles, set up once.
+struct MatSrc {
+    __amdgpu_buffer_rsrc_t r0, r1;
+    const unsigned char *lds;
+    int KB;
+};
+template <bool Q8, bool CACHED>
+__device__ __forceinline__ MatSrc mat_src(const TMat &m, bool two, const unsigned char *wc) {
+    MatSrc s;
+    if (Q8) {
+        s.r0 = rsrc(m.a, (unsigned)m.tiles * m.KB * kWave * 8u);
+        s.r1 = rsrc(m.scale, (unsigned)m.tiles * m.KB * kTile * 2u);
+    } else {
+        const unsigned bytes = (unsigned)m.tiles * m.KB * kWave * 16u;
+        s.r0 = rsrc(m.a, bytes);
+        s.r1 = rsrc(two ? m.a_lo : m.a, bytes);
+    }
+    s.lds = CACHED ? wc + m.lds_off : nullptr;
+    s.KB = m.KB;
+    return s;
+}
+
+// Fragments of one unit, blocks sb0 .. sb0+kUnit-1 of tile `tile` (local index
+// li in the LDS cache).  FULL: all kUnit blocks exist (K is a whole number of
+// units), so every offset is a lane constant plus a wave-uniform base plus an
+// immediate.  Otherwise blocks past nb read as zero (buffer loads past the
+// range return 0; cached blocks are zeroed).
+template <bool Q8, bool CACHED, bool FULL>
+__device__ __forceinline__ void unit_load_src(const MatSrc &m, bool two, int tile, int li, int sb0, int nb, int lane,
+                                              uint4 (&f)[kUnit]) {
+    if (CACHED) {
+#pragma unroll
+        for (int j = 0; j < kUnit; ++j) {
+            const bool ok = FULL || j < nb;
+            const int sb = ok ? sb0 + j : sb0;
+            uint4 v;
+            if (Q8) {
+                const unsigned char *blk = m.lds + ((size_t)li * m.KB + sb) * 544;
+                const uint2 q = *reinterpret_cast<const uint2 *>(blk + lane * 8);
+                const uint2 d = *reinterpret_cast<const uint2 *>(blk + 512 + (lane >> 4) * 8);
+                v = make_uint4(q.x, q.y, d.x, d.y);
+            } else {
+                const int kb = two ? sb >> 1 : sb;
+                const int plane = two ? (sb & 1) : 0;
+                v = *reinterpret_cast<const uint4 *>(m.lds + (((size_t)li * m.KB + kb) * (two ? 2 : 1) + plane) * 1024 +
+                                                     lane * 16);
+            }
+            f[j] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
+        return;
+    }
+    if (Q8) {
+        const int f0 = tile * m.KB + sb0;   // wave-uniform fragment index of block sb0
+#pragma unroll
+        for (int j = 0; j < kUnit; ++j) {
+            uint2 q, d;
+            if (FULL) {
+                q = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(m.r0, lane * 8 + j * 512, f0 * 512, 0));
+                d = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(m.r1, (lane >> 4) * 8 + j * 32,
+                                                                                  f0 * 32, 0));
+            } else {
+                const bool ok = j < nb;
+                const unsigned oq = ok ? (unsigned)((f0 + j) * kWave + lane) * 8u : kBad;
+                const unsigned os = ok ? (unsigned)((f0 + j) * kTile + (lane >> 4) * 4) * 2u : kBad;
+                q = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(m.r0, oq, 0, 0));
+                d = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(m.r1, os, 0, 0));
+            }
+            f[j] = make_uint4(q.x, q.y, d.x, d.y);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kUnit; ++j) {
+            const int sb = sb0 + j;
+            const int kb = two ? sb >> 1 : sb;
+            const bool ok = FULL || j < nb;
+            const unsigned o = ok ? (unsigned)(((tile * m.KB + kb) * kWave + lane) * 16) : kBad;
+            f[j] = __builtin_bit_cast(uint4, (two && (sb & 1)) ? __builtin_amdgcn_raw_buffer_load_b128(m.r1, o, 0, 0)
+                                                               : __builtin_amdgcn_raw_buffer_load_b128(m.r0, o, 0, 0));
+        }
+    }
+}
+
 // The activation fragments of a unit's K blocks (all reads issued at once).
 __device__ __forceinline__ void unit_act(const Act &x, int xo, bool two, int sb0, int nb, half8 (&ah)[kUnit],
                                          half8 (&al)[kUnit]) {
@@ -625,7 +709,7 @@ __device__ __forceinline__ int wave_cut(int N, int w) { return (int)(((long long
 
 __device__ __forceinline__ int blocks_per_item(const TMat &m) { return m.type == PK_TYPE_F32 ? 2 * m.KB : m.KB; }
 
-template <bool Q8, bool CACHED, bool KMAJ>
+template <bool Q8, bool CACHED, bool KMAJ, bool FULL>
 __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
                                                const Act &x, f32x4 *red, const unsigned char *wc) {
     // wave-uniform unit bookkeeping: the weight buffer descriptors stay in SGPRs
@@ -640,31 +724,34 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
     // rows past x.n are not staged (they hold older values) and the columns
     // they feed are never read.
     const int xo = (lane & 15) * x.kp + (lane >> 4) * 8;
-    // the two matrices' descriptors, read once (not per unit from the kernel arguments)
-    const WView vA = wview(A), vB = wview(Bm);
     half8 ah[kUnit], al[kUnit];
     if (KMAJ) {
         // unit u = c * n_items + item: a wave's range runs over items at one K
         // chunk c, so its activation fragments are read once per chunk; one
-        // partial per unit, in slot item * S + c
-        int c = c0 / n_items, item = c0 - c * n_items, have = -1;
-        for (int u = c0; u < c1; ++u) {
+        // partial per unit, in slot item * S + c.  Per chunk the wave's items
+        // of A come first, then those of B, each with its matrix's sources
+        // fixed for the whole loop.
+        const MatSrc sA = mat_src<Q8, CACHED>(A, two, wc), sB = mat_src<Q8, CACHED>(Bm, two, wc);
+        for (int u = c0; u < c1;) {
+            const int c = u / n_items, i0 = u - c * n_items, i1 = min(n_items, i0 + (c1 - u));
             const int sb0 = c * kUnit, nb = min(kUnit, KBe - sb0);
-            if (c != have) {
-                unit_act(x, xo, two, sb0, nb, ah, al);
-                have = c;
+            unit_act(x, xo, two, sb0, nb, ah, al);
+            for (int item = i0; item < min(i1, n_a); ++item) {
+                uint4 f[kUnit];
+                unit_load_src<Q8, CACHED, FULL>(sA, two, rank + item * P, item, sb0, nb, lane, f);
+                red[(item * S + c) * kWave + lane] = unit_mma<Q8>(f, ah, al, two, sb0, f32x4{0.f, 0.f, 0.f, 0.f});
             }
-            const bool in_a = item < n_a;
-            const int li = in_a ? item : item - n_a;
-            uint4 f[kUnit];
-            unit_load<Q8, CACHED>(pick(in_a, vA, vB), two, rank + li * P, li, wc, sb0, nb, lane, f);
-            red[(item * S + c) * kWave + lane] = unit_mma<Q8>(f, ah, al, two, sb0, f32x4{0.f, 0.f, 0.f, 0.f});
-            if (++item == n_items) {
-                item = 0;
-                ++c;
+            for (int item = max(i0, n_a); item < i1; ++item) {
+                const int li = item - n_a;
+                uint4 f[kUnit];
+                unit_load_src<Q8, CACHED, FULL>(sB, two, rank + li * P, li, sb0, nb, lane, f);
+                red[(item * S + c) * kWave + lane] = unit_mma<Q8>(f, ah, al, two, sb0, f32x4{0.f, 0.f, 0.f, 0.f});
             }
+            u += i1 - i0;
         }
     } else {
+        // the two matrices' descriptors, read once (not per unit from the kernel arguments)
+        const WView vA = wview(A), vB = wview(Bm);
         // unit u = item * S + c: a wave keeps one running partial per item, in
         // slot item + wave
         int item = c0 / S, c = c0 - item * S;
@@ -721,14 +808,21 @@ __device__ __forceinline__ void run_phase_(const TMat &A, int n_a, const TMat &B
                                            const Act &x, f32x4 *red, const unsigned char *wc, EpiFn epi) {
     // both matrices of a phase are in the LDS weight cache or neither
     const bool cached = wc != nullptr && A.lds_off >= 0;
-    if (A.type == PK_TYPE_Q8_0) {
-        if (cached) phase_partials<true, true, KMAJ>(A, n_a, Bm, n_items, rank, P, x, red, wc);
-        else phase_partials<true, false, KMAJ>(A, n_a, Bm, n_items, rank, P, x, red, wc);
-    } else {
-        if (cached) phase_partials<false, true, KMAJ>(A, n_a, Bm, n_items, rank, P, x, red, wc);
-        else phase_partials<false, false, KMAJ>(A, n_a, Bm, n_items, rank, P, x, red, wc);
-    }
     const int KBe = A.type == PK_TYPE_F32 ? 2 * A.KB : A.KB;
+    // K-major with K a whole number of units: the unmasked unit loads
+    const bool full = KMAJ && KBe % kUnit == 0;
+    if (A.type == PK_TYPE_Q8_0) {
+        if (cached) {
+            if (full) phase_partials<true, true, KMAJ, true>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+            else phase_partials<true, true, KMAJ, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+        } else {
+            if (full) phase_partials<true, false, KMAJ, true>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+            else phase_partials<true, false, KMAJ, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+        }
+    } else {
+        if (cached) phase_partials<false, true, KMAJ, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+        else phase_partials<false, false, KMAJ, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+    }
     phase_reduce<KMAJ>(n_items, (KBe + kUnit - 1) / kUnit, red, epi);
 }
 template <class EpiFn>
