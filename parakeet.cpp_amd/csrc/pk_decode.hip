@@ -118,6 +118,29 @@ struct DevBuf {
     template <class T> T *as() const { return static_cast<T *>(p); }
 };
 
+// Pinned host memory, grown on demand (staging of the outputs copied back).
+struct HostBuf {
+    void *p = nullptr;
+    size_t n = 0;
+    HostBuf() = default;
+    HostBuf(const HostBuf &) = delete;
+    HostBuf &operator=(const HostBuf &) = delete;
+    ~HostBuf() { if (p) (void)hipHostFree(p); }
+    int ensure(size_t bytes) {
+        if (bytes <= n) return 0;
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        n = 0;
+        if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) {
+            p = nullptr;
+            return fail(PK_ERR_NOMEM, "hipHostMalloc(%zu) failed", bytes);
+        }
+        n = bytes;
+        return 0;
+    }
+    template <class T> T *as() const { return static_cast<T *>(p); }
+};
+
 int check_tensor(const pk_tensor &t, int rows, int cols, const char *name) {
     if (!t.data) return fail(PK_ERR_TENSOR, "missing tensor %s", name);
     if (t.ne0 != cols || t.ne1 != rows)
@@ -253,6 +276,7 @@ struct pk_decoder {
     // per-call scratch
     DevBuf d_desc, d_encp, d_keys, d_sync, d_enc, d_out, d_xchg, d_flags, d_prof;
     std::vector<uint8_t> h_desc;
+    HostBuf h_out;             // staging of host-memory outputs
     int last_iters = 0;
 };
 
@@ -717,9 +741,23 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     const float *enc = bt->enc;
     if (host && rows > 0) {
         if ((rc = dec->d_enc.ensure((size_t)rows * D * 4))) return rc;
-        for (int i = 0; i < m; ++i)
-            HIP_TRY(hipMemcpyAsync(dec->d_enc.as<float>() + (size_t)dst_row[i] * D, bt->enc + (size_t)src_row[i] * D,
-                                   (size_t)T[i] * D * 4, hipMemcpyHostToDevice, dec->stream));
+        // one copy per run of utterances whose source rows follow each other
+        // (one copy in all when the caller packs them in order); the device
+        // rows are packed in utterance order
+        for (int i = 0; i < m;) {
+            int j = i + 1;
+            long long end = src_row[i] + T[i];
+            while (j < m && (T[j] == 0 || src_row[j] == end)) {
+                if (T[j] > 0) end = src_row[j] + T[j];
+                ++j;
+            }
+            const long long n_rows = end - src_row[i];
+            if (n_rows > 0)
+                HIP_TRY(hipMemcpyAsync(dec->d_enc.as<float>() + (size_t)dst_row[i] * D,
+                                       bt->enc + (size_t)src_row[i] * D, (size_t)n_rows * D * 4,
+                                       hipMemcpyHostToDevice, dec->stream));
+            i = j;
+        }
         enc = dec->d_enc.as<float>();
         src_row = dst_row;
     }
@@ -897,31 +935,51 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     int status[4] = {0, 0, 0, 0};
     HIP_TRY(hipMemcpyAsync(status, p.status, sizeof status, hipMemcpyDeviceToHost, dec->stream));
     if (host) {
-        std::vector<int> tmp_ntok(m), tmp_steps(m), tmp_nseg(m);
-        HIP_TRY(hipMemcpyAsync(tmp_ntok.data(), o_ntok, 4 * (size_t)m, hipMemcpyDeviceToHost, dec->stream));
-        HIP_TRY(hipMemcpyAsync(tmp_steps.data(), o_steps, 4 * (size_t)m, hipMemcpyDeviceToHost, dec->stream));
-        HIP_TRY(hipMemcpyAsync(tmp_nseg.data(), o_nseg, 4 * (size_t)m, hipMemcpyDeviceToHost, dec->stream));
+        // the counters of every utterance in one copy (n_tokens, steps,
+        // n_segments are consecutive), then the filled prefix of each output
+        // row in one strided copy per array, staged in pinned memory
+        std::vector<int> cnt(3 * (size_t)m);
+        HIP_TRY(hipMemcpyAsync(cnt.data(), o_ntok, 12 * (size_t)m, hipMemcpyDeviceToHost, dec->stream));
         HIP_TRY(hipStreamSynchronize(dec->stream));
+        const int *c_tok = cnt.data(), *c_steps = c_tok + m, *c_seg = c_steps + m;
+        int wt = 0, ws = 0, wr = 0;
+        for (int i = 0; i < m; ++i) {
+            wt = std::max(wt, std::min(c_tok[i], tcap));
+            ws = std::max(ws, std::min(c_seg[i], scap));
+            wr = std::max(wr, std::min(c_steps[i], trcap));
+        }
+        if (!bt->segments) ws = 0;
+        if (!o_trace) wr = 0;
+        const size_t stage = (size_t)m * (wt + ws + 2 * (size_t)wr) * 4;
+        if (stage > 0) {
+            if ((rc = dec->h_out.ensure(stage))) return rc;
+            int *s_tok = dec->h_out.as<int>(), *s_seg = s_tok + (size_t)m * wt, *s_tr = s_seg + (size_t)m * ws;
+            if (wt)
+                HIP_TRY(hipMemcpy2DAsync(s_tok, 4 * (size_t)wt, o_tok, 4 * (size_t)tcap, 4 * (size_t)wt, m,
+                                         hipMemcpyDeviceToHost, dec->stream));
+            if (ws)
+                HIP_TRY(hipMemcpy2DAsync(s_seg, 4 * (size_t)ws, o_seg, 4 * (size_t)scap, 4 * (size_t)ws, m,
+                                         hipMemcpyDeviceToHost, dec->stream));
+            if (wr)
+                HIP_TRY(hipMemcpy2DAsync(s_tr, 8 * (size_t)wr, o_trace, 8 * (size_t)trcap, 8 * (size_t)wr, m,
+                                         hipMemcpyDeviceToHost, dec->stream));
+            HIP_TRY(hipStreamSynchronize(dec->stream));
+        }
+        const int *s_tok = dec->h_out.as<int>(), *s_seg = s_tok + (size_t)m * wt, *s_tr = s_seg + (size_t)m * ws;
         for (int i = 0; i < m; ++i) {
             const int u = map[i];
-            bt->n_tokens[u] = tmp_ntok[i];
-            bt->steps[u] = tmp_steps[i];
-            const int nt = std::min(tmp_ntok[i], tcap);
-            if (nt > 0)
-                HIP_TRY(hipMemcpy(bt->tokens + (size_t)u * tcap, o_tok + (size_t)i * tcap, 4 * (size_t)nt,
-                                  hipMemcpyDeviceToHost));
-            if (bt->n_segments) bt->n_segments[u] = tmp_nseg[i];
-            if (bt->segments && scap > 0) {
-                const int ns = std::min(tmp_nseg[i], scap);
-                if (ns > 0)
-                    HIP_TRY(hipMemcpy(bt->segments + (size_t)u * scap, o_seg + (size_t)i * scap, 4 * (size_t)ns,
-                                      hipMemcpyDeviceToHost));
+            bt->n_tokens[u] = c_tok[i];
+            bt->steps[u] = c_steps[i];
+            const int nt = std::min(c_tok[i], tcap);
+            if (nt > 0) memcpy(bt->tokens + (size_t)u * tcap, s_tok + (size_t)i * wt, 4 * (size_t)nt);
+            if (bt->n_segments) bt->n_segments[u] = c_seg[i];
+            if (ws) {
+                const int ns = std::min(c_seg[i], scap);
+                if (ns > 0) memcpy(bt->segments + (size_t)u * scap, s_seg + (size_t)i * ws, 4 * (size_t)ns);
             }
-            if (o_trace) {
-                const int ns = std::min(tmp_steps[i], trcap);
-                if (ns > 0)
-                    HIP_TRY(hipMemcpy(bt->trace + (size_t)u * trcap * 2, o_trace + (size_t)i * trcap * 2,
-                                      8 * (size_t)ns, hipMemcpyDeviceToHost));
+            if (wr) {
+                const int ns = std::min(c_steps[i], trcap);
+                if (ns > 0) memcpy(bt->trace + (size_t)u * trcap * 2, s_tr + (size_t)i * wr * 2, 8 * (size_t)ns);
             }
         }
     } else {

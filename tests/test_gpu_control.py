@@ -229,3 +229,40 @@ def test_device_memory_batch_matches_host(tmp_path, kind):
         assert steps[u] == want[u]["steps"], u
         if kind == "eou":
             assert segs[u, :nseg[u]].tolist() == want[u]["segments"].tolist(), u
+
+
+def test_host_memory_scattered_rows(tmp_path):
+    """Host buffers whose utterances are not packed in order (gaps, reversed
+    order, a zero-frame EOU window): the uploads follow runs of consecutive
+    rows and the results equal the packed batch's."""
+    import ctypes as C
+    from parakeet_amd import pk, synth
+    path = str(tmp_path / "e.gguf")
+    small_eou(path)
+    dec = pk.Decoder.from_gguf(path, n_slots=12)
+    D = dec.info.D
+    Ts = [7, 0, 12, 3, 9, 4]
+    encs = [synth.encoder_frames(600 + u, T, D) for u, T in enumerate(Ts)]
+    want = dec.decode(encs, slots=list(range(6)), max_symbols=5)
+    # rows: utterances 0 and 1 back to back, 2 after a gap, 3..5 in reverse order
+    order_rows = {0: 0, 1: 7, 2: 10, 5: 30, 4: 34, 3: 43}
+    frames = np.full((50, D), np.nan, np.float32)
+    for u, r in order_rows.items():
+        frames[r:r + Ts[u]] = encs[u]
+    rows = np.array([order_rows[u] for u in range(6)], np.int64)
+    T = np.array(Ts, np.int32)
+    slots = np.arange(6, 12, dtype=np.int32)
+    cap = max(Ts) * 5 + 1
+    toks = np.zeros((6, cap), np.int32)
+    ntok, steps, nseg = np.zeros(6, np.int32), np.zeros(6, np.int32), np.zeros(6, np.int32)
+    segs = np.zeros((6, cap + 1), np.int32)
+    b = pk.PkBatch()
+    b.n_utts, b.mem, b.d_enc, b.max_symbols = 6, pk.MEM_HOST, D, 5
+    b.enc, b.enc_row, b.n_frames, b.slot = pk._ptr(frames), pk._ptr(rows), pk._ptr(T), pk._ptr(slots)
+    b.tokens, b.token_cap, b.n_tokens, b.steps = pk._ptr(toks), cap, pk._ptr(ntok), pk._ptr(steps)
+    b.segments, b.seg_cap, b.n_segments = pk._ptr(segs), cap + 1, pk._ptr(nseg)
+    pk.check(pk.lib().pk_decode(dec.h, C.byref(b)))
+    for u in range(6):
+        assert toks[u, :ntok[u]].tolist() == want[u]["tokens"].tolist(), u
+        assert steps[u] == want[u]["steps"], u
+        assert segs[u, :nseg[u]].tolist() == want[u]["segments"].tolist(), u
