@@ -798,9 +798,10 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     HIP_TRY(hipEventRecord(dec->ev[0], dec->stream));
     if (rows > 0) {
         if ((rc = dec->d_encp.ensure((size_t)rows * J * 4))) return rc;
-        dim3 grid((max_T + pkdev::kEpTile - 1) / pkdev::kEpTile, m, (J + pkdev::kEpTile - 1) / pkdev::kEpTile);
+        // tiles over the packed rows of all utterances
+        dim3 grid((unsigned)((rows + pkdev::kEpTile - 1) / pkdev::kEpTile), 1, (J + pkdev::kEpTile - 1) / pkdev::kEpTile);
         pkdev::enc_proj_kernel<<<grid, 256, 0, dec->stream>>>(dec->w_enc_hi, dec->w_enc_lo, J, dec->b_enc, enc, D,
-                                                              d_src, d_dst, d_T, dec->d_encp.as<float>());
+                                                              d_src, d_dst, m, rows, dec->d_encp.as<float>());
         HIP_TRY(hipGetLastError());
     }
     HIP_TRY(hipEventRecord(dec->ev[1], dec->stream));

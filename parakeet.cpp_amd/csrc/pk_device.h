@@ -278,35 +278,46 @@ __global__ void __launch_bounds__(256) embed_proj_kernel(const float *__restrict
 // GEMM with f32 accuracy.  Frames (f32) are split into f16 hi + lo when staged
 // in LDS; W_e arrives as f16 hi / lo planes [J][D] (split once at load).
 // Each 16x16 output tile takes hi.hi + lo.hi + hi.lo (the lo.lo term is below
-// f32 rounding).  Workgroup: 64 frames x 64 outputs, 4 waves of 16 frames;
-// K steps of 32.  d_enc % 32 == 0.
+// f32 rounding).  Workgroup: 64 output rows x 64 outputs, 4 waves of 16 rows;
+// K steps of 32.  d_enc % 32 == 0.  Output rows are the frames of all
+// utterances packed in order (utterance u owns rows dst_row[u] ..
+// dst_row[u] + T[u]), so short windows of many utterances share tiles; a
+// row's utterance is the last u with dst_row[u] <= row.
 constexpr int kEpTile = 64, kEpK = 32, kEpStride = kEpK + 8;   // LDS row stride in halves
 __global__ void __launch_bounds__(256) enc_proj_kernel(const _Float16 *__restrict whi, const _Float16 *__restrict wlo,
                                                        int J, const float *__restrict bias,
                                                        const float *__restrict enc, int d_enc,
                                                        const long long *__restrict src_row,
-                                                       const long long *__restrict dst_row,
-                                                       const int *__restrict T, float *__restrict out) {
+                                                       const long long *__restrict dst_row, int n_utts,
+                                                       long long rows, float *__restrict out) {
     __shared__ __attribute__((aligned(16))) _Float16 ah[kEpTile * kEpStride], al[kEpTile * kEpStride];
     __shared__ __attribute__((aligned(16))) _Float16 bh[kEpTile * kEpStride], bl[kEpTile * kEpStride];
-    const int u = blockIdx.y;
-    const int Tu = T[u];
-    const int m0 = blockIdx.x * kEpTile;
-    if (m0 >= Tu) return;
+    const long long m0 = (long long)blockIdx.x * kEpTile;
     const int n0 = blockIdx.z * kEpTile;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const float *src = enc + (size_t)src_row[u] * d_enc;
     const int sr = tid / 4, sc = (tid % 4) * 8;   // staging: row / column of this thread's 8 values
+    // the source frame of this thread's staging row
+    const long long r = m0 + sr;
+    const bool live = r < rows;
+    const float *src = enc;
+    if (live) {
+        int lo = 0, hi = n_utts - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (dst_row[mid] <= r) lo = mid;
+            else hi = mid - 1;
+        }
+        src = enc + (size_t)(src_row[lo] + (r - dst_row[lo])) * d_enc;
+    }
     f32x4 acc[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int k0 = 0; k0 < d_enc; k0 += kEpK) {
         {
-            const int row = m0 + sr;
             float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
-            if (row < Tu) {
-                v0 = *reinterpret_cast<const float4 *>(src + (size_t)row * d_enc + k0 + sc);
-                v1 = *reinterpret_cast<const float4 *>(src + (size_t)row * d_enc + k0 + sc + 4);
+            if (live) {
+                v0 = *reinterpret_cast<const float4 *>(src + k0 + sc);
+                v1 = *reinterpret_cast<const float4 *>(src + k0 + sc + 4);
             }
             const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
             half8 h, l;
@@ -341,8 +352,7 @@ __global__ void __launch_bounds__(256) enc_proj_kernel(const _Float16 *__restric
         }
         __syncthreads();
     }
-    // D fragment: lane holds output column 16t + lane % 16 of frames 4 (lane / 16) .. +3
-    float *dst = out + (size_t)dst_row[u] * J;
+    // D fragment: lane holds output column 16t + lane % 16 of rows 4 (lane / 16) .. +3
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const int col = n0 + t * 16 + (lane & 15);
@@ -350,8 +360,8 @@ __global__ void __launch_bounds__(256) enc_proj_kernel(const _Float16 *__restric
         const float bc = bias[col];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = m0 + wave * 16 + (lane >> 4) * 4 + i;
-            if (row < Tu) dst[(size_t)row * J + col] = acc[t][i] + bc;
+            const long long row = m0 + wave * 16 + (lane >> 4) * 4 + i;
+            if (row < rows) out[(size_t)row * J + col] = acc[t][i] + bc;
         }
     }
 }
