@@ -274,7 +274,7 @@ struct pk_decoder {
     DevBuf slots_h, slots_c, slots_pp, slots_r, slots_ctrl;
     DevBuf special;
     // per-call scratch
-    DevBuf d_desc, d_encp, d_keys, d_sync, d_enc, d_out, d_xchg, d_flags, d_prof;
+    DevBuf d_desc, d_encp, d_clear, d_enc, d_out, d_xchg, d_prof;   // d_clear: status, barrier flags, argmax keys
     std::vector<uint8_t> h_desc;
     HostBuf h_out;             // staging of host-memory outputs
     int last_iters = 0;
@@ -849,21 +849,24 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     p.shards = 1;
     while (p.shards < pkdev::kShards && p.shards * 8 < pl.P) p.shards *= 2;
     const size_t keys_bytes = (size_t)2 * m * p.shards * 2 * 8;
-    if ((rc = dec->d_keys.ensure(keys_bytes))) return rc;
-    if ((rc = dec->d_sync.ensure(64))) return rc;
-    if ((rc = dec->d_flags.ensure((size_t)nwg * kFlagStride * 4))) return rc;
+    // the words every launch starts from zero, in one allocation cleared by
+    // one fill: 64 B of status, the barrier flags, the argmax keys
+    const size_t flags_bytes = (size_t)nwg * kFlagStride * 4, clear_bytes = 256 + flags_bytes + keys_bytes;
+    if ((rc = dec->d_clear.ensure(clear_bytes))) return rc;
     const size_t xh = 2 * (size_t)L * m * H, xp = (size_t)m * J, xr = 2 * (size_t)L * m * 4 * H;
+    // the loop addresses the exchange buffers with 32-bit buffer offsets
+    if ((2 * xh + xp + xr) * 4 >= (1ull << 31))
+        return fail(PK_ERR_UNSUPPORTED, "exchange buffers of %d utterances exceed 2 GiB", m);
     if ((rc = dec->d_xchg.ensure((2 * xh + xp + xr) * 4))) return rc;
     p.hx = dec->d_xchg.as<float>();
     p.cx = p.hx + xh;
     p.ppx = p.cx + xh;
     p.rx = p.ppx + xp;
-    p.keys = dec->d_keys.as<unsigned long long>();
-    p.flags = dec->d_flags.as<unsigned>();
-    p.status = dec->d_sync.as<int>() + 4;
-    HIP_TRY(hipMemsetAsync(dec->d_keys.p, 0, keys_bytes, dec->stream));
-    HIP_TRY(hipMemsetAsync(dec->d_sync.p, 0, 64, dec->stream));
-    HIP_TRY(hipMemsetAsync(dec->d_flags.p, 0, (size_t)nwg * kFlagStride * 4, dec->stream));
+    p.xchg_bytes = (unsigned)((2 * xh + xp + xr) * 4);
+    p.status = dec->d_clear.as<int>() + 4;
+    p.flags = reinterpret_cast<unsigned *>(dec->d_clear.as<uint8_t>() + 256);
+    p.keys = reinterpret_cast<unsigned long long *>(dec->d_clear.as<uint8_t>() + 256 + flags_bytes);
+    HIP_TRY(hipMemsetAsync(dec->d_clear.p, 0, clear_bytes, dec->stream));
     // PK_PROFILE_PHASES=1: workgroup 0 accumulates per-phase wall-clock time (stderr summary)
     const bool prof = getenv("PK_PROFILE_PHASES") != nullptr;
     p.prof = nullptr;

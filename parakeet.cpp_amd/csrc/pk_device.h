@@ -93,6 +93,7 @@ struct KParams {
     float *cx;           // [2][L][n][H]
     float *ppx;          // [n][J]
     float *rx;           // [2][L][n][4H]  W_hh . h (no bias), unit-major rows, ping-pong like hx
+    unsigned xchg_bytes; // hx, cx, ppx, rx: one allocation in this order, from hx
     // domains: independent utterance groups, each on dom_size workgroups
     int n_dom, dom_size, nt;
     const int *dom_n;            // [n_dom] utterances per domain
@@ -477,6 +478,31 @@ __device__ __forceinline__ size_t rx_off(const KParams &p, int buf, int layer, i
 struct Bufs {
     __amdgpu_buffer_rsrc_t hx, cx, ppx, rx, ep, encp;
 };
+
+// One utterance's slot state in float4 chunks: h of every layer, c_0, pp,
+// R_0 (c and R of layers >= 1 live in the LDS state during a launch).  Chunk
+// q is at `slot` in its slot array and at float offset `x` from p.hx in the
+// exchange buffers (hx, cx, ppx, rx are consecutive).
+struct StateChunk {
+    float *slot;
+    long long x;
+};
+__device__ __forceinline__ int state_chunks(const KParams &p) { return (p.L * p.H + p.H + p.J + 4 * p.H) / 4; }
+__device__ __forceinline__ StateChunk state_chunk(const KParams &p, int q, int slot, int b, int buf) {
+    const int H = p.H, L = p.L, J = p.J;
+    int i = 4 * q;
+    if (i < L * H) {
+        const int l = i / H;
+        return {p.slot_h + (size_t)slot * L * H + i, (long long)hx_off(p, buf, l, b) + (i - l * H)};
+    }
+    i -= L * H;
+    if (i < H) return {p.slot_c + (size_t)slot * L * H + i, (long long)(p.cx - p.hx) + (long long)hx_off(p, buf, 0, b) + i};
+    i -= H;
+    if (i < J) return {p.slot_pp + (size_t)slot * J + i, (long long)(p.ppx - p.hx) + (long long)b * J + i};
+    i -= J;
+    return {p.slot_r + (size_t)slot * L * 4 * H + i, (long long)(p.rx - p.hx) + (long long)rx_off(p, buf, 0, b) + i};
+}
+constexpr int kCopyB = 4;   // float4 per thread in flight when copying state
 
 // Stage vectors of length K for n <= 16 utterances into an activation block:
 // row u <- src(off(u)) via coherent loads; rows n .. 15 are zero.  Every
@@ -893,26 +919,36 @@ __device__ __forceinline__ void bias_table(const KParams &p, int rank, int P, fl
 }
 
 // Copy this workgroup's tiles of m (rank, rank+P, ...) into its LDS cache:
-// per K block the fragment, then (q8_0) the 16 block scales.
+// per K block the fragment, then (q8_0) the 16 block scales.  kCacheB 16-byte
+// chunks per thread are loaded before any is stored.
+constexpr int kCacheB = 8;
+__device__ __forceinline__ const unsigned char *cache_src(const TMat &m, int rank, int P, int chunks, int c) {
+    const int ch = c % chunks, blk = c / chunks;      // blk = local tile * KB + kb
+    const int li = blk / m.KB, kb = blk % m.KB;
+    const size_t f = (size_t)(rank + li * P) * m.KB + kb;   // global fragment index
+    if (m.type == PK_TYPE_Q8_0)
+        return ch < 32 ? static_cast<const unsigned char *>(m.a) + f * 512 + ch * 16
+                       : reinterpret_cast<const unsigned char *>(m.scale) + f * 32 + (ch - 32) * 16;
+    if (m.type == PK_TYPE_F16) return static_cast<const unsigned char *>(m.a) + f * 1024 + ch * 16;
+    return static_cast<const unsigned char *>(ch < 64 ? m.a : m.a_lo) + f * 1024 + (ch % 64) * 16;
+}
 __device__ __forceinline__ void cache_matrix(const TMat &m, int rank, int P, unsigned char *wc) {
     if (m.lds_off < 0) return;
     const int n = owned(m.tiles, rank, P);
     const int bpb = cache_block_bytes(m.type), chunks = bpb / 16;
-    const size_t nchunk = (size_t)n * m.KB * chunks;
-    for (size_t c = threadIdx.x; c < nchunk; c += kBlock) {
-        const int ch = (int)(c % chunks);
-        const size_t blk = c / chunks;                      // local tile * KB + kb
-        const int li = (int)(blk / m.KB), kb = (int)(blk % m.KB);
-        const size_t f = (size_t)(rank + li * P) * m.KB + kb;   // global fragment index
-        const unsigned char *src;
-        if (m.type == PK_TYPE_Q8_0)
-            src = ch < 32 ? static_cast<const unsigned char *>(m.a) + f * 512 + ch * 16
-                          : reinterpret_cast<const unsigned char *>(m.scale) + f * 32 + (ch - 32) * 16;
-        else if (m.type == PK_TYPE_F16)
-            src = static_cast<const unsigned char *>(m.a) + f * 1024 + ch * 16;
-        else
-            src = static_cast<const unsigned char *>(ch < 64 ? m.a : m.a_lo) + f * 1024 + (ch % 64) * 16;
-        *reinterpret_cast<uint4 *>(wc + m.lds_off + blk * bpb + ch * 16) = *reinterpret_cast<const uint4 *>(src);
+    const int nchunk = n * m.KB * chunks;
+    if (nchunk == 0) return;
+    for (int base = 0; base < nchunk; base += kCacheB * kBlock) {
+        uint4 v[kCacheB];
+#pragma unroll
+        for (int j = 0; j < kCacheB; ++j)   // clamped: chunks past the end reload the last one
+            v[j] = *reinterpret_cast<const uint4 *>(cache_src(m, rank, P, chunks, min(base + (int)threadIdx.x + j * kBlock, nchunk - 1)));
+#pragma unroll
+        for (int j = 0; j < kCacheB; ++j) {
+            const int c = base + threadIdx.x + j * kBlock;
+            if (c < nchunk)   // local offset: (local tile * KB + kb) * bpb + chunk * 16
+                *reinterpret_cast<uint4 *>(wc + m.lds_off + (size_t)(c / chunks) * bpb + (c % chunks) * 16) = v[j];
+        }
     }
 }
 
@@ -958,9 +994,8 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         lds_sync();
         TL(0);
         pmark(p, s, tlast, kPrJStage);
-        // bias rows of this wave's first two items and the blank offset of this
-        // lane's utterance, loaded before the products
-        const int u = lane & 15, wave = threadIdx.x / kWave;
+        // the blank offset of this lane's utterance, loaded before the products
+        const int u = lane & 15;
         const float bb = u < nc ? s.bbias[s.jst[c0 + u]] : 0.0f;
         // (b_out is zero-padded to whole tiles)
         const float *btab = S.bias + bias_base(p, s.rank, s.P, p.L);
@@ -1083,12 +1118,12 @@ __device__ __forceinline__ float *st_at(const KParams &p, const Lds &S, int l, i
 
 __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Lds &S, const Bufs &B, const Act &x,
                                               int lc, int c0, int nc) {
-    const int lane = threadIdx.x & (kWave - 1), H = p.H;
+    const int lane = threadIdx.x & (kWave - 1);
     const bool last = lc == p.L - 1;
     const TMat &wc = last ? p.w_pred : p.w_ih[lc + 1];
     const TMat &wr = p.w_hh[lc];
     const int n_c = owned(wc.tiles, s.rank, s.P), n_r = owned(wr.tiles, s.rank, s.P);
-    const int wave = threadIdx.x / kWave, layer = lc + 1, u = lane & 15, g = lane >> 4;
+    const int layer = lc + 1, u = lane & 15, g = lane >> 4;
     // this lane's utterance (a valid index for every lane; lanes u >= nc store nothing)
     const int ul = s.lst[c0 + min(u, nc - 1)], b = s.b[ul], cur = s.cur[ul];
     const bool zero = s.flags[ul] & kFlagZeroHC;
@@ -1372,18 +1407,28 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         else s.t[ul] = 0;
     }
     __syncthreads();
-    // copy the slot state of this workgroup's utterances into the exchange buffers
+    // copy the slot state of this workgroup's utterances into the exchange
+    // buffers (kCopyB loads in flight per thread, then the stores)
+    const __amdgpu_buffer_rsrc_t bx = rsrc(p.hx, p.xchg_bytes);
+    const int nq = state_chunks(p);
     for (int ul = s.rank; ul < s.n; ul += s.P) {
         const int b = s.b[ul], slot = p.slot[b];
-        for (int i = threadIdx.x; i < L * H; i += kBlock) {
-            const int l = i / H, k = i - l * H;
-            st_coh(p.hx + hx_off(p, 0, l, b) + k, p.slot_h[(size_t)slot * L * H + i]);
+        for (int q0 = 0; q0 < nq; q0 += kCopyB * kBlock) {
+            float4 v[kCopyB];
+            long long xo[kCopyB];
+#pragma unroll
+            for (int j = 0; j < kCopyB; ++j) {
+                const int q = q0 + threadIdx.x + j * kBlock;
+                if (q < nq) {
+                    const StateChunk c = state_chunk(p, q, slot, b, 0);
+                    v[j] = *reinterpret_cast<const float4 *>(c.slot);
+                    xo[j] = c.x;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < kCopyB; ++j)
+                if (q0 + threadIdx.x + j * kBlock < nq) st4_coh(bx, (unsigned)(xo[j] * 4), v[j]);
         }
-        for (int i = threadIdx.x; i < H; i += kBlock)   // layer 0; layers >= 1 go to the LDS state
-            st_coh(p.cx + hx_off(p, 0, 0, b) + i, p.slot_c[(size_t)slot * L * H + i]);
-        for (int i = threadIdx.x; i < J; i += kBlock) st_coh(p.ppx + (size_t)b * J + i, p.slot_pp[(size_t)slot * J + i]);
-        for (int i = threadIdx.x; i < 4 * H; i += kBlock)
-            st_coh(p.rx + rx_off(p, 0, 0, b) + i, p.slot_r[(size_t)slot * L * 4 * H + i]);
     }
     bias_table(p, s.rank, s.P, S.bias);
     // LDS state of layers >= 1: R and c of this workgroup's unit tiles for every utterance of the domain
@@ -1466,15 +1511,20 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
     for (int ul = s.rank; ul < s.n; ul += s.P) {
         const int b = s.b[ul], slot = p.slot[b];
         const int cur = s.cur[ul];
-        for (int i = threadIdx.x; i < L * H; i += kBlock) {
-            const int l = i / H, k = i - l * H;
-            p.slot_h[(size_t)slot * L * H + i] = ld_coh(p.hx + hx_off(p, cur, l, b) + k);
+        for (int q0 = 0; q0 < nq; q0 += kCopyB * kBlock) {
+            float4 v[kCopyB];
+            float *dst[kCopyB];
+#pragma unroll
+            for (int j = 0; j < kCopyB; ++j) {
+                const int q = q0 + threadIdx.x + j * kBlock;
+                const StateChunk c = state_chunk(p, min(q, nq - 1), slot, b, cur);
+                v[j] = ld4_coh(bx, q < nq ? (unsigned)(c.x * 4) : kBad);
+                dst[j] = c.slot;
+            }
+#pragma unroll
+            for (int j = 0; j < kCopyB; ++j)
+                if (q0 + threadIdx.x + j * kBlock < nq) *reinterpret_cast<float4 *>(dst[j]) = v[j];
         }
-        for (int i = threadIdx.x; i < H; i += kBlock)   // layer 0; layers >= 1 come from the LDS state
-            p.slot_c[(size_t)slot * L * H + i] = ld_coh(p.cx + hx_off(p, cur, 0, b) + i);
-        for (int i = threadIdx.x; i < J; i += kBlock) p.slot_pp[(size_t)slot * J + i] = ld_coh(p.ppx + (size_t)b * J + i);
-        for (int i = threadIdx.x; i < 4 * H; i += kBlock)
-            p.slot_r[(size_t)slot * L * 4 * H + i] = ld_coh(p.rx + rx_off(p, cur, 0, b) + i);
         if (threadIdx.x == 0) {
             int *ctrl = p.slot_ctrl + (size_t)slot * PK_CTRL_N;
             ctrl[PK_CTRL_INIT] = 1;
