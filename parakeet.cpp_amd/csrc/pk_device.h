@@ -193,14 +193,13 @@ struct Act {
     int n;      // live rows
 };
 
+// Four values split as in split_f16 (packed conversions).
 __device__ __forceinline__ void put4(const Act &x, int row, int k, float4 v) {
-    _Float16 h0, h1, h2, h3, l0, l1, l2, l3;
-    split_f16(v.x, h0, l0);
-    split_f16(v.y, h1, l1);
-    split_f16(v.z, h2, l2);
-    split_f16(v.w, h3, l3);
-    *reinterpret_cast<half4 *>(x.hi + row * x.kp + k) = half4{h0, h1, h2, h3};
-    *reinterpret_cast<half4 *>(x.lo + row * x.kp + k) = half4{l0, l1, l2, l3};
+    const f32x4 f = {v.x, v.y, v.z, v.w};
+    const half4 h = __builtin_convertvector(f, half4);
+    const half4 l = __builtin_convertvector(f - __builtin_convertvector(h, f32x4), half4);
+    *reinterpret_cast<half4 *>(x.hi + row * x.kp + k) = h;
+    *reinterpret_cast<half4 *>(x.lo + row * x.kp + k) = l;
 }
 
 // ---------------------------------------------------------------- argmax keys
@@ -507,25 +506,28 @@ constexpr int kCopyB = 4;   // float4 per thread in flight when copying state
 // Stage vectors of length K for n <= 16 utterances into an activation block:
 // row u <- src(off(u)) via coherent loads; rows n .. 15 are zero.  Every
 // thread issues all of its loads before converting any of them.
-constexpr int kStageMax = 5;    // float4 per thread per round: one round covers 16 rows of K <= 640
+// Staging: 32 threads per row, so a 512-thread block covers 16 rows per
+// round; each thread resolves its row once and moves float4 chunks sub,
+// sub + 32, ... (kStageMax per thread in flight: 160 float4 = K 640 per pass).
+constexpr int kStageMax = 5, kStageTpr = 32;
 template <class OffFn>
 __device__ __forceinline__ void stage_act(const Act &x, int K, int n, __amdgpu_buffer_rsrc_t r, OffFn off) {
-    const int per = K / 4;
-    for (int base = 0; base < n * per; base += kStageMax * kBlock) {
-        float4 v[kStageMax];
+    const int per = K / 4, sub = threadIdx.x % kStageTpr;
+    for (int u0 = 0; u0 < n; u0 += kBlock / kStageTpr) {
+        const int u = u0 + threadIdx.x / kStageTpr;
+        const bool live = u < n;
+        const unsigned row = (unsigned)(off(live ? u : n - 1) * 4);   // byte offset of the row
+        for (int k0 = 0; k0 < per; k0 += kStageTpr * kStageMax) {
+            float4 v[kStageMax];
 #pragma unroll
-        for (int j = 0; j < kStageMax; ++j) {
-            const int i = base + threadIdx.x + j * kBlock;
-            const int u = i / per, k = (i - u * per) * 4;
-            const bool ok = i < n * per;
-            v[j] = ld4_coh(r, ok ? (unsigned)((off(min(u, n - 1)) + k) * 4) : kBad);
-        }
+            for (int j = 0; j < kStageMax; ++j) {
+                const int k4 = k0 + sub + kStageTpr * j;
+                v[j] = ld4_coh(r, live && k4 < per ? row + (unsigned)k4 * 16 : kBad);
+            }
 #pragma unroll
-        for (int j = 0; j < kStageMax; ++j) {
-            const int i = base + threadIdx.x + j * kBlock;
-            if (i < n * per) {
-                const int u = i / per, k = (i - u * per) * 4;
-                put4(x, u, k, v[j]);
+            for (int j = 0; j < kStageMax; ++j) {
+                const int k4 = k0 + sub + kStageTpr * j;
+                if (live && k4 < per) put4(x, u, k4 * 4, v[j]);
             }
         }
     }
@@ -963,30 +965,36 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         const int nc = min(kTile, s.nj - c0);
         Act x = S.act[0];
         x.n = nc;
-        // stage hidden = relu(encp[t] + pp) for this column tile
-        for (int base = 0; base < nc * (J / 4); base += kStageMax * kBlock) {
-            const int per = J / 4;
-            float4 e[kStageMax], q[kStageMax];
+        // stage hidden = relu(encp[t] + pp) for this column tile (row mapping as in stage_act)
+        {
+            const int per = J / 4, sub = threadIdx.x % kStageTpr;
+            for (int u0 = 0; u0 < nc; u0 += kBlock / kStageTpr) {
+                const int u = u0 + threadIdx.x / kStageTpr;
+                const bool live = u < nc;
+                const int ul = s.jst[c0 + (live ? u : nc - 1)];
+                const unsigned erow = (unsigned)((size_t)(s.erow[ul] + s.t[ul]) * J * 4);
+                const unsigned prow = (unsigned)((size_t)s.b[ul] * J * 4);
+                for (int k0 = 0; k0 < per; k0 += kStageTpr * kStageMax) {
+                    float4 e[kStageMax], q[kStageMax];
 #pragma unroll
-            for (int j = 0; j < kStageMax; ++j) {
-                const int i = base + threadIdx.x + j * kBlock;
-                const int u = i / per, k = (i - u * per) * 4;
-                const bool ok = i < nc * per;
-                const int ul = s.jst[c0 + min(u, nc - 1)], b = s.b[ul];
-                e[j] = ld4(B.encp, ok ? (unsigned)(((size_t)(s.erow[ul] + s.t[ul]) * J + k) * 4) : kBad);
-                q[j] = ld4_coh(B.ppx, ok ? (unsigned)(((size_t)b * J + k) * 4) : kBad);
-            }
+                    for (int j = 0; j < kStageMax; ++j) {
+                        const int k4 = k0 + sub + kStageTpr * j;
+                        const bool ok = live && k4 < per;
+                        e[j] = ld4(B.encp, ok ? erow + (unsigned)k4 * 16 : kBad);
+                        q[j] = ld4_coh(B.ppx, ok ? prow + (unsigned)k4 * 16 : kBad);
+                    }
 #pragma unroll
-            for (int j = 0; j < kStageMax; ++j) {
-                const int i = base + threadIdx.x + j * kBlock;
-                if (i < nc * per) {
-                    const int u = i / per, k = (i - u * per) * 4;
-                    float4 v = make_float4(e[j].x + q[j].x, e[j].y + q[j].y, e[j].z + q[j].z, e[j].w + q[j].w);
-                    v.x = (0.0f < v.x) ? v.x : 0.0f;
-                    v.y = (0.0f < v.y) ? v.y : 0.0f;
-                    v.z = (0.0f < v.z) ? v.z : 0.0f;
-                    v.w = (0.0f < v.w) ? v.w : 0.0f;
-                    put4(x, u, k, v);
+                    for (int j = 0; j < kStageMax; ++j) {
+                        const int k4 = k0 + sub + kStageTpr * j;
+                        if (live && k4 < per) {
+                            float4 v = make_float4(e[j].x + q[j].x, e[j].y + q[j].y, e[j].z + q[j].z, e[j].w + q[j].w);
+                            v.x = (0.0f < v.x) ? v.x : 0.0f;
+                            v.y = (0.0f < v.y) ? v.y : 0.0f;
+                            v.z = (0.0f < v.z) ? v.z : 0.0f;
+                            v.w = (0.0f < v.w) ? v.w : 0.0f;
+                            put4(x, u, k4 * 4, v);
+                        }
+                    }
                 }
             }
         }

@@ -238,8 +238,12 @@ class Decoder:
         T = np.array([e.shape[0] if e.ndim == 2 else 0 for e in encs], np.int32)
         rows = np.concatenate([[0], np.cumsum(T)[:-1]]).astype(np.int64) if n else np.zeros(0, np.int64)
         d_enc = encs[0].shape[1] if n and encs[0].ndim == 2 else info.D
-        enc = (np.concatenate([np.ascontiguousarray(e, np.float32).reshape(-1, d_enc) for e in encs])
-               if n and T.sum() > 0 else np.zeros((1, d_enc), np.float32))
+        if n and T.sum() > 0:
+            live = [e for e in encs if e.ndim == 2 and e.shape[0] > 0]
+            enc = (np.concatenate(live) if all(e.dtype == np.float32 for e in live)
+                   else np.concatenate([np.asarray(e, np.float32) for e in live]))
+        else:
+            enc = np.zeros((1, d_enc), np.float32)
         maxT = int(T.max()) if n else 0
         cap = token_cap if token_cap is not None else maxT * max(1, max_symbols) + 1
         toks = np.zeros((n, cap), np.int32)
@@ -259,13 +263,12 @@ class Decoder:
         b.segments, b.seg_cap, b.n_segments = _ptr(segs), cap + 1, _ptr(nseg)
         b.trace, b.trace_cap = (_ptr(tr) if trace else None), tcap
         check(lib().pk_decode(self.h, C.byref(b)))
-        out = []
-        for u in range(n):
-            r = dict(tokens=toks[u, :ntok[u]].copy(), steps=int(steps[u]),
-                     segments=segs[u, :nseg[u]].copy())
-            if trace:
-                r["trace"] = tr[u, :min(steps[u], tcap)].copy()
-            out.append(r)
+        # per-utterance views of this call's output arrays
+        nt, st, ns = ntok.tolist(), steps.tolist(), nseg.tolist()
+        out = [dict(tokens=toks[u, :nt[u]], steps=st[u], segments=segs[u, :ns[u]]) for u in range(n)]
+        if trace:
+            for u in range(n):
+                out[u]["trace"] = tr[u, :min(st[u], tcap)]
         return out
 
     def decode_device(self, enc_ptr: int, enc_row, n_frames, slots, max_symbols: int,
