@@ -375,6 +375,8 @@ struct Ctl {                      // per-workgroup copy of its domain's control 
     int lst[kDomCap], jst[kDomCap];
     long long erow[kDomCap];      // first encp row of each utterance
     float bbias[kDomCap];         // blank logit offset of each utterance
+    int tbase[kDomCap];           // tokens before this call (EOU segment indices)
+    int dur[PK_MAX_DURATIONS];    // duration values (the decision step reads them from LDS)
     int n, nl, nj;
     int dom, rank, P;
     unsigned long long wgkey[kDomCap][2];   // this workgroup's best key per utterance and head
@@ -1281,7 +1283,7 @@ __device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp)
             }
         }
         if (p.kind == PK_KIND_TDT) {
-            const int dur = p.n_dur > 0 ? p.durations[di] : di;
+            const int dur = p.n_dur > 0 ? s.dur[di] : di;
             const int adv = dur > 1 ? dur : 1;
             if (tok == p.blank) {
                 s.t[ul] += adv;
@@ -1305,7 +1307,7 @@ __device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp)
             if (tok == p.blank || tok == p.eob) {
                 frame_done = true;
             } else if (tok == p.eou) {
-                const int total = (p.tokens_base ? p.tokens_base[b] : 0) + s.ntok[ul];
+                const int total = s.tbase[ul] + s.ntok[ul];
                 if (total > s.segst[ul]) {
                     const int ns = s.nseg[ul]++;
                     if (writer) {
@@ -1390,6 +1392,7 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         s.P = p.dom_size;
         s.n = p.dom_n[s.dom];
     }
+    if (threadIdx.x < PK_MAX_DURATIONS) s.dur[threadIdx.x] = threadIdx.x < p.n_dur ? p.durations[threadIdx.x] : 0;
     __syncthreads();
     for (int ul = threadIdx.x; ul < s.n; ul += kBlock) {
         const int b = p.dom_list[s.dom * kDomCap + ul];
@@ -1400,6 +1403,7 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         s.T[ul] = p.T[b];
         s.erow[ul] = p.encp_row[b];
         s.bbias[ul] = p.blank_bias ? p.blank_bias[b] : 0.0f;
+        s.tbase[ul] = p.tokens_base ? p.tokens_base[b] : 0;
         s.ntok[ul] = 0;
         s.steps[ul] = 0;
         s.nseg[ul] = 0;
