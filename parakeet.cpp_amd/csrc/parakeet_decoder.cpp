@@ -454,6 +454,7 @@ int eou_decode_window(const ParakeetCtcModel &model, const EouRuntimeWeights &W,
                       int n_frames, int D_enc, const EouDecodeOptions &opts, EouDecodeState &state,
                       std::vector<int32_t> &out_tokens, std::vector<EouSegmentBoundary> &out_segments,
                       int &out_steps) {
+    (void)model;   // kept for the reference signature; the runtime weights carry every size used here
     if (D_enc != W.D_enc) {
         std::fprintf(stderr, "eou_decode_window: encoder d_model mismatch (%d vs %d)\n", D_enc, W.D_enc);
         return 1;
