@@ -8,10 +8,18 @@ N(0,1), 1024-d, seed 1000+u), max_symbols_per_step 10, every utterance
 decoded in lockstep with on-device compaction.  A decode step is one joint
 evaluation for one utterance (the reference's out_steps counter).
 
-Prints one JSON line.  Extra fields: the B=1, T=125 latency (us/step) and the
-B=256, T=750 throughput on the same decoder, the roofline of the dominant
-kernel (the decode loop), and the CPU baseline (the oracle, a C restatement
-of the reference's scalar decoder, timed on this host on a bounded sample).
+Prints one JSON line.  Extra fields: the roofline of the dominant kernel (the
+decode loop), the CPU baseline (the oracle, a C restatement of the
+reference's scalar decoder, timed on this host on a bounded sample), and the
+other workload shapes (--no-extras skips them):
+  b1                 B=1, T=125 on the same decoder: latency per step
+  b256               B=256, T=750 on the same decoder
+  ragged_b512        B=512, T ~ U{50..1500}, blank-logit offsets {0, +2, +4}
+  tdt11b_f16_b256    TDT-1.1b shapes (vocab 1024), f16 weights, B=256, T=375
+  eou_stream_b128    EOU-120m shapes, q8_0, 128 sessions x 40 chunks of 2 frames,
+                     state carried between chunk calls
+Each carries its own roofline ratio (roofline time of its lockstep
+iterations over the measured loop time).
 """
 from __future__ import annotations
 
@@ -47,31 +55,33 @@ def parse():
 
 
 class Workload:
-    """B utterances of T frames resident on the device, with output buffers and
-    fresh state slots for every call."""
+    """Utterances of Ts[u] frames resident on the device (packed rows), with
+    output buffers and fresh state slots for every call."""
 
-    def __init__(self, pk, hipmem, dec, B, T, D, max_sym, n_calls, slot_base, first_seed=1000,
+    def __init__(self, pk, hipmem, dec, Ts, D, max_sym, n_calls, slot_base, first_seed=1000,
                  blank_bias=None):
         from parakeet_amd import synth
         self.pk, self.hm, self.dec = pk, hipmem, dec
-        self.B, self.T, self.max_sym = B, T, max_sym
-        frames = np.empty((B * T, D), np.float32)
-        for u in range(B):
-            frames[u * T:(u + 1) * T] = synth.encoder_frames(u, T, D, base_seed=first_seed)
+        self.Ts = np.ascontiguousarray(Ts, np.int32)
+        self.B, self.max_sym = len(self.Ts), max_sym
+        self.rows = np.concatenate([[0], np.cumsum(self.Ts, dtype=np.int64)[:-1]]).astype(np.int64)
+        frames = np.empty((int(self.Ts.sum()), D), np.float32)
+        for u in range(self.B):
+            r, t = int(self.rows[u]), int(self.Ts[u])
+            frames[r:r + t] = synth.encoder_frames(u, t, D, base_seed=first_seed)
         self.enc = hipmem.DeviceArray.from_numpy(frames)
         del frames
-        self.rows = np.arange(B, dtype=np.int64) * T
-        self.Ts = np.full(B, T, np.int32)
+        T = int(self.Ts.max())
         self.cap = T * max(1, max_sym) + 1
         self.tcap = T * (max(1, max_sym) + 1) + 1
-        self.out = dict(tokens=hipmem.DeviceArray(4 * B * self.cap), n_tokens=hipmem.DeviceArray(4 * B),
-                        steps=hipmem.DeviceArray(4 * B))
-        self.trace = hipmem.DeviceArray(8 * B * self.tcap)
+        self.out = dict(tokens=hipmem.DeviceArray(4 * self.B * self.cap), n_tokens=hipmem.DeviceArray(4 * self.B),
+                        steps=hipmem.DeviceArray(4 * self.B))
+        self.trace = hipmem.DeviceArray(8 * self.B * self.tcap)
         self.blank_bias = blank_bias
         self.calls = 0
         self.n_calls = n_calls
         self.slot_base = slot_base
-        assert slot_base + B * n_calls <= dec.n_slots
+        assert slot_base + self.B * n_calls <= dec.n_slots
 
     def run(self, trace=False):
         assert self.calls < self.n_calls, "every call decodes fresh slots"
@@ -91,6 +101,10 @@ class Workload:
         tr = self.trace.to_numpy(np.int32, self.B * self.tcap * 2).reshape(self.B, self.tcap, 2)
         return [tr[u, :st[u]] for u in range(self.B)]
 
+    def free(self):
+        for a in (self.enc, self.trace, *self.out.values()):
+            a.free()
+
 
 def timed(wl, warmup, steps):
     for _ in range(warmup):
@@ -107,6 +121,105 @@ def timed(wl, warmup, steps):
     wl.hm.synchronize()
     wall = time.perf_counter() - t0
     return wall, float(np.mean(loop_ms)), float(np.mean(enc_ms)), int(np.max(iters))
+
+
+def matrix_types(rd, pfx):
+    t = rd.tensors
+    return dict(embed=t[f"{pfx}.predict.embed.weight"].ggml_type, lstm=t[f"{pfx}.predict.lstm.0.w_ih"].ggml_type,
+                pred=t[f"{pfx}.joint.pred.weight"].ggml_type, out=t[f"{pfx}.joint.out.weight"].ggml_type,
+                enc=t[f"{pfx}.joint.enc.weight"].ggml_type)
+
+
+def roof_time(roofline, cost, A_j, A_l):
+    """Roofline time of the given lockstep iterations: (seconds, binding resource)."""
+    b, f = cost.iteration(A_j, A_l)
+    tb, tf = b / (roofline.HBM_PEAK_GBS * 1e9), f / (roofline.BF16_PEAK_TFLOPS * 1e12)
+    return float(np.maximum(tb, tf).sum()), ("hbm" if tb.sum() >= tf.sum() else "mfma")
+
+
+def lockstep_extra(pk, hipmem, roofline, dec, cost, Ts, D, MS, slot_base, blank_bias=None, timed_calls=2):
+    """One traced call (decisions for the cost model), one warm-up call, then
+    `timed_calls` timed calls of the same batch on fresh slots."""
+    wl = Workload(pk, hipmem, dec, Ts, D, MS, timed_calls + 2, slot_base, blank_bias=blank_bias)
+    wl.run(trace=True)
+    A_j, A_l = roofline.lockstep_counts(wl.traces(), 0, dec.info.blank)
+    t_roof, bound = roof_time(roofline, cost, A_j, A_l)
+    wall, loop, enc, iters = timed(wl, 1, timed_calls)
+    st = int(wl.steps().sum())
+    wl.free()
+    return {"utterances": len(Ts), "frames_total": int(np.sum(Ts)), "decode_steps": st,
+            "steps_per_s": round(st * timed_calls / wall, 1), "loop_ms": round(loop, 3),
+            "enc_proj_ms": round(enc, 3), "iterations": iters,
+            "us_per_iteration": round(loop * 1e3 / max(1, iters), 3),
+            "roofline": {"bound": bound, "t_roof_over_t_kernel": round(t_roof / (loop * 1e-3), 5)}}
+
+
+def eou_stream_extra(pk, hipmem, roofline, gguf, synth, tmp, B=128, chunks=40, F=2):
+    """EOU-120m-shaped q8_0 decoder: B sessions fed `chunks` chunks of F frames,
+    state carried in the slots.  Frames are resident in HBM; each chunk call
+    reads its token counts back (the caller needs them for the next call's
+    segment base), and that copy is inside the timed wall."""
+    path = os.path.join(tmp, "eou-120m-q8_0.gguf")
+    synth.make_shape(path, "eou-120m")
+    rd = gguf.GGUFReader(path)
+    dec = pk.Decoder(rd, n_slots=2 * B)
+    info = dec.info
+    cost = roofline.DecoderCost(info, matrix_types(rd, "eou"))
+    MS, D = info.max_symbols, info.D
+    frames = np.empty((B * chunks * F, D), np.float32)
+    for u in range(B):
+        frames[u * chunks * F:(u + 1) * chunks * F] = synth.encoder_frames(u, chunks * F, D)
+    enc = hipmem.DeviceArray.from_numpy(frames)
+    del frames
+    cap, tcap, scap = F * max(1, MS) + 1, F * (max(1, MS) + 1) + 1, F * max(1, MS) + 2
+    tok = hipmem.DeviceArray(4 * B * cap * chunks)
+    seg = hipmem.DeviceArray(4 * B * scap * chunks)
+    steps = hipmem.DeviceArray(4 * B * chunks)
+    nseg = hipmem.DeviceArray(4 * B * chunks)
+    ntok = [hipmem.DeviceArray(4 * B) for _ in range(chunks)]
+    tr = hipmem.DeviceArray(8 * B * tcap * chunks)
+    Ts = np.full(B, F, np.int32)
+
+    def stream(slot_base, trace):
+        total = np.zeros(B, np.int32)
+        loop = enc_ms = 0.0
+        slots = np.arange(B, dtype=np.int32) + slot_base
+        for c in range(chunks):
+            rows = np.arange(B, dtype=np.int64) * chunks * F + c * F
+            ptrs = dict(tokens=tok.ptr + 4 * B * cap * c, n_tokens=ntok[c].ptr, steps=steps.ptr + 4 * B * c,
+                        segments=seg.ptr + 4 * B * scap * c, seg_cap=scap, n_segments=nseg.ptr + 4 * B * c)
+            if trace:
+                ptrs["trace"] = tr.ptr + 8 * B * tcap * c
+            dec.decode_device(enc.ptr, rows, Ts, slots, MS, ptrs, cap, trace_cap=tcap if trace else 0,
+                              tokens_base=total)
+            total += ntok[c].to_numpy(np.int32, B)
+            t = dec.last_timing()
+            loop += t["loop_ms"]
+            enc_ms += t["enc_proj_ms"]
+        return total, loop, enc_ms
+
+    stream(0, True)                                        # untimed: decisions for the cost model
+    st = steps.to_numpy(np.int32, B * chunks).reshape(chunks, B)
+    trs = tr.to_numpy(np.int32, chunks * B * tcap * 2).reshape(chunks, B, tcap, 2)
+    t_roof, bound = 0.0, "hbm"
+    for c in range(chunks):
+        A_j, A_l = roofline.lockstep_counts([trs[c, u, :st[c, u]] for u in range(B)], 1, info.blank,
+                                            info.eou_id, info.eob_id, info.special, fresh=(c == 0))
+        t, bound = roof_time(roofline, cost, A_j, A_l)
+        t_roof += t
+    hipmem.synchronize()
+    t0 = time.perf_counter()
+    total, loop, enc_ms = stream(B, False)
+    wall = time.perf_counter() - t0
+    n_steps = int(steps.to_numpy(np.int32, B * chunks).sum())
+    for a in (enc, tok, seg, steps, nseg, tr, *ntok):
+        a.free()
+    dec.close()
+    return {"sessions": B, "chunks": chunks, "frames_per_chunk": F, "decode_steps": n_steps,
+            "tokens": int(total.sum()), "steps_per_s": round(n_steps / wall, 1),
+            "us_per_chunk_call": round(wall / chunks * 1e6, 1),
+            "loop_ms_per_call": round(loop / chunks, 4), "enc_proj_ms_per_call": round(enc_ms / chunks, 4),
+            "roofline": {"bound": bound, "t_roof_over_t_kernel": round(t_roof / (loop * 1e-3), 5)}}
 
 
 def main():
@@ -140,17 +253,12 @@ def main():
     synth.make_shape(path, "tdt-0.6b-v3")
     rd = gguf.GGUFReader(path)
     n_calls = args.warmup + args.steps + 1
-    n_b1, n_b256 = 24, 3
-    dec = pk.Decoder(rd, n_slots=B * n_calls + (0 if args.no_extras else n_b1 + 256 * n_b256))
+    n_b1 = 24
+    dec = pk.Decoder(rd, n_slots=B * n_calls + (0 if args.no_extras else n_b1 + 256 * 4 + 512 * 4))
     info = dec.info
-    types = dict(embed=rd.tensors["tdt.predict.embed.weight"].ggml_type,
-                 lstm=rd.tensors["tdt.predict.lstm.0.w_ih"].ggml_type,
-                 pred=rd.tensors["tdt.joint.pred.weight"].ggml_type,
-                 out=rd.tensors["tdt.joint.out.weight"].ggml_type,
-                 enc=rd.tensors["tdt.joint.enc.weight"].ggml_type)
-    cost = roofline.DecoderCost(info, types)
+    cost = roofline.DecoderCost(info, matrix_types(rd, "tdt"))
 
-    wl = Workload(pk, hipmem, dec, B, T, D, MS, n_calls, 0)
+    wl = Workload(pk, hipmem, dec, np.full(B, T), D, MS, n_calls, 0)
     wl.run(trace=True)                                     # untimed: decisions for the cost model
     traces = wl.traces()
     steps_per_call = int(sum(len(t) for t in traces))
@@ -229,20 +337,32 @@ def main():
 
     if not args.no_extras:
         # B=1, T=125 (10 s of audio): per-step latency
-        wl1 = Workload(pk, hipmem, dec, 1, 125, D, MS, n_b1, B * n_calls)
+        wl1 = Workload(pk, hipmem, dec, np.full(1, 125), D, MS, n_b1, B * n_calls)
         wall1, loop1, enc1, it1 = timed(wl1, 2, 20)
         st1 = int(wl1.steps().sum())
         out["b1"] = {"frames": 125, "decode_steps": st1, "us_per_step_loop": round(loop1 * 1e3 / st1, 3),
                      "us_per_step_incl_enc_proj": round((loop1 + enc1) * 1e3 / st1, 3),
                      "us_per_step_wall": round(wall1 / 20 * 1e6 / st1, 3)}
-        del wl1
-        # B=256, T=750: lockstep throughput
-        wl256 = Workload(pk, hipmem, dec, 256, 750, D, MS, n_b256, B * n_calls + n_b1)
-        wall2, loop2, enc2, it2 = timed(wl256, 1, 2)
-        st2 = int(wl256.steps().sum())
-        out["b256"] = {"frames": 750, "decode_steps": st2, "steps_per_s": round(st2 * 2 / wall2, 1),
-                       "loop_ms": round(loop2, 3), "enc_proj_ms": round(enc2, 3), "iterations": it2}
-        del wl256
+        wl1.free()
+        base = B * n_calls + n_b1
+        # B=256, T=750: lockstep throughput on the same decoder
+        out["b256"] = lockstep_extra(pk, hipmem, roofline, dec, cost, np.full(256, 750), D, MS, base)
+        base += 256 * 4
+        # B=512, T ~ U{50..1500}, blank-logit offsets {0, +2, +4}
+        Tr = synth.ragged_lengths(512)
+        out["ragged_b512"] = lockstep_extra(pk, hipmem, roofline, dec, cost, Tr, D, MS, base,
+                                             blank_bias=synth.blank_offsets(512))
+        # TDT-1.1b shapes, f16 weights, B=256, T=375
+        p11 = os.path.join(tmp, "tdt-1.1b-f16.gguf")
+        synth.make_shape(p11, "tdt-1.1b")
+        rd11 = gguf.GGUFReader(p11)
+        dec11 = pk.Decoder(rd11, n_slots=256 * 4)
+        cost11 = roofline.DecoderCost(dec11.info, matrix_types(rd11, "tdt"))
+        out["tdt11b_f16_b256"] = lockstep_extra(pk, hipmem, roofline, dec11, cost11, np.full(256, 375),
+                                                dec11.info.D, MS, 0)
+        dec11.close()
+        # EOU-120m shapes, q8_0: 128 sessions x 40 chunks of 2 frames, state carried
+        out["eou_stream_b128"] = eou_stream_extra(pk, hipmem, roofline, gguf, synth, tmp)
 
     print(json.dumps(out), flush=True)
     dec.close()

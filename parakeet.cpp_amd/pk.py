@@ -272,8 +272,11 @@ class Decoder:
         return out
 
     def decode_device(self, enc_ptr: int, enc_row, n_frames, slots, max_symbols: int,
-                      out_ptrs: dict, token_cap: int, blank_bias=None, trace_cap: int = 0):
-        """Device-memory batch (inputs resident in HBM): pointers are device addresses."""
+                      out_ptrs: dict, token_cap: int, blank_bias=None, trace_cap: int = 0,
+                      tokens_base=None):
+        """Device-memory batch (inputs resident in HBM): pointers are device
+        addresses; the descriptor arrays (enc_row, n_frames, slots, blank_bias,
+        tokens_base) are host arrays."""
         n = len(n_frames)
         rows = np.ascontiguousarray(enc_row, np.int64)
         T = np.ascontiguousarray(n_frames, np.int32)
@@ -282,7 +285,8 @@ class Decoder:
         b = PkBatch()
         b.n_utts, b.mem, b.d_enc, b.max_symbols = n, MEM_DEVICE, self.info.D, max_symbols
         b.enc, b.enc_row, b.n_frames, b.slot = C.c_void_p(enc_ptr), _ptr(rows), _ptr(T), _ptr(sl)
-        b.blank_bias = _ptr(bb)
+        tb = None if tokens_base is None else np.ascontiguousarray(tokens_base, np.int32)
+        b.blank_bias, b.tokens_base = _ptr(bb), _ptr(tb)
         b.tokens, b.token_cap = C.c_void_p(out_ptrs["tokens"]), token_cap
         b.n_tokens, b.steps = C.c_void_p(out_ptrs["n_tokens"]), C.c_void_p(out_ptrs["steps"])
         b.segments = C.c_void_p(out_ptrs["segments"]) if out_ptrs.get("segments") else None
