@@ -165,6 +165,32 @@ int eou_decode_batch(const ParakeetCtcModel &model, const EouRuntimeWeights &W, 
                      const std::vector<EouDecodeState *> &states, std::vector<std::vector<int32_t>> &out_tokens,
                      std::vector<std::vector<EouSegmentBoundary>> &out_segments, std::vector<int> &out_steps);
 
+// ---- Encoder -> decoder handoff on the device ----
+//
+// The reference copies the encoder output to the host (EncoderOutputs::encoder_out,
+// src/parakeet_ctc.cpp:1660-1667) and decodes from there.  An encoder whose
+// output stays in device memory hands it over in place instead: the enc_proj
+// kernel reads the rows directly, with no host copy and no upload.  Utterance
+// u's window is rows row_offset[u] .. row_offset[u] + n_frames[u] (variable
+// lengths, in any order).  The rows must be complete before the call: the
+// decoder runs on its own stream, so the caller synchronises the stream that
+// produced them.  Return codes as the host-frame calls, plus 3 for windows
+// outside the output.
+struct DeviceEncoderOutput {
+    const float *data = nullptr;   // device address of [n_rows][d_model] f32, 16-byte aligned
+    int64_t n_rows = 0;
+    int d_model = 0;
+};
+int tdt_decode_batch_device(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const DeviceEncoderOutput &enc,
+                            const std::vector<int64_t> &row_offset, const std::vector<int> &n_frames,
+                            const TdtDecodeOptions &opts, const std::vector<TdtDecodeState *> &states,
+                            std::vector<std::vector<int32_t>> &out_tokens, std::vector<int> &out_steps);
+int eou_decode_batch_device(const ParakeetCtcModel &model, const EouRuntimeWeights &W, const DeviceEncoderOutput &enc,
+                            const std::vector<int64_t> &row_offset, const std::vector<int> &n_frames,
+                            const EouDecodeOptions &opts, const std::vector<EouDecodeState *> &states,
+                            std::vector<std::vector<int32_t>> &out_tokens,
+                            std::vector<std::vector<EouSegmentBoundary>> &out_segments, std::vector<int> &out_steps);
+
 // src/sentencepiece_bpe.cpp:9-38: pieces joined (blank/bos/eos/pad skipped), U+2581 -> ' ',
 // leading spaces trimmed.
 std::string detokenize(const BpeVocab &vocab, const std::vector<int32_t> &ids);
@@ -278,6 +304,10 @@ public:
     EngineResult transcribe_features(const float *encoder_out, int T_enc, int D_enc);
     std::vector<EngineResult> transcribe_features_batch(const std::vector<const float *> &encoder_out,
                                                         const std::vector<int> &T_enc, int D_enc);
+    // The same over an encoder output resident in device memory (see DeviceEncoderOutput).
+    std::vector<EngineResult> transcribe_device_batch(const DeviceEncoderOutput &encoder_out,
+                                                      const std::vector<int64_t> &row_offset,
+                                                      const std::vector<int> &T_enc);
     // The decode half of Engine::transcribe_samples_stream (src/parakeet_engine.cpp:389-489):
     // the encoder output in windows of opts.chunk_frames frames, one segment per window.
     EngineResult transcribe_features_stream(const float *encoder_out, int T_enc, int D_enc,

@@ -47,7 +47,15 @@ extern "C" {
 
 enum { PK_KIND_TDT = 0, PK_KIND_EOU = 1 };
 enum { PK_TYPE_F32 = 0, PK_TYPE_F16 = 1, PK_TYPE_Q8_0 = 8 };   /* ggml type ids */
-enum { PK_MEM_HOST = 0, PK_MEM_DEVICE = 1 };
+/* pk_batch.mem: where the frames and the outputs live.
+ *   PK_MEM_HOST           frames and outputs in host memory (frames uploaded per call)
+ *   PK_MEM_DEVICE         frames and outputs in device memory
+ *   PK_MEM_DEVICE_FRAMES  frames in device memory, read in place (an encoder output
+ *                         that stays on the device, instead of the host copy of
+ *                         src/parakeet_ctc.cpp:1660-1667); outputs in host memory
+ * Device frames must be complete before the call: the decoder runs on its own
+ * stream, so the caller synchronises the stream that produced them. */
+enum { PK_MEM_HOST = 0, PK_MEM_DEVICE = 1, PK_MEM_DEVICE_FRAMES = 2 };
 
 enum {
     PK_OK = 0,
@@ -97,9 +105,9 @@ typedef struct pk_decoder pk_decoder;
 
 /* One batched decode call: utterance u decodes frames
  * enc[enc_row[u] .. enc_row[u] + n_frames[u]) with the state in slot[u].
- * Descriptor arrays (enc_row .. tokens_base) are host arrays.  When
- * mem == PK_MEM_DEVICE, enc and every output array are device pointers,
- * otherwise host pointers. */
+ * Descriptor arrays (enc_row .. tokens_base) are host arrays.  enc is a
+ * device pointer for PK_MEM_DEVICE and PK_MEM_DEVICE_FRAMES; the output
+ * arrays are device pointers for PK_MEM_DEVICE only. */
 typedef struct pk_batch {
     int32_t n_utts;
     int32_t mem;

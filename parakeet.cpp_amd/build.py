@@ -59,20 +59,22 @@ def build_decoder():
     return out
 
 
-def build_api_test(name="decoder_api_main"):
-    """tests/cpp/<name>: drivers of the C++ API for the tests (not part of the library)."""
+def build_api_test(name="decoder_api_main", hip=False):
+    """tests/cpp/<name>: drivers of the C++ API for the tests (not part of the library).
+    hip: the driver calls the HIP runtime itself (device-resident frames), so hipcc builds it."""
     src = os.path.join(ROOT, "tests", "cpp", name + ".cpp")
     if not os.path.exists(src) or not os.path.exists(os.path.join(HERE, "libparakeet_decoder.so")):
         return None
     out = os.path.join(ROOT, "tests", "cpp", name)
-    _run(["g++", "-O2", "-std=c++17", "-Wall", f"-I{INC}", src, f"-L{HERE}", "-lparakeet_decoder", "-lparakeet_hip",
+    cc = [HIPCC, *HIP_FLAGS] if hip else ["g++", "-O2", "-std=c++17", "-Wall", f"-I{INC}"]
+    _run([*cc, src, f"-L{HERE}", "-lparakeet_decoder", "-lparakeet_hip",
           "-Wl,-rpath,$ORIGIN/../../parakeet.cpp_amd", "-o", out + ".tmp"])
     os.replace(out + ".tmp", out)
     return out
 
 
 def build_all():
-    return [build_hip(), build_decoder(), build_calib(), build_api_test("decoder_api_main"),
+    return [build_hip(), build_decoder(), build_calib(), build_api_test("decoder_api_main", hip=True),
             build_api_test("loader_main")]
 
 

@@ -124,12 +124,32 @@ std::shared_ptr<detail::SlotLease> lease(const std::shared_ptr<detail::SlotPool>
     return l;
 }
 
+// Encoder frames of a batch: one host window per utterance (packed into one
+// upload per call), or rows of an encoder output resident in device memory,
+// read in place by the enc_proj kernel.
+struct Frames {
+    bool device = false;
+    std::vector<const float *> host;   // host window of each utterance
+    const float *dev = nullptr;        // device encoder output
+    std::vector<int64_t> dev_row;      // first row of each utterance in it
+    Frames pick(const std::vector<int> &idx, size_t i, size_t j) const {
+        Frames f;
+        f.device = device;
+        f.dev = dev;
+        for (size_t k = i; k < j; ++k) {
+            if (device) f.dev_row.push_back(dev_row[idx[k]]);
+            else f.host.push_back(host[idx[k]]);
+        }
+        return f;
+    }
+};
+
 // One batched device call; fills per-utterance tokens/steps (+ EOU segments).
-int run_batch(detail::SlotPool &pool, int D_enc, int max_symbols, const std::vector<const float *> &enc,
-              const std::vector<int> &n_frames, const std::vector<int> &slots, const std::vector<int> &tokens_base,
+int run_batch(detail::SlotPool &pool, int D_enc, int max_symbols, const Frames &fr, const std::vector<int> &n_frames,
+              const std::vector<int> &slots, const std::vector<int> &tokens_base,
               std::vector<std::vector<int32_t>> &tokens, std::vector<std::vector<int32_t>> *segments,
               std::vector<int> &steps) {
-    const int n = (int)enc.size();
+    const int n = (int)n_frames.size();
     int64_t rows = 0;
     int max_T = 0;
     std::vector<int64_t> row(n);
@@ -138,20 +158,25 @@ int run_batch(detail::SlotPool &pool, int D_enc, int max_symbols, const std::vec
         rows += std::max(0, n_frames[u]);
         max_T = std::max(max_T, n_frames[u]);
     }
-    std::vector<float> packed((size_t)std::max<int64_t>(rows, 1) * D_enc);
-    for (int u = 0; u < n; ++u)
-        if (n_frames[u] > 0)
-            memcpy(packed.data() + (size_t)row[u] * D_enc, enc[u], sizeof(float) * (size_t)n_frames[u] * D_enc);
+    std::vector<float> packed;
+    if (fr.device) {
+        row = fr.dev_row;
+    } else {
+        packed.resize((size_t)std::max<int64_t>(rows, 1) * D_enc);
+        for (int u = 0; u < n; ++u)
+            if (n_frames[u] > 0)
+                memcpy(packed.data() + (size_t)row[u] * D_enc, fr.host[u], sizeof(float) * (size_t)n_frames[u] * D_enc);
+    }
     const int cap = max_T * std::max(1, max_symbols) + 1;
     std::vector<int32_t> tok((size_t)n * cap), ntok(n), st(n), seg((size_t)n * (cap + 1)), nseg(n);
     std::vector<int32_t> T(n_frames.begin(), n_frames.end()), sl(slots.begin(), slots.end());
     std::vector<int32_t> base(tokens_base.begin(), tokens_base.end());
     pk_batch b{};
     b.n_utts = n;
-    b.mem = PK_MEM_HOST;
+    b.mem = fr.device ? PK_MEM_DEVICE_FRAMES : PK_MEM_HOST;
     b.d_enc = D_enc;
     b.max_symbols = max_symbols;
-    b.enc = packed.data();
+    b.enc = fr.device ? fr.dev : packed.data();
     b.enc_row = row.data();
     b.n_frames = T.data();
     b.slot = sl.data();
@@ -176,6 +201,30 @@ int run_batch(detail::SlotPool &pool, int D_enc, int max_symbols, const std::vec
         if (segments)
             (*segments)[u].assign(seg.begin() + (size_t)u * (cap + 1), seg.begin() + (size_t)u * (cap + 1) + nseg[u]);
     }
+    return 0;
+}
+
+// Frames of a device-resident encoder output, checked against its extent.
+// Returns 0, 1 (d_model mismatch, the reference's rc) or 3 (bad rows).
+int device_frames(const DeviceEncoderOutput &enc, const std::vector<int64_t> &row_offset,
+                  const std::vector<int> &n_frames, int D_expected, const char *who, Frames &fr) {
+    if (enc.d_model != D_expected) {
+        std::fprintf(stderr, "%s: encoder d_model mismatch (%d vs %d)\n", who, enc.d_model, D_expected);
+        return 1;
+    }
+    if (row_offset.size() != n_frames.size()) return 3;
+    for (size_t u = 0; u < n_frames.size(); ++u) {
+        if (n_frames[u] <= 0) continue;
+        if (!enc.data || row_offset[u] < 0 || row_offset[u] + n_frames[u] > enc.n_rows) {
+            std::fprintf(stderr, "%s: utterance %zu rows [%lld, %lld) outside the encoder output (%lld rows)\n", who,
+                         u, (long long)row_offset[u], (long long)(row_offset[u] + n_frames[u]),
+                         (long long)enc.n_rows);
+            return 3;
+        }
+    }
+    fr.device = true;
+    fr.dev = enc.data;
+    fr.dev_row = row_offset;
     return 0;
 }
 
@@ -311,35 +360,27 @@ void tdt_init_state(TdtRuntimeWeights &W, int, TdtDecodeState &state) {
     state.initialized = true;
 }
 
-int tdt_decode_batch(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const std::vector<const float *> &enc,
-                     const std::vector<int> &n_frames, int D_enc, const TdtDecodeOptions &opts,
-                     const std::vector<TdtDecodeState *> &states, std::vector<std::vector<int32_t>> &out_tokens,
-                     std::vector<int> &out_steps) {
-    const int n = (int)enc.size();
-    out_steps.assign(n, 0);
-    out_tokens.assign(n, {});
-    if (D_enc != W.D_enc) {
-        std::fprintf(stderr, "tdt_decode_window: encoder d_model mismatch (%d vs %d)\n", D_enc, W.D_enc);
-        return 1;
-    }
-    if ((int)n_frames.size() != n || (int)states.size() != n) return 3;
+namespace {
+
+int tdt_batch(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const Frames &fr, const std::vector<int> &n_frames,
+              int D_enc, const TdtDecodeOptions &opts, const std::vector<TdtDecodeState *> &states,
+              std::vector<std::vector<int32_t>> &out_tokens, std::vector<int> &out_steps) {
+    const int n = (int)n_frames.size();
     std::vector<int> idx, slots, T;
-    std::vector<const float *> e;
     for (int u = 0; u < n; ++u) {
         if (n_frames[u] <= 0) continue;   // src/parakeet_tdt.cpp:879
         if (!states[u]->initialized) tdt_init_state(W, model.blank_id, *states[u]);
         idx.push_back(u);
         slots.push_back(states[u]->slot->slot);
         T.push_back(n_frames[u]);
-        e.push_back(enc[u]);
     }
     for (size_t i = 0; i < idx.size(); i += PK_MAX_BATCH) {
         const size_t j = std::min(idx.size(), i + PK_MAX_BATCH);
-        std::vector<const float *> ee(e.begin() + i, e.begin() + j);
         std::vector<int> tt(T.begin() + i, T.begin() + j), ss(slots.begin() + i, slots.begin() + j);
         std::vector<std::vector<int32_t>> toks;
         std::vector<int> steps;
-        if (int rc = run_batch(*W.pool, D_enc, opts.max_symbols_per_step, ee, tt, ss, {}, toks, nullptr, steps))
+        if (int rc = run_batch(*W.pool, D_enc, opts.max_symbols_per_step, fr.pick(idx, i, j), tt, ss, {}, toks,
+                               nullptr, steps))
             return rc;
         for (size_t k = i; k < j; ++k) {
             const int u = idx[k];
@@ -352,6 +393,38 @@ int tdt_decode_batch(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const 
         }
     }
     return 0;
+}
+
+}  // namespace
+
+int tdt_decode_batch(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const std::vector<const float *> &enc,
+                     const std::vector<int> &n_frames, int D_enc, const TdtDecodeOptions &opts,
+                     const std::vector<TdtDecodeState *> &states, std::vector<std::vector<int32_t>> &out_tokens,
+                     std::vector<int> &out_steps) {
+    const int n = (int)enc.size();
+    out_steps.assign(n, 0);
+    out_tokens.assign(n, {});
+    if (D_enc != W.D_enc) {
+        std::fprintf(stderr, "tdt_decode_window: encoder d_model mismatch (%d vs %d)\n", D_enc, W.D_enc);
+        return 1;
+    }
+    if ((int)n_frames.size() != n || (int)states.size() != n) return 3;
+    Frames fr;
+    fr.host = enc;
+    return tdt_batch(model, W, fr, n_frames, D_enc, opts, states, out_tokens, out_steps);
+}
+
+int tdt_decode_batch_device(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const DeviceEncoderOutput &enc,
+                            const std::vector<int64_t> &row_offset, const std::vector<int> &n_frames,
+                            const TdtDecodeOptions &opts, const std::vector<TdtDecodeState *> &states,
+                            std::vector<std::vector<int32_t>> &out_tokens, std::vector<int> &out_steps) {
+    const int n = (int)n_frames.size();
+    out_steps.assign(n, 0);
+    out_tokens.assign(n, {});
+    if ((int)states.size() != n) return 3;
+    Frames fr;
+    if (int rc = device_frames(enc, row_offset, n_frames, W.D_enc, "tdt_decode_batch_device", fr)) return rc;
+    return tdt_batch(model, W, fr, n_frames, W.D_enc, opts, states, out_tokens, out_steps);
 }
 
 int tdt_decode_window(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const float *encoder_out_window,
@@ -409,32 +482,27 @@ void eou_init_state(const EouRuntimeWeights &W, EouDecodeState &state) {
     state.initialized = true;
 }
 
-int eou_decode_batch(const ParakeetCtcModel &, const EouRuntimeWeights &W, const std::vector<const float *> &enc,
-                     const std::vector<int> &n_frames, int D_enc, const EouDecodeOptions &opts,
-                     const std::vector<EouDecodeState *> &states, std::vector<std::vector<int32_t>> &out_tokens,
-                     std::vector<std::vector<EouSegmentBoundary>> &out_segments, std::vector<int> &out_steps) {
-    const int n = (int)enc.size();
-    out_tokens.assign(n, {});
-    out_segments.assign(n, {});
-    out_steps.assign(n, 0);
-    if (D_enc != W.D_enc) {
-        std::fprintf(stderr, "eou_decode_window: encoder d_model mismatch (%d vs %d)\n", D_enc, W.D_enc);
-        return 1;
-    }
-    if ((int)n_frames.size() != n || (int)states.size() != n) return 3;
-    std::vector<int> slots(n), base(n, 0);
+namespace {
+
+int eou_batch(const EouRuntimeWeights &W, const Frames &fr, const std::vector<int> &n_frames, int D_enc,
+              const EouDecodeOptions &opts, const std::vector<EouDecodeState *> &states,
+              std::vector<std::vector<int32_t>> &out_tokens, std::vector<std::vector<EouSegmentBoundary>> &out_segments,
+              std::vector<int> &out_steps) {
+    const int n = (int)n_frames.size();
+    std::vector<int> idx(n), slots(n), base(n, 0);
     for (int u = 0; u < n; ++u) {
         if (!states[u]->initialized) eou_init_state(W, *states[u]);
+        idx[u] = u;
         slots[u] = states[u]->slot->slot;
     }
     for (int i = 0; i < n; i += PK_MAX_BATCH) {
         const int j = std::min(n, i + PK_MAX_BATCH);
-        std::vector<const float *> ee(enc.begin() + i, enc.begin() + j);
         std::vector<int> tt(n_frames.begin() + i, n_frames.begin() + j), ss(slots.begin() + i, slots.begin() + j);
         std::vector<int> bb(base.begin() + i, base.begin() + j);
         std::vector<std::vector<int32_t>> toks, segs;
         std::vector<int> steps;
-        if (int rc = run_batch(*W.pool, D_enc, opts.max_symbols_per_step, ee, tt, ss, bb, toks, &segs, steps))
+        if (int rc = run_batch(*W.pool, D_enc, opts.max_symbols_per_step, fr.pick(idx, i, j), tt, ss, bb, toks, &segs,
+                               steps))
             return rc;
         for (int u = i; u < j; ++u) {
             out_tokens[u] = std::move(toks[u - i]);
@@ -448,6 +516,41 @@ int eou_decode_batch(const ParakeetCtcModel &, const EouRuntimeWeights &W, const
         }
     }
     return 0;
+}
+
+}  // namespace
+
+int eou_decode_batch(const ParakeetCtcModel &, const EouRuntimeWeights &W, const std::vector<const float *> &enc,
+                     const std::vector<int> &n_frames, int D_enc, const EouDecodeOptions &opts,
+                     const std::vector<EouDecodeState *> &states, std::vector<std::vector<int32_t>> &out_tokens,
+                     std::vector<std::vector<EouSegmentBoundary>> &out_segments, std::vector<int> &out_steps) {
+    const int n = (int)enc.size();
+    out_tokens.assign(n, {});
+    out_segments.assign(n, {});
+    out_steps.assign(n, 0);
+    if (D_enc != W.D_enc) {
+        std::fprintf(stderr, "eou_decode_window: encoder d_model mismatch (%d vs %d)\n", D_enc, W.D_enc);
+        return 1;
+    }
+    if ((int)n_frames.size() != n || (int)states.size() != n) return 3;
+    Frames fr;
+    fr.host = enc;
+    return eou_batch(W, fr, n_frames, D_enc, opts, states, out_tokens, out_segments, out_steps);
+}
+
+int eou_decode_batch_device(const ParakeetCtcModel &, const EouRuntimeWeights &W, const DeviceEncoderOutput &enc,
+                            const std::vector<int64_t> &row_offset, const std::vector<int> &n_frames,
+                            const EouDecodeOptions &opts, const std::vector<EouDecodeState *> &states,
+                            std::vector<std::vector<int32_t>> &out_tokens,
+                            std::vector<std::vector<EouSegmentBoundary>> &out_segments, std::vector<int> &out_steps) {
+    const int n = (int)n_frames.size();
+    out_tokens.assign(n, {});
+    out_segments.assign(n, {});
+    out_steps.assign(n, 0);
+    if ((int)states.size() != n) return 3;
+    Frames fr;
+    if (int rc = device_frames(enc, row_offset, n_frames, W.D_enc, "eou_decode_batch_device", fr)) return rc;
+    return eou_batch(W, fr, n_frames, W.D_enc, opts, states, out_tokens, out_segments, out_steps);
 }
 
 int eou_decode_window(const ParakeetCtcModel &model, const EouRuntimeWeights &W, const float *encoder_out_window,
@@ -466,8 +569,10 @@ int eou_decode_window(const ParakeetCtcModel &model, const EouRuntimeWeights &W,
     std::vector<int32_t> toks;
     std::vector<int> steps;
     std::vector<std::vector<int32_t>> tv, sv;
-    if (int rc = run_batch(*W.pool, D_enc, opts.max_symbols_per_step, {encoder_out_window}, {n},
-                           {state.slot->slot}, {base}, tv, &sv, steps))
+    Frames fr;
+    fr.host = {encoder_out_window};
+    if (int rc = run_batch(*W.pool, D_enc, opts.max_symbols_per_step, fr, {n}, {state.slot->slot}, {base}, tv, &sv,
+                           steps))
         return rc;
     out_steps = steps[0];
     out_tokens.insert(out_tokens.end(), tv[0].begin(), tv[0].end());
@@ -552,20 +657,23 @@ EngineResult Engine::transcribe_features(const float *enc, int T_enc, int D_enc)
     return transcribe_features_batch({enc}, {T_enc}, D_enc)[0];
 }
 
-std::vector<EngineResult> Engine::transcribe_features_batch(const std::vector<const float *> &enc,
-                                                            const std::vector<int> &T_enc, int D_enc) {
+namespace {
+
+// The Engine's batch decode over either frame source: fresh states, one result per utterance.
+std::vector<EngineResult> engine_decode(Engine::Impl &E, const Frames &fr, const std::vector<int> &T_enc, int D_enc) {
     const auto t0 = std::chrono::steady_clock::now();
-    const int n = (int)enc.size();
+    const int n = (int)T_enc.size();
     std::vector<EngineResult> out(n);
-    const ParakeetCtcModel &m = pimpl_->model;
+    const ParakeetCtcModel &m = E.model;
     if (m.model_type == ParakeetModelType::TDT) {
         std::vector<TdtDecodeState> states(n);
         std::vector<TdtDecodeState *> sp(n);
         for (int u = 0; u < n; ++u) sp[u] = &states[u];
-        std::vector<std::vector<int32_t>> toks;
-        std::vector<int> steps;
-        if (int rc = tdt_decode_batch(m, pimpl_->tdt, enc, T_enc, D_enc, TdtDecodeOptions{}, sp, toks, steps))
-            throw std::runtime_error("parakeet::Engine: tdt decode failed (rc=" + std::to_string(rc) + ")");
+        std::vector<std::vector<int32_t>> toks(n);
+        std::vector<int> steps(n, 0);
+        int rc = D_enc != E.tdt.D_enc ? 1 : 0;
+        if (rc == 0) rc = tdt_batch(m, E.tdt, fr, T_enc, D_enc, TdtDecodeOptions{}, sp, toks, steps);
+        if (rc) throw std::runtime_error("parakeet::Engine: tdt decode failed (rc=" + std::to_string(rc) + ")");
         for (int u = 0; u < n; ++u) {
             out[u].token_ids = std::move(toks[u]);
             out[u].text = detokenize(m.vocab, out[u].token_ids);
@@ -577,11 +685,12 @@ std::vector<EngineResult> Engine::transcribe_features_batch(const std::vector<co
         std::vector<EouDecodeState> states(n);
         std::vector<EouDecodeState *> sp(n);
         for (int u = 0; u < n; ++u) sp[u] = &states[u];
-        std::vector<std::vector<int32_t>> toks;
-        std::vector<std::vector<EouSegmentBoundary>> segs;
-        std::vector<int> steps;
-        if (int rc = eou_decode_batch(m, pimpl_->eou, enc, T_enc, D_enc, o, sp, toks, segs, steps))
-            throw std::runtime_error("parakeet::Engine: eou decode failed (rc=" + std::to_string(rc) + ")");
+        std::vector<std::vector<int32_t>> toks(n);
+        std::vector<std::vector<EouSegmentBoundary>> segs(n);
+        std::vector<int> steps(n, 0);
+        int rc = D_enc != E.eou.D_enc ? 1 : 0;
+        if (rc == 0) rc = eou_batch(E.eou, fr, T_enc, D_enc, o, sp, toks, segs, steps);
+        if (rc) throw std::runtime_error("parakeet::Engine: eou decode failed (rc=" + std::to_string(rc) + ")");
         for (int u = 0; u < n; ++u) {
             out[u].token_ids = std::move(toks[u]);
             out[u].steps = steps[u];
@@ -606,6 +715,28 @@ std::vector<EngineResult> Engine::transcribe_features_batch(const std::vector<co
         out[u].encoder_frames = T_enc[u];
     }
     return out;
+}
+
+}  // namespace
+
+std::vector<EngineResult> Engine::transcribe_features_batch(const std::vector<const float *> &enc,
+                                                            const std::vector<int> &T_enc, int D_enc) {
+    if (enc.size() != T_enc.size())
+        throw std::invalid_argument("parakeet::Engine::transcribe_features_batch: size mismatch");
+    Frames fr;
+    fr.host = enc;
+    return engine_decode(*pimpl_, fr, T_enc, D_enc);
+}
+
+std::vector<EngineResult> Engine::transcribe_device_batch(const DeviceEncoderOutput &enc,
+                                                          const std::vector<int64_t> &row_offset,
+                                                          const std::vector<int> &T_enc) {
+    const ParakeetCtcModel &m = pimpl_->model;
+    const int D = m.model_type == ParakeetModelType::TDT ? pimpl_->tdt.D_enc : pimpl_->eou.D_enc;
+    Frames fr;
+    if (int rc = device_frames(enc, row_offset, T_enc, D, "parakeet::Engine::transcribe_device_batch", fr))
+        throw std::runtime_error("parakeet::Engine: device frames rejected (rc=" + std::to_string(rc) + ")");
+    return engine_decode(*pimpl_, fr, T_enc, D);
 }
 
 // ------------------------------------------------------------------ streaming over features

@@ -691,7 +691,8 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     if (n == 0) return 0;
     if (!bt->enc_row || !bt->n_frames || !bt->slot || !bt->n_tokens || !bt->steps || !bt->tokens)
         return fail(PK_ERR_ARG, "pk_decode: missing batch array");
-    if (bt->mem != PK_MEM_HOST && bt->mem != PK_MEM_DEVICE) return fail(PK_ERR_ARG, "bad mem kind");
+    if (bt->mem != PK_MEM_HOST && bt->mem != PK_MEM_DEVICE && bt->mem != PK_MEM_DEVICE_FRAMES)
+        return fail(PK_ERR_ARG, "bad mem kind");
     HIP_TRY(hipSetDevice(dec->device));
     std::vector<char> seen(dec->n_slots, 0);
     for (int u = 0; u < n; ++u) {
@@ -705,7 +706,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     for (int u = 0; u < n; ++u)
         if (keep_empty || p.kind == PK_KIND_EOU || bt->n_frames[u] > 0) map.push_back(u);
     const int m = (int)map.size();
-    const bool host = bt->mem == PK_MEM_HOST;
+    const bool enc_host = bt->mem == PK_MEM_HOST, host = bt->mem != PK_MEM_DEVICE;   // host: outputs
     if (!host && m != n) return fail(PK_ERR_ARG, "device-memory batches must not contain empty TDT windows");
     if (host)
         for (int u = 0; u < n; ++u) {   // outputs of utterances that do not run
@@ -739,7 +740,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     int rc;
     // encoder frames: device pointer as given, or packed host rows uploaded
     const float *enc = bt->enc;
-    if (host && rows > 0) {
+    if (enc_host && rows > 0) {
         if ((rc = dec->d_enc.ensure((size_t)rows * D * 4))) return rc;
         // one copy per run of utterances whose source rows follow each other
         // (one copy in all when the caller packs them in order); the device
@@ -761,6 +762,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         enc = dec->d_enc.as<float>();
         src_row = dst_row;
     }
+    if (rows > 0 && !enc) return fail(PK_ERR_ARG, "pk_decode: missing encoder frames");
     if (rows > 0 && reinterpret_cast<uintptr_t>(enc) % 16 != 0)
         return fail(PK_ERR_ARG, "encoder frames must be 16-byte aligned");
     const Plan pl = plan_domains(m, dec->nwg, T);

@@ -8,7 +8,10 @@
 //   - Engine::transcribe_features on the first TDT utterance;
 //   - Engine::transcribe_features_stream (Mode 2) on the first TDT utterance, and
 //     EOU FeatureStreamSessions (Mode 3) fed chunk by chunk: all sessions in one
-//     launch per chunk, and one session per launch.
+//     launch per chunk, and one session per launch;
+//   - the encoder output resident in device memory: tdt/eou_decode_batch_device
+//     and Engine::transcribe_device_batch on ragged windows, beside the same
+//     windows decoded from host memory, plus their argument checks.
 // Usage: decoder_api_main TDT.gguf TDT_FRAMES EOU.gguf EOU_FRAMES WINDOW
 // Frame files: int32 n, T, D, then n*T*D float32 (utterance-major).
 #include <cstdio>
@@ -17,6 +20,8 @@
 #include <memory>
 #include <string>
 #include <vector>
+
+#include <hip/hip_runtime_api.h>
 
 #include "parakeet_decoder.h"
 
@@ -92,6 +97,153 @@ int fail(const char *what, int rc) {
 }
 
 }  // namespace
+
+// Ragged windows over utterance-major frames: utterance u decodes rows
+// u*T .. u*T + len(u) (len(u) = T, 7T/8, 3T/4, 5T/8, ...).
+int window_len(const Frames &f, int u) { return std::max(1, f.T - (u % 4) * (f.T / 8)); }
+
+// Frames uploaded to device memory, freed with the object.
+struct DeviceCopy {
+    float *p = nullptr;
+    bool ok = false;
+    explicit DeviceCopy(const Frames &f) {
+        const size_t bytes = f.data.size() * sizeof(float);
+        ok = hipMalloc(reinterpret_cast<void **>(&p), bytes) == hipSuccess &&
+             hipMemcpy(p, f.data.data(), bytes, hipMemcpyHostToDevice) == hipSuccess &&
+             hipDeviceSynchronize() == hipSuccess;
+    }
+    ~DeviceCopy() { if (p) (void)hipFree(p); }
+};
+
+void int_lists(const std::vector<std::vector<int32_t>> &v) {
+    printf("[");
+    for (size_t u = 0; u < v.size(); ++u) {
+        if (u) printf(",");
+        ints(v[u]);
+    }
+    printf("]");
+}
+
+int device_section(const char *tdt_path, const char *eou_path, const Frames &ft, const Frames &fe) {
+    using namespace parakeet;
+    int rc;
+    DeviceCopy dt(ft), de(fe);
+    if (!dt.ok || !de.ok) return fail("device copy of the frames", -1);
+    // TDT: host windows and device rows, fresh states each
+    ParakeetCtcModel tdt;
+    if ((rc = load_from_gguf(tdt_path, tdt)) != 0) return fail("load_from_gguf(tdt)", rc);
+    TdtRuntimeWeights tw;
+    if ((rc = tdt_prepare_runtime(tdt, tw, 2 * ft.n + 4)) != 0) return fail("tdt_prepare_runtime", rc);
+    const DeviceEncoderOutput dout{dt.p, (int64_t)ft.n * ft.T, ft.D};
+    std::vector<const float *> hp;
+    std::vector<int64_t> rows;
+    std::vector<int> nf;
+    for (int u = 0; u < ft.n; ++u) {
+        hp.push_back(ft.utt(u));
+        rows.push_back((int64_t)u * ft.T);
+        nf.push_back(window_len(ft, u));
+    }
+    std::vector<std::vector<int32_t>> th, td;
+    std::vector<int> sh, sd;
+    {
+        std::vector<TdtDecodeState> a(ft.n), b(ft.n);
+        std::vector<TdtDecodeState *> pa, pb;
+        for (int u = 0; u < ft.n; ++u) {
+            pa.push_back(&a[u]);
+            pb.push_back(&b[u]);
+        }
+        if ((rc = tdt_decode_batch(tdt, tw, hp, nf, ft.D, TdtDecodeOptions{}, pa, th, sh)) != 0)
+            return fail("tdt_decode_batch", rc);
+        if ((rc = tdt_decode_batch_device(tdt, tw, dout, rows, nf, TdtDecodeOptions{}, pb, td, sd)) != 0)
+            return fail("tdt_decode_batch_device", rc);
+    }
+    printf("{\"tdt_host\":");
+    int_lists(th);
+    printf(",\"tdt_dev\":");
+    int_lists(td);
+    printf(",\"tdt_steps_host\":");
+    ints(std::vector<int32_t>(sh.begin(), sh.end()));
+    printf(",\"tdt_steps_dev\":");
+    ints(std::vector<int32_t>(sd.begin(), sd.end()));
+    {   // argument checks: a window past the end of the output, a d_model mismatch
+        TdtDecodeState st;
+        std::vector<std::vector<int32_t>> t;
+        std::vector<int> s;
+        const int rc_range = tdt_decode_batch_device(tdt, tw, dout, {(int64_t)ft.n * ft.T - 1}, {2}, TdtDecodeOptions{},
+                                                     {&st}, t, s);
+        DeviceEncoderOutput bad = dout;
+        bad.d_model = ft.D + 1;
+        const int rc_dim = tdt_decode_batch_device(tdt, tw, bad, {0}, {1}, TdtDecodeOptions{}, {&st}, t, s);
+        printf(",\"rc_range\":%d,\"rc_dim\":%d", rc_range, rc_dim);
+    }
+    // EOU: the same with segment boundaries
+    ParakeetCtcModel eou;
+    if ((rc = load_from_gguf(eou_path, eou)) != 0) return fail("load_from_gguf(eou)", rc);
+    EouRuntimeWeights ew;
+    if ((rc = eou_prepare_runtime(eou, ew, 2 * fe.n + 4)) != 0) return fail("eou_prepare_runtime", rc);
+    EouDecodeOptions eopt;
+    eopt.max_symbols_per_step = eou.encoder_cfg.eou_max_symbols_per_step;
+    const DeviceEncoderOutput eout{de.p, (int64_t)fe.n * fe.T, fe.D};
+    std::vector<const float *> ehp;
+    std::vector<int64_t> erows;
+    std::vector<int> enf;
+    for (int u = 0; u < fe.n; ++u) {
+        ehp.push_back(fe.utt(u));
+        erows.push_back((int64_t)u * fe.T);
+        enf.push_back(window_len(fe, u));
+    }
+    std::vector<std::vector<int32_t>> eh, ed;
+    std::vector<std::vector<EouSegmentBoundary>> gh, gd;
+    std::vector<int> esh, esd;
+    {
+        std::vector<EouDecodeState> a(fe.n), b(fe.n);
+        std::vector<EouDecodeState *> pa, pb;
+        for (int u = 0; u < fe.n; ++u) {
+            pa.push_back(&a[u]);
+            pb.push_back(&b[u]);
+        }
+        if ((rc = eou_decode_batch(eou, ew, ehp, enf, fe.D, eopt, pa, eh, gh, esh)) != 0)
+            return fail("eou_decode_batch", rc);
+        if ((rc = eou_decode_batch_device(eou, ew, eout, erows, enf, eopt, pb, ed, gd, esd)) != 0)
+            return fail("eou_decode_batch_device", rc);
+    }
+    auto seg_ints = [](const std::vector<std::vector<EouSegmentBoundary>> &g) {
+        std::vector<std::vector<int32_t>> v(g.size());
+        for (size_t u = 0; u < g.size(); ++u)
+            for (auto &b : g[u]) v[u].push_back(b.token_index);
+        return v;
+    };
+    printf(",\"eou_host\":");
+    int_lists(eh);
+    printf(",\"eou_dev\":");
+    int_lists(ed);
+    printf(",\"eou_seg_host\":");
+    int_lists(seg_ints(gh));
+    printf(",\"eou_seg_dev\":");
+    int_lists(seg_ints(gd));
+    // Engine over the TDT model
+    try {
+        EngineOptions eo;
+        eo.model_gguf_path = tdt_path;
+        eo.n_slots = 2 * ft.n + 4;
+        Engine engine(eo);
+        const std::vector<EngineResult> rh = engine.transcribe_features_batch(hp, nf, ft.D);
+        const std::vector<EngineResult> rd = engine.transcribe_device_batch(dout, rows, nf);
+        std::vector<std::vector<int32_t>> a, b;
+        for (auto &r : rh) a.push_back(r.token_ids);
+        for (auto &r : rd) b.push_back(r.token_ids);
+        printf(",\"engine_host\":");
+        int_lists(a);
+        printf(",\"engine_dev\":");
+        int_lists(b);
+        printf(",\"engine_text_equal\":%d", (int)(rh.size() == rd.size() && !rh.empty() && rh[0].text == rd[0].text));
+    } catch (const std::exception &e) {
+        fprintf(stderr, "Engine (device frames): %s\n", e.what());
+        return 1;
+    }
+    printf("}");
+    return 0;
+}
 
 int main(int argc, char **argv) {
     if (argc != 6) {
@@ -289,6 +441,8 @@ int main(int argc, char **argv) {
         fprintf(stderr, "Engine: %s\n", e.what());
         return 1;
     }
+    printf(",\"device\":");
+    if ((rc = device_section(argv[1], argv[3], ft, fe)) != 0) return rc;
     printf("}\n");
     return 0;
 }

@@ -20,7 +20,12 @@ against the C ABI path that the parity tests pin against the oracle.
   window's decode, whose text is the growth of detokenize(all tokens so far),
   timed by the encoder frame stride 1000 * hop * subsampling / sample_rate
   (:35-41); one EndOfTurn event (confidence 1) per EOU boundary of the chunk;
-  sessions fed in one launch equal sessions fed one at a time."""
+  sessions fed in one launch equal sessions fed one at a time;
+- the encoder output resident in device memory (the handoff that replaces the
+  host copy of src/parakeet_ctc.cpp:1660-1667): ragged windows decoded in place
+  by tdt/eou_decode_batch_device and Engine::transcribe_device_batch equal the
+  same windows decoded from host memory and through the C ABI; a window past
+  the end of the output returns 3 and a d_model mismatch 1."""
 import json
 import os
 import subprocess
@@ -77,8 +82,10 @@ def test_cpp_api_matches_c_abi(tmp_path):
     assert r.returncode == 0, r.stderr
     out = json.loads(r.stdout)
 
-    dt = pk.Decoder.from_gguf(tdt_path, n_slots=4)
+    dt = pk.Decoder.from_gguf(tdt_path, n_slots=6)
     ref_t = dt.decode(encs_t)
+    lens = [max(1, T - (u % 4) * (T // 8)) for u in range(3)]   # the driver's ragged windows
+    rag_t = dt.decode([encs_t[u][:lens[u]] for u in range(3)], slots=[3, 4, 5])   # fresh states
     pieces_t = dt.info.pieces
     blank_t = dt.info.blank
     for u in range(3):
@@ -93,8 +100,9 @@ def test_cpp_api_matches_c_abi(tmp_path):
     assert out["engine"]["steps"] == ref_t[0]["steps"]
     dt.close()
 
-    de = pk.Decoder.from_gguf(eou_path, n_slots=4)
+    de = pk.Decoder.from_gguf(eou_path, n_slots=6)
     ref_e = de.decode(encs_e, max_symbols=5)
+    rag_e = de.decode([encs_e[u][:lens[u]] for u in range(3)], slots=[3, 4, 5], max_symbols=5)
     # the oracle, windows decoded into fresh token vectors with the state carried
     om = oracle.OracleModel.from_gguf(eou_path, G)
     chunks = [[] for _ in range(3)]
@@ -156,5 +164,19 @@ def test_cpp_api_matches_c_abi(tmp_path):
         n_events += len(log["events"])
     assert n_events == sum(len(s) for s in out["eou"]["chunked_segments"])
     assert n_events > 0        # the synthetic EOU model does fire <EOU> on these frames
+
+    dv = out["device"]
+    for u in range(3):
+        want_t, want_e = rag_t[u]["tokens"].tolist(), rag_e[u]["tokens"].tolist()
+        assert dv["tdt_host"][u] == want_t, ("tdt host frames", u)
+        assert dv["tdt_dev"][u] == want_t, ("tdt device frames", u)
+        assert dv["tdt_steps_host"][u] == dv["tdt_steps_dev"][u] == rag_t[u]["steps"], u
+        assert dv["eou_host"][u] == want_e, ("eou host frames", u)
+        assert dv["eou_dev"][u] == want_e, ("eou device frames", u)
+        assert dv["eou_seg_host"][u] == dv["eou_seg_dev"][u] == rag_e[u]["segments"].tolist(), u
+        assert dv["engine_host"][u] == want_t, ("engine host frames", u)
+        assert dv["engine_dev"][u] == want_t, ("engine device frames", u)
+    assert dv["engine_text_equal"] == 1
+    assert dv["rc_range"] == 3 and dv["rc_dim"] == 1
     print("cpp api: tokens", [len(x) for x in out["tdt"]["greedy"]], [len(x) for x in out["eou"]["greedy"]],
           "eou segments", [len(x) for x in out["eou"]["segments"]], "EndOfTurn events", n_events)
