@@ -24,7 +24,7 @@ PK_MAX_LAYERS = 8
 PK_MAX_DURATIONS = 16
 PK_MAX_BATCH = 512
 KIND_TDT, KIND_EOU = 0, 1
-MEM_HOST, MEM_DEVICE = 0, 1
+MEM_HOST, MEM_DEVICE, MEM_DEVICE_FRAMES = 0, 1, 2   # pk_batch.mem (parakeet_hip.h)
 PK_CTRL_N = 8
 CTRL_INIT, CTRL_SYM, CTRL_CARRY, CTRL_LAST, CTRL_SEGSTART, CTRL_CUR = range(6)
 

@@ -1,8 +1,14 @@
 """The C-ABI library loads on a CPU-only host and exports every entry point
-that include/parakeet_hip.h declares (no compute calls without a GPU)."""
+that include/parakeet_hip.h declares (no compute calls without a GPU); the
+Python mirror's constants match the header; the C++ API library defines the
+device-frame handoff entry points."""
 import ctypes
 import os
 import re
+import shutil
+import subprocess
+
+import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
@@ -20,3 +26,30 @@ def test_hip_library_exports_header_symbols(pkg):
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
     assert sorted(pk.EXPORTED) == names
+
+
+def header_enum(header, prefix):
+    """PK_<prefix>_* = value pairs of the header's enums."""
+    text = open(os.path.join(ROOT, "include", header)).read()
+    return {m.group(1): int(m.group(2)) for m in re.finditer(rf"\bPK_({prefix}_\w+)\s*=\s*(\d+)", text)}
+
+
+def test_python_mirror_constants_match_header(pkg):
+    from parakeet_amd import pk
+    for prefix in ("MEM", "KIND"):
+        enum = header_enum("parakeet_hip.h", prefix)
+        assert enum, prefix
+        for name, value in enum.items():
+            assert getattr(pk, name) == value, name
+
+
+def test_decoder_library_exports_device_handoff(pkg):
+    """The C++ API library defines the device-frame entry points the header declares."""
+    lib = os.path.join(ROOT, "parakeet.cpp_amd", "libparakeet_decoder.so")
+    nm = shutil.which("nm")
+    if nm is None or not os.path.exists(lib):
+        pytest.skip("nm or the built library is missing")
+    syms = subprocess.run([nm, "-DC", "--defined-only", lib], capture_output=True, text=True, check=True).stdout
+    for name in ("parakeet::tdt_decode_batch_device(", "parakeet::eou_decode_batch_device(",
+                 "parakeet::Engine::transcribe_device_batch("):
+        assert name in syms, name
