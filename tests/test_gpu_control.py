@@ -266,3 +266,44 @@ def test_host_memory_scattered_rows(tmp_path):
         assert toks[u, :ntok[u]].tolist() == want[u]["tokens"].tolist(), u
         assert steps[u] == want[u]["steps"], u
         assert segs[u, :nseg[u]].tolist() == want[u]["segments"].tolist(), u
+
+
+def test_device_frames_host_outputs(tmp_path):
+    """PK_MEM_DEVICE_FRAMES (an encoder output left in HBM, outputs to host
+    arrays): scattered device rows, reversed order and an empty TDT window
+    (which returns before initialising, src/parakeet_tdt.cpp:879, so its
+    outputs are zero) give the host-memory batch's results; a frame pointer
+    that is not 16-byte aligned is refused before any launch."""
+    import ctypes as C
+    from parakeet_amd import hipmem, pk, synth
+    path = str(tmp_path / "t.gguf")
+    small_tdt(path)
+    dec = pk.Decoder.from_gguf(path, n_slots=12)
+    D = dec.info.D
+    Ts = [9, 0, 14, 6]
+    encs = [synth.encoder_frames(650 + u, T, D) for u, T in enumerate(Ts)]
+    want = dec.decode(encs, slots=list(range(4)))
+    order_rows = {0: 20, 1: 0, 2: 2, 3: 31}
+    frames = np.full((40, D), np.nan, np.float32)     # rows between windows are never read
+    for u, r in order_rows.items():
+        frames[r:r + Ts[u]] = encs[u]
+    enc_d = hipmem.DeviceArray.from_numpy(frames)
+    rows = np.array([order_rows[u] for u in range(4)], np.int64)
+    T = np.array(Ts, np.int32)
+    slots = np.arange(4, 8, dtype=np.int32)
+    cap = max(Ts) * dec.info.max_symbols + 1
+    toks = np.zeros((4, cap), np.int32)
+    ntok, steps = np.full(4, -1, np.int32), np.full(4, -1, np.int32)
+    b = pk.PkBatch()
+    b.n_utts, b.mem, b.d_enc, b.max_symbols = 4, pk.MEM_DEVICE_FRAMES, D, dec.info.max_symbols
+    b.enc, b.enc_row, b.n_frames, b.slot = C.c_void_p(enc_d.ptr), pk._ptr(rows), pk._ptr(T), pk._ptr(slots)
+    b.tokens, b.token_cap, b.n_tokens, b.steps = pk._ptr(toks), cap, pk._ptr(ntok), pk._ptr(steps)
+    pk.check(pk.lib().pk_decode(dec.h, C.byref(b)))
+    for u in range(4):
+        assert toks[u, :ntok[u]].tolist() == want[u]["tokens"].tolist(), u
+        assert steps[u] == want[u]["steps"], u
+    assert ntok[1] == 0 and steps[1] == 0
+    b.enc = C.c_void_p(enc_d.ptr + 4)
+    b.slot = pk._ptr(np.arange(8, 12, dtype=np.int32))
+    assert pk.lib().pk_decode(dec.h, C.byref(b)) == 3      # PK_ERR_ARG
+    assert "aligned" in pk.lib().pk_last_error().decode()
