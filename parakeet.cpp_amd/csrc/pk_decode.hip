@@ -325,8 +325,11 @@ struct Plan {
 Plan plan_domains(int m, int nwg, const std::vector<int32_t> &T) {
     Plan pl;
     int C, nt;
+    // one 16-utterance column tile per domain up to 256 utterances (at 129..256 this beats
+    // 32-utterance domains: each staging moves half the rows and runs once per phase);
+    // beyond that, 16 workgroups per domain is the least that keeps the products short
     if (m <= kTile) { C = 1; nt = 1; }
-    else if (m <= 8 * kTile) { nt = 1; C = 1; while (C * kTile < m) C *= 2; }
+    else if (m <= 16 * kTile) { nt = 1; C = 1; while (C * kTile < m) C *= 2; }
     else { nt = 2; C = 1; while (C * 2 * kTile < m) C *= 2; }
     while (C > 1 && nwg / C < 8) C /= 2;      // at least 8 workgroups per domain
     pl.n_dom = C;
