@@ -169,3 +169,29 @@ def test_cfg5_ragged_blank_bias(tdt06):
     assert by_bias[0.0] <= by_bias[2.0] <= by_bias[4.0], by_bias
     print(f"cfg5: steps={sum(r['steps'] for r in res)} blank fraction by bias {by_bias}")
     dev.close()
+
+
+def test_eou_b200_sixteen_utterance_domains(tmp_path):
+    """EOU-120m shapes, q8_0, 200 sessions in one call: the batch runs as
+    sixteen-utterance domains of 16 workgroups (the plan for 129..256
+    utterances).  A sample decoded alone gives the same decisions bit for bit,
+    and the sample replays through the oracle."""
+    from parakeet_amd import gguf, pk, synth
+    import oracle
+    path = str(tmp_path / "eou.gguf")
+    synth.make_shape(path, "eou-120m")
+    B, T = 200, 6
+    dev = pk.Decoder.from_gguf(path, n_slots=B + 4)
+    om = oracle.OracleModel.from_gguf(path, gguf)
+    encs = [synth.encoder_frames(900 + u, T, 512) for u in range(B)]
+    res = dev.decode(encs, trace=True, max_symbols=5)
+    sample = [0, 77, 150, 199]
+    for k, u in enumerate(sample):
+        alone = dev.decode([encs[u]], slots=[B + k], trace=True, max_symbols=5)[0]
+        assert np.array_equal(alone["trace"], res[u]["trace"]), u
+        assert alone["segments"].tolist() == res[u]["segments"].tolist(), u
+    reps = _replay_all(om, [encs[u] for u in sample], [res[u] for u in sample], 5)
+    reps = [(sample[i], rep, st) for i, rep, st in reps]
+    near, worst = _assert_replays(dev, reps, res)
+    print(f"eou B=200: steps={sum(r['steps'] for r in res)} sample near_ties={near} worst_state_rel={worst:.2e}")
+    dev.close()
