@@ -231,19 +231,36 @@ class Decoder:
     def decode(self, encs: list, slots=None, max_symbols: int | None = None, blank_bias=None,
                tokens_base=None, trace: bool = False, token_cap: int | None = None):
         """Host-memory batch: encs[u] is [T_u, D] f32.  Returns a list of dicts."""
-        info = self.info
         n = len(encs)
-        max_symbols = info.max_symbols if max_symbols is None else max_symbols
-        slots = np.arange(n, dtype=np.int32) if slots is None else np.asarray(slots, np.int32)
         T = np.array([e.shape[0] if e.ndim == 2 else 0 for e in encs], np.int32)
         rows = np.concatenate([[0], np.cumsum(T)[:-1]]).astype(np.int64) if n else np.zeros(0, np.int64)
-        d_enc = encs[0].shape[1] if n and encs[0].ndim == 2 else info.D
+        d_enc = encs[0].shape[1] if n and encs[0].ndim == 2 else self.info.D
         if n and T.sum() > 0:
             live = [e for e in encs if e.ndim == 2 and e.shape[0] > 0]
             enc = (np.concatenate(live) if all(e.dtype == np.float32 for e in live)
                    else np.concatenate([np.asarray(e, np.float32) for e in live]))
         else:
             enc = np.zeros((1, d_enc), np.float32)
+        return self._decode(MEM_HOST, _ptr(enc), rows, T, d_enc, slots, max_symbols, blank_bias, tokens_base,
+                            trace, token_cap)
+
+    def decode_device_frames(self, enc_ptr: int, enc_row, n_frames, slots=None, max_symbols: int | None = None,
+                             blank_bias=None, tokens_base=None, trace: bool = False, token_cap: int | None = None):
+        """Frames already in device memory (e.g. an encoder output tensor's data
+        pointer), read in place: utterance u decodes rows enc_row[u] ..
+        enc_row[u] + n_frames[u] of the [rows, D] f32 array at enc_ptr.  The
+        producer's stream must be synchronised first.  Returns what decode does."""
+        rows = np.ascontiguousarray(enc_row, np.int64)
+        T = np.ascontiguousarray(n_frames, np.int32)
+        return self._decode(MEM_DEVICE_FRAMES, C.c_void_p(enc_ptr), rows, T, self.info.D, slots, max_symbols,
+                            blank_bias, tokens_base, trace, token_cap)
+
+    def _decode(self, mem, enc, rows, T, d_enc, slots, max_symbols, blank_bias, tokens_base, trace, token_cap):
+        """One pk_decode call with host outputs; per-utterance result dicts."""
+        info = self.info
+        n = len(T)
+        max_symbols = info.max_symbols if max_symbols is None else max_symbols
+        slots = np.arange(n, dtype=np.int32) if slots is None else np.asarray(slots, np.int32)
         maxT = int(T.max()) if n else 0
         cap = token_cap if token_cap is not None else maxT * max(1, max_symbols) + 1
         toks = np.zeros((n, cap), np.int32)
@@ -256,8 +273,8 @@ class Decoder:
         bb = None if blank_bias is None else np.ascontiguousarray(blank_bias, np.float32)
         tb = None if tokens_base is None else np.ascontiguousarray(tokens_base, np.int32)
         b = PkBatch()
-        b.n_utts, b.mem, b.d_enc, b.max_symbols = n, MEM_HOST, d_enc, max_symbols
-        b.enc, b.enc_row, b.n_frames, b.slot = _ptr(enc), _ptr(rows), _ptr(T), _ptr(slots)
+        b.n_utts, b.mem, b.d_enc, b.max_symbols = n, mem, d_enc, max_symbols
+        b.enc, b.enc_row, b.n_frames, b.slot = enc, _ptr(rows), _ptr(T), _ptr(slots)
         b.blank_bias, b.tokens_base = _ptr(bb), _ptr(tb)
         b.tokens, b.token_cap, b.n_tokens, b.steps = _ptr(toks), cap, _ptr(ntok), _ptr(steps)
         b.segments, b.seg_cap, b.n_segments = _ptr(segs), cap + 1, _ptr(nseg)

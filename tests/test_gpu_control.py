@@ -307,3 +307,30 @@ def test_device_frames_host_outputs(tmp_path):
     b.slot = pk._ptr(np.arange(8, 12, dtype=np.int32))
     assert pk.lib().pk_decode(dec.h, C.byref(b)) == 3      # PK_ERR_ARG
     assert "aligned" in pk.lib().pk_last_error().decode()
+
+
+@pytest.mark.parametrize("kind", ["tdt", "eou"])
+def test_python_decode_device_frames(tmp_path, kind):
+    """Decoder.decode_device_frames (the Python form of the device handoff):
+    ragged windows of one device array, decoded in place, equal decode() of
+    the same frames from host memory, traces and EOU segments included."""
+    from parakeet_amd import hipmem, pk, synth
+    path = str(tmp_path / "m.gguf")
+    (small_tdt if kind == "tdt" else small_eou)(path)
+    dec = pk.Decoder.from_gguf(path, n_slots=10)
+    D = dec.info.D
+    Ts = [11, 4, 0, 16] if kind == "eou" else [11, 4, 1, 16]
+    encs = [synth.encoder_frames(680 + u, T, D) for u, T in enumerate(Ts)]
+    want = dec.decode(encs, slots=[0, 1, 2, 3], trace=True)
+    rows = np.array([40, 0, 20, 22], np.int64)
+    frames = np.full((60, D), np.nan, np.float32)
+    for u, T in enumerate(Ts):
+        frames[rows[u]:rows[u] + T] = encs[u]
+    enc_d = hipmem.DeviceArray.from_numpy(frames)
+    hipmem.synchronize()
+    got = dec.decode_device_frames(enc_d.ptr, rows, Ts, slots=[4, 5, 6, 7], trace=True)
+    for u in range(len(Ts)):
+        assert got[u]["tokens"].tolist() == want[u]["tokens"].tolist(), u
+        assert got[u]["steps"] == want[u]["steps"], u
+        assert np.array_equal(got[u]["trace"], want[u]["trace"]), u
+        assert got[u]["segments"].tolist() == want[u]["segments"].tolist(), u
