@@ -900,7 +900,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         auto items = [&](const pkdev::TMat &m) { return (m.tiles + pl.P - 1) / pl.P; };
         auto units = [&](const pkdev::TMat &m) {
             const int kbe = m.type == PK_TYPE_F32 ? 2 * m.KB : m.KB;
-            return (kbe + pkdev::kUnit - 1) / pkdev::kUnit;
+            return (kbe + pkdev::unit_blocks(m.type) - 1) / pkdev::unit_blocks(m.type);
         };
         int most = items(p.w_out), kslots = items(p.w_out) * units(p.w_out);
         for (int l = 0; l < p.L; ++l) {

@@ -540,7 +540,7 @@ __device__ __forceinline__ void stage_act(const Act &x, int K, int n, __amdgpu_b
 // A phase multiplies weight row tiles ("items") by one staged 16-utterance
 // activation block.  Items 0 .. n_a-1 are tiles rank, rank+P, ... of matrix A,
 // items n_a .. n_items-1 the same of matrix B (same storage type and K).  Each
-// item's K blocks are cut into units of at most kUnit blocks (f32 weights count
+// item's K blocks are cut into units of at most kUnitOf blocks (f32 weights count
 // every K block twice, once per f16 plane); the units are numbered item-major
 // and every wave takes a contiguous range of them.  A unit's fragments are
 // loaded with one batch of loads and multiplied by straight-line code, so
@@ -549,7 +549,10 @@ __device__ __forceinline__ void stage_act(const Act &x, int K, int n, __amdgpu_b
 // (item, wave) in LDS slot item + wave; phase_reduce sums each item's partials
 // in wave order -- a fixed order, so results do not depend on timing.
 
-constexpr int kUnit = 5;   // K blocks per unit (measured: 5 beats 8 and 10 with fragments from L2 or LDS)
+// K blocks per unit, by weight storage.  Measured: q8_0 5 (beats 4, 8 and 10 at B=1/64/256);
+// f16 and f32 4 (TDT-1.1b f16 at B=256: 49.9 vs 60.5 ms per launch with 5).
+template <bool Q8> constexpr int kUnitOf = Q8 ? 5 : 4;
+__host__ __device__ constexpr int unit_blocks(int type) { return type == PK_TYPE_Q8_0 ? 5 : 4; }
 
 // Fragments of one unit: blocks sb0 .. sb0+nb-1 of one tile; blocks past nb
 // read as zero (buffer loads past the range return 0).
@@ -567,12 +570,12 @@ __device__ __forceinline__ WView pick(bool first, const WView &x, const WView &y
 
 template <bool Q8, bool CACHED>
 __device__ __forceinline__ void unit_load(const WView m, bool two, int tile, int li, const unsigned char *wc, int sb0,
-                                          int nb, int lane, uint4 (&f)[kUnit]) {
+                                          int nb, int lane, uint4 (&f)[kUnitOf<Q8>]) {
     const unsigned bad = 0x80000000u;
     if (CACHED) {   // this workgroup's tiles are cached in LDS (local index li)
         const unsigned char *base = wc + m.lds_off;
 #pragma unroll
-        for (int j = 0; j < kUnit; ++j) {
+        for (int j = 0; j < kUnitOf<Q8>; ++j) {
             const bool ok = j < nb;
             const int sb = ok ? sb0 + j : sb0;
             uint4 v;
@@ -596,7 +599,7 @@ __device__ __forceinline__ void unit_load(const WView m, bool two, int tile, int
         const __amdgpu_buffer_rsrc_t rs = rsrc(m.scale, (unsigned)m.tiles * m.KB * kTile * 2u);
         const unsigned f0 = (unsigned)tile * m.KB + sb0;
 #pragma unroll
-        for (int j = 0; j < kUnit; ++j) {
+        for (int j = 0; j < kUnitOf<Q8>; ++j) {
             const bool ok = j < nb;
             const unsigned oq = ok ? ((f0 + j) * kWave + lane) * 8u : bad;
             const unsigned os = ok ? ((f0 + j) * kTile + (lane >> 4) * 4u) * 2u : bad;
@@ -609,7 +612,7 @@ __device__ __forceinline__ void unit_load(const WView m, bool two, int tile, int
         const __amdgpu_buffer_rsrc_t rh = rsrc(m.a, bytes);
         const __amdgpu_buffer_rsrc_t rl = rsrc(two ? m.a_lo : m.a, bytes);
 #pragma unroll
-        for (int j = 0; j < kUnit; ++j) {
+        for (int j = 0; j < kUnitOf<Q8>; ++j) {
             const int sb = sb0 + j;
             const int kb = two ? sb >> 1 : sb;
             const unsigned o = j < nb ? (((unsigned)tile * m.KB + kb) * kWave + lane) * 16u : bad;
@@ -643,17 +646,17 @@ __device__ __forceinline__ MatSrc mat_src(const TMat &m, bool two, const unsigne
     return s;
 }
 
-// Fragments of one unit, blocks sb0 .. sb0+kUnit-1 of tile `tile` (local index
-// li in the LDS cache).  FULL: all kUnit blocks exist (K is a whole number of
+// Fragments of one unit, blocks sb0 .. sb0+kUnitOf-1 of tile `tile` (local index
+// li in the LDS cache).  FULL: all kUnitOf blocks exist (K is a whole number of
 // units), so every offset is a lane constant plus a wave-uniform base plus an
 // immediate.  Otherwise blocks past nb read as zero (buffer loads past the
 // range return 0; cached blocks are zeroed).
 template <bool Q8, bool CACHED, bool FULL>
 __device__ __forceinline__ void unit_load_src(const MatSrc &m, bool two, int tile, int li, int sb0, int nb, int lane,
-                                              uint4 (&f)[kUnit]) {
+                                              uint4 (&f)[kUnitOf<Q8>]) {
     if (CACHED) {
 #pragma unroll
-        for (int j = 0; j < kUnit; ++j) {
+        for (int j = 0; j < kUnitOf<Q8>; ++j) {
             const bool ok = FULL || j < nb;
             const int sb = ok ? sb0 + j : sb0;
             uint4 v;
@@ -675,7 +678,7 @@ __device__ __forceinline__ void unit_load_src(const MatSrc &m, bool two, int til
     if (Q8) {
         const int f0 = tile * m.KB + sb0;   // wave-uniform fragment index of block sb0
 #pragma unroll
-        for (int j = 0; j < kUnit; ++j) {
+        for (int j = 0; j < kUnitOf<Q8>; ++j) {
             uint2 q, d;
             if (FULL) {
                 q = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(m.r0, lane * 8 + j * 512, f0 * 512, 0));
@@ -692,7 +695,7 @@ __device__ __forceinline__ void unit_load_src(const MatSrc &m, bool two, int til
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < kUnit; ++j) {
+        for (int j = 0; j < kUnitOf<Q8>; ++j) {
             const int sb = sb0 + j;
             const int kb = two ? sb >> 1 : sb;
             const bool ok = FULL || j < nb;
@@ -704,10 +707,11 @@ __device__ __forceinline__ void unit_load_src(const MatSrc &m, bool two, int til
 }
 
 // The activation fragments of a unit's K blocks (all reads issued at once).
-__device__ __forceinline__ void unit_act(const Act &x, int xo, bool two, int sb0, int nb, half8 (&ah)[kUnit],
-                                         half8 (&al)[kUnit]) {
+template <int U>
+__device__ __forceinline__ void unit_act(const Act &x, int xo, bool two, int sb0, int nb, half8 (&ah)[U],
+                                         half8 (&al)[U]) {
 #pragma unroll
-    for (int j = 0; j < kUnit; ++j) {
+    for (int j = 0; j < U; ++j) {
         const int sb = min(sb0 + j, sb0 + nb - 1);
         const int kb = two ? sb >> 1 : sb;
         ah[j] = *reinterpret_cast<const half8 *>(x.hi + xo + kb * 32);
@@ -718,10 +722,11 @@ __device__ __forceinline__ void unit_act(const Act &x, int xo, bool two, int sb0
 // acc += (unit's weight blocks) . (activation blocks).  Zero blocks past nb
 // add nothing.
 template <bool Q8>
-__device__ __forceinline__ f32x4 unit_mma(const uint4 (&f)[kUnit], const half8 (&ah)[kUnit], const half8 (&al)[kUnit],
+__device__ __forceinline__ f32x4 unit_mma(const uint4 (&f)[kUnitOf<Q8>], const half8 (&ah)[kUnitOf<Q8>],
+                                          const half8 (&al)[kUnitOf<Q8>],
                                           bool two, int sb0, f32x4 acc) {
 #pragma unroll
-    for (int j = 0; j < kUnit; ++j) {
+    for (int j = 0; j < kUnitOf<Q8>; ++j) {
         const half8 bh = ah[j], bl = al[j];
         if (Q8) {
             const half8 w = q8_to_half8(make_uint2(f[j].x, f[j].y));
@@ -756,7 +761,8 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
     const int lane = threadIdx.x & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const bool two = !Q8 && A.type == PK_TYPE_F32;
     const int KBe = two ? 2 * A.KB : A.KB;
-    const int S = (KBe + kUnit - 1) / kUnit;          // units per item
+    constexpr int U = kUnitOf<Q8>;
+    const int S = (KBe + U - 1) / U;                  // units per item
     const int N = n_items * S;
     const int c0 = wave_cut(N, wave), c1 = wave_cut(N, wave + 1);
     if (c0 >= c1) return;
@@ -764,7 +770,7 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
     // rows past x.n are not staged (they hold older values) and the columns
     // they feed are never read.
     const int xo = (lane & 15) * x.kp + (lane >> 4) * 8;
-    half8 ah[kUnit], al[kUnit];
+    half8 ah[U], al[U];
     if (KMAJ) {
         // unit u = c * n_items + item: a wave's range runs over items at one K
         // chunk c, so its activation fragments are read once per chunk; one
@@ -774,16 +780,16 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
         const MatSrc sA = mat_src<Q8, CACHED>(A, two, wc), sB = mat_src<Q8, CACHED>(Bm, two, wc);
         for (int u = c0; u < c1;) {
             const int c = u / n_items, i0 = u - c * n_items, i1 = min(n_items, i0 + (c1 - u));
-            const int sb0 = c * kUnit, nb = min(kUnit, KBe - sb0);
+            const int sb0 = c * U, nb = min(U, KBe - sb0);
             unit_act(x, xo, two, sb0, nb, ah, al);
             for (int item = i0; item < min(i1, n_a); ++item) {
-                uint4 f[kUnit];
+                uint4 f[U];
                 unit_load_src<Q8, CACHED, FULL>(sA, two, rank + item * P, item, sb0, nb, lane, f);
                 red[(item * S + c) * kWave + lane] = unit_mma<Q8>(f, ah, al, two, sb0, f32x4{0.f, 0.f, 0.f, 0.f});
             }
             for (int item = max(i0, n_a); item < i1; ++item) {
                 const int li = item - n_a;
-                uint4 f[kUnit];
+                uint4 f[U];
                 unit_load_src<Q8, CACHED, FULL>(sB, two, rank + li * P, li, sb0, nb, lane, f);
                 red[(item * S + c) * kWave + lane] = unit_mma<Q8>(f, ah, al, two, sb0, f32x4{0.f, 0.f, 0.f, 0.f});
             }
@@ -797,10 +803,10 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
         int item = c0 / S, c = c0 - item * S;
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         for (int u = c0; u < c1; ++u) {
-            const int sb0 = c * kUnit, nb = min(kUnit, KBe - sb0);
+            const int sb0 = c * U, nb = min(U, KBe - sb0);
             const bool in_a = item < n_a;
             const int li = in_a ? item : item - n_a;
-            uint4 f[kUnit];
+            uint4 f[U];
             unit_load<Q8, CACHED>(pick(in_a, vA, vB), two, rank + li * P, li, wc, sb0, nb, lane, f);
             unit_act(x, xo, two, sb0, nb, ah, al);
             acc = unit_mma<Q8>(f, ah, al, two, sb0, acc);
@@ -850,7 +856,8 @@ __device__ __forceinline__ void run_phase_(const TMat &A, int n_a, const TMat &B
     const bool cached = wc != nullptr && A.lds_off >= 0;
     const int KBe = A.type == PK_TYPE_F32 ? 2 * A.KB : A.KB;
     // K-major with K a whole number of units: the unmasked unit loads
-    const bool full = KMAJ && KBe % kUnit == 0;
+    const int U = unit_blocks(A.type);
+    const bool full = KMAJ && KBe % U == 0;
     if (A.type == PK_TYPE_Q8_0) {
         if (cached) {
             if (full) phase_partials<true, true, KMAJ, true>(A, n_a, Bm, n_items, rank, P, x, red, wc);
@@ -863,7 +870,7 @@ __device__ __forceinline__ void run_phase_(const TMat &A, int n_a, const TMat &B
         if (cached) phase_partials<false, true, KMAJ, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
         else phase_partials<false, false, KMAJ, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
     }
-    phase_reduce<KMAJ>(n_items, (KBe + kUnit - 1) / kUnit, red, epi);
+    phase_reduce<KMAJ>(n_items, (KBe + U - 1) / U, red, epi);
 }
 template <class EpiFn>
 __device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
