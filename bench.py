@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--frames", type=int, default=750)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-utts", type=int, default=16)
+    ap.add_argument("--cpu-utts", type=int, default=64)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain device copy of MIB MiB (calibrates hardware byte counters)")
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -87,6 +87,8 @@ class Workload:
         assert self.calls < self.n_calls, "every call decodes fresh slots"
         slots = np.arange(self.B, dtype=np.int32) + self.slot_base + self.calls * self.B
         self.calls += 1
+        if trace:
+            self.traced_slots = slots
         ptrs = {k: v.ptr for k, v in self.out.items()}
         if trace:
             ptrs["trace"] = self.trace.ptr
@@ -104,6 +106,43 @@ class Workload:
     def free(self):
         for a in (self.enc, self.trace, *self.out.values()):
             a.free()
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def sampled_parity(om, wl, traces, encs_of, sample, max_symbols):
+    """Teacher-forced oracle replay of a sample of the workload's utterances
+    (decisions from the traced call): unexplained mismatches, near-ties, and
+    the worst L2-relative error of the final h and c against the oracle."""
+    from concurrent.futures import ThreadPoolExecutor
+    sample = [u for u in sample if u < wl.B]
+
+    def one(u):
+        st = om.new_state()
+        rep = om.replay_window(encs_of(u), st, max_symbols, traces[u], tie_eps=1e-4)
+        return u, rep, st
+    with ThreadPoolExecutor(len(sample)) as ex:
+        reps = list(ex.map(one, sample))
+    unexplained = near = 0
+    worst = 0.0
+    for u, rep, st in reps:
+        unexplained += rep["stats"]["unexplained"] + rep["stats"]["structure_error"]
+        near += rep["stats"]["near_ties"]
+        d = wl.dec.read_state(int(wl.traced_slots[u]))
+        for a, b in ((d["h"], st.h), (d["c"], st.c)):
+            worst = max(worst, float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)))
+    return {"utterances": list(sample), "steps": int(sum(len(traces[u]) for u in sample)),
+            "unexplained_mismatches": int(unexplained), "near_ties": int(near),
+            "tie_eps": 1e-4, "max_state_rel_err": float(f"{worst:.3e}")}
 
 
 def timed(wl, warmup, steps):
@@ -319,7 +358,11 @@ def main():
         import oracle
         om = oracle.OracleModel.from_gguf(path, gguf)
         nu = min(args.cpu_utts, B)
-        threads = max(1, min(16, os.cpu_count() or 1, nu))
+        host_cpus = os.cpu_count() or 1
+        # the reference CLI runs one decoder per hardware thread (std::thread::hardware_concurrency,
+        # src/main.cpp:57); the GPU box grants this process a 16-thread CPU share (OMP_NUM_THREADS)
+        share = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+        threads = max(1, min(share, host_cpus, nu))
         encs = [synth.encoder_frames(u, T, D) for u in range(nu)]
         t0 = time.perf_counter()
         r = om.decode_batch(encs, MS, n_threads=threads)
@@ -327,13 +370,25 @@ def main():
         cpu_steps = int(np.sum(r["steps"]))
         out["cpu_baseline"] = {"value": round(cpu_steps / dt, 1), "unit": "decode steps/s", "cores": threads,
                                "kind": "port",
-                               "sample": f"first {nu} of the {B} utterances (full {T} frames each), "
-                                         f"{cpu_steps} steps in {dt:.2f} s, one utterance per thread task, "
-                                         f"oracle built with -O3 -ffast-math -funroll-loops"}
-        # the same utterances decoded on the device agree token for token
+                               "sample": f"all {nu} of the {B} utterances (full {T} frames each), "
+                                         f"{cpu_steps} steps in {dt:.2f} s, one utterance per thread task on "
+                                         f"{threads} threads, oracle built with -O3 -ffast-math -funroll-loops",
+                               "host_cpus": host_cpus, "cpu_model": cpu_model()}
+        # the same utterances decoded on the device emit the same tokens
         dev_tok = wl.out["n_tokens"].to_numpy(np.int32, B)[:nu]
         out["cpu_baseline"]["token_counts_equal"] = bool(
             all(len(r["tokens"][u]) == dev_tok[u] for u in range(nu)))
+        # B=1 latency of the scalar reference loop: one thread, the 125-frame utterance
+        e1 = synth.encoder_frames(0, 125, D)
+        t0 = time.perf_counter()
+        r1 = om.decode_window(e1, om.new_state(), MS)
+        dt1 = time.perf_counter() - t0
+        out["cpu_baseline"]["b1"] = {"us_per_step": round(dt1 * 1e6 / max(1, r1["steps"]), 1), "cores": 1,
+                                     "steps": int(r1["steps"]), "frames": 125}
+        # parity of the timed workload, outside the timed region: a sample of its
+        # utterances replayed through the oracle following the device's decisions
+        out["parity"] = sampled_parity(om, wl, traces, encs_of=lambda u: synth.encoder_frames(u, T, D),
+                                       sample=(0, 21, 42, 63), max_symbols=MS)
 
     if not args.no_extras:
         # B=1, T=125 (10 s of audio): per-step latency
@@ -345,6 +400,7 @@ def main():
                      "us_per_step_wall": round(wall1 / 20 * 1e6 / st1, 3)}
         wl1.free()
         base = B * n_calls + n_b1
+        wl.free()
         # B=256, T=750: lockstep throughput on the same decoder
         out["b256"] = lockstep_extra(pk, hipmem, roofline, dec, cost, np.full(256, 750), D, MS, base)
         base += 256 * 4
@@ -365,6 +421,9 @@ def main():
         out["eou_stream_b128"] = eou_stream_extra(pk, hipmem, roofline, gguf, synth, tmp)
 
     print(json.dumps(out), flush=True)
+    # every device buffer is released before the interpreter exits (no HIP call
+    # runs from a finaliser after the runtime has been torn down)
+    wl.free()
     dec.close()
 
 

@@ -129,6 +129,13 @@ typedef struct pk_batch {
     int32_t *n_segments;        /* EOU out [n_utts], nullable */
     int32_t *trace;             /* out [n_utts][trace_cap][2] (token, duration index) per step, nullable */
     int32_t trace_cap;
+    /* Debug tap, nullable: out [n_utts][logit_steps][V+1+num_durations] f32, the joint
+     * logits (bias and blank offset included) of each utterance's first logit_steps
+     * steps -- the values src/parakeet_tdt.cpp:154-177 produces before the argmax.
+     * Rows of steps an utterance does not reach are left untouched.  Parity tests
+     * only; a timed call passes NULL. */
+    float *logits;
+    int32_t logit_steps;
 } pk_batch;
 
 /* Slot control words (pk_slot_read ctrl[]): */

@@ -813,9 +813,13 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
 
     // outputs: device arrays as given, or a device staging area copied back
     const int tcap = bt->token_cap, scap = std::max(bt->seg_cap, 0), trcap = bt->trace ? bt->trace_cap : 0;
+    const int lsteps = bt->logits ? std::max(bt->logit_steps, 0) : 0;
+    const size_t lrow = (size_t)lsteps * p.Vo;   // tapped floats per utterance
     int *o_tok, *o_ntok, *o_steps, *o_seg = nullptr, *o_nseg = nullptr, *o_trace = nullptr;
+    float *o_logits = nullptr;
     if (host) {
-        const size_t need = ((size_t)m * tcap + 3 * (size_t)m + (size_t)m * scap + (size_t)m * trcap * 2) * 4 + 64;
+        const size_t need =
+            ((size_t)m * tcap + 3 * (size_t)m + (size_t)m * scap + (size_t)m * trcap * 2 + (size_t)m * lrow) * 4 + 64;
         if ((rc = dec->d_out.ensure(need))) return rc;
         int *o = dec->d_out.as<int>();
         o_tok = o; o += (size_t)m * tcap;
@@ -823,10 +827,12 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         o_steps = o; o += m;
         o_nseg = o; o += m;
         o_seg = scap > 0 ? o : nullptr; o += (size_t)m * scap;
-        o_trace = trcap > 0 ? o : nullptr;
+        o_trace = trcap > 0 ? o : nullptr; o += (size_t)m * trcap * 2;
+        o_logits = lrow > 0 ? reinterpret_cast<float *>(o) : nullptr;
     } else {
         o_tok = bt->tokens; o_ntok = bt->n_tokens; o_steps = bt->steps;
         o_seg = bt->segments; o_nseg = bt->n_segments; o_trace = bt->trace;
+        o_logits = lrow > 0 ? bt->logits : nullptr;
     }
     p.n_utts = m;
     p.encp = dec->d_encp.as<float>();
@@ -840,6 +846,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     p.n_tokens = o_ntok; p.steps = o_steps;
     p.segs = o_seg; p.seg_cap = scap; p.n_segs = o_nseg;
     p.trace = o_trace; p.trace_cap = trcap;
+    p.logits = o_logits; p.logit_steps = lsteps;
     p.max_sym = bt->max_symbols;
     p.max_iter = max_iter;
     p.n_dom = pl.n_dom;
@@ -974,6 +981,10 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
                                          hipMemcpyDeviceToHost, dec->stream));
             HIP_TRY(hipStreamSynchronize(dec->stream));
         }
+        if (o_logits)   // debug tap: straight into the caller's rows (utterance order may differ)
+            for (int i = 0; i < m; ++i)
+                HIP_TRY(hipMemcpy(bt->logits + (size_t)map[i] * lrow, o_logits + (size_t)i * lrow, lrow * 4,
+                                  hipMemcpyDeviceToHost));
         const int *s_tok = dec->h_out.as<int>(), *s_seg = s_tok + (size_t)m * wt, *s_tr = s_seg + (size_t)m * ws;
         for (int i = 0; i < m; ++i) {
             const int u = map[i];

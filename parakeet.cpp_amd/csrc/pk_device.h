@@ -88,6 +88,7 @@ struct KParams {
     int *n_tokens; int *steps;
     int *segs; int seg_cap; int *n_segs;
     int *trace; int trace_cap;
+    float *logits; int logit_steps;   // nullable debug tap [n_utts][logit_steps][Vo]
     // exchange buffers of one launch (batch-indexed, written/read coherently)
     float *hx;           // [2][L][n][H] ping-pong by utterance parity
     float *cx;           // [2][L][n][H]
@@ -1017,6 +1018,12 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         // (b_out is zero-padded to whole tiles)
         const float *btab = S.bias + bias_base(p, s.rank, s.P, p.L);
         TL(1);
+        // debug logit tap: this lane's utterance row of the current step
+        float *ltap = nullptr;
+        if (p.logits && u < nc) {
+            const int ul = s.jst[c0 + u], step = s.steps[ul];
+            if (step < p.logit_steps) ltap = p.logits + ((size_t)s.b[ul] * p.logit_steps + step) * p.Vo;
+        }
         // each lane keeps its best key per head over all its rows; lanes of one
         // column then combine, and one LDS atomic per column and head follows
         unsigned long long best0 = 0ull, best1 = 0ull;
@@ -1032,6 +1039,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
                           const float bias = i == 0 ? bias4.x : i == 1 ? bias4.y : i == 2 ? bias4.z : bias4.w;
                           float v = acc[i] + bias;
                           if (row == p.blank) v += bb;
+                          if (ltap) ltap[row] = v;
                           if (row < p.V1) {
                               const unsigned long long key = make_key(v, row);
                               best0 = key > best0 ? key : best0;

@@ -7,6 +7,7 @@ runtime instance.
 from __future__ import annotations
 
 import ctypes as C
+import sys
 
 import numpy as np
 
@@ -60,6 +61,12 @@ class DeviceArray:
             self.ptr = None
 
     def __del__(self):
+        # No HIP call while the interpreter shuts down: the runtime (and a
+        # profiler's preloaded library) may already be torn down by then.
+        # Callers free their buffers explicitly; a buffer left to the garbage
+        # collector at exit is reclaimed with the process.
+        if sys.is_finalizing():
+            return
         try:
             self.free()
         except Exception:

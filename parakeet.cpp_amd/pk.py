@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import sys
 
 import numpy as np
 
@@ -63,7 +64,7 @@ class PkBatch(C.Structure):
                 ("tokens_base", C.c_void_p), ("tokens", C.c_void_p), ("token_cap", C.c_int32),
                 ("n_tokens", C.c_void_p), ("steps", C.c_void_p), ("segments", C.c_void_p),
                 ("seg_cap", C.c_int32), ("n_segments", C.c_void_p), ("trace", C.c_void_p),
-                ("trace_cap", C.c_int32)]
+                ("trace_cap", C.c_int32), ("logits", C.c_void_p), ("logit_steps", C.c_int32)]
 
 
 EXPORTED = ["pk_decoder_create", "pk_decoder_destroy", "pk_slot_init", "pk_slot_reset",
@@ -206,6 +207,8 @@ class Decoder:
             self.h = None
 
     def __del__(self):
+        if sys.is_finalizing():   # no HIP call during interpreter shutdown (see hipmem.DeviceArray)
+            return
         try:
             self.close()
         except Exception:
@@ -229,8 +232,10 @@ class Decoder:
 
     # ---- decode ----
     def decode(self, encs: list, slots=None, max_symbols: int | None = None, blank_bias=None,
-               tokens_base=None, trace: bool = False, token_cap: int | None = None):
-        """Host-memory batch: encs[u] is [T_u, D] f32.  Returns a list of dicts."""
+               tokens_base=None, trace: bool = False, token_cap: int | None = None, logit_steps: int = 0):
+        """Host-memory batch: encs[u] is [T_u, D] f32.  Returns a list of dicts
+        (``logits``: [logit_steps, Vo] joint logits of the first steps when
+        logit_steps > 0; rows past the utterance's steps are NaN)."""
         n = len(encs)
         T = np.array([e.shape[0] if e.ndim == 2 else 0 for e in encs], np.int32)
         rows = np.concatenate([[0], np.cumsum(T)[:-1]]).astype(np.int64) if n else np.zeros(0, np.int64)
@@ -242,10 +247,11 @@ class Decoder:
         else:
             enc = np.zeros((1, d_enc), np.float32)
         return self._decode(MEM_HOST, _ptr(enc), rows, T, d_enc, slots, max_symbols, blank_bias, tokens_base,
-                            trace, token_cap)
+                            trace, token_cap, logit_steps)
 
     def decode_device_frames(self, enc_ptr: int, enc_row, n_frames, slots=None, max_symbols: int | None = None,
-                             blank_bias=None, tokens_base=None, trace: bool = False, token_cap: int | None = None):
+                             blank_bias=None, tokens_base=None, trace: bool = False, token_cap: int | None = None,
+                             logit_steps: int = 0):
         """Frames already in device memory (e.g. an encoder output tensor's data
         pointer), read in place: utterance u decodes rows enc_row[u] ..
         enc_row[u] + n_frames[u] of the [rows, D] f32 array at enc_ptr.  The
@@ -253,9 +259,10 @@ class Decoder:
         rows = np.ascontiguousarray(enc_row, np.int64)
         T = np.ascontiguousarray(n_frames, np.int32)
         return self._decode(MEM_DEVICE_FRAMES, C.c_void_p(enc_ptr), rows, T, self.info.D, slots, max_symbols,
-                            blank_bias, tokens_base, trace, token_cap)
+                            blank_bias, tokens_base, trace, token_cap, logit_steps)
 
-    def _decode(self, mem, enc, rows, T, d_enc, slots, max_symbols, blank_bias, tokens_base, trace, token_cap):
+    def _decode(self, mem, enc, rows, T, d_enc, slots, max_symbols, blank_bias, tokens_base, trace, token_cap,
+                logit_steps=0):
         """One pk_decode call with host outputs; per-utterance result dicts."""
         info = self.info
         n = len(T)
@@ -279,6 +286,10 @@ class Decoder:
         b.tokens, b.token_cap, b.n_tokens, b.steps = _ptr(toks), cap, _ptr(ntok), _ptr(steps)
         b.segments, b.seg_cap, b.n_segments = _ptr(segs), cap + 1, _ptr(nseg)
         b.trace, b.trace_cap = (_ptr(tr) if trace else None), tcap
+        lg = None
+        if logit_steps > 0:
+            lg = np.full((n, logit_steps, info.Vo), np.nan, np.float32)
+            b.logits, b.logit_steps = _ptr(lg), logit_steps
         check(lib().pk_decode(self.h, C.byref(b)))
         # per-utterance views of this call's output arrays
         nt, st, ns = ntok.tolist(), steps.tolist(), nseg.tolist()
@@ -286,6 +297,9 @@ class Decoder:
         if trace:
             for u in range(n):
                 out[u]["trace"] = tr[u, :min(st[u], tcap)]
+        if lg is not None:
+            for u in range(n):
+                out[u]["logits"] = lg[u]
         return out
 
     def decode_device(self, enc_ptr: int, enc_row, n_frames, slots, max_symbols: int,

@@ -99,15 +99,16 @@ def test_cfg3_tdt11b_f16(tmp_path):
 
 
 def test_cfg4_eou_streaming_sessions(tmp_path):
-    """EOU-120m shapes, q8_0, B=128 sessions fed 2-frame chunks (10 chunks),
-    state carried; every window replayed on the oracle carrying its own state."""
+    """EOU-120m shapes, q8_0, B=128 sessions fed 2-frame chunks (all 40 chunks
+    of the workload), state carried; every window replayed on the oracle
+    carrying its own state."""
     from parakeet_amd import gguf, pk, synth
     import oracle
     path = str(tmp_path / "eou.gguf")
     synth.make_shape(path, "eou-120m")
     dev = pk.Decoder.from_gguf(path, n_slots=128)
     om = oracle.OracleModel.from_gguf(path, gguf)
-    B, C = 128, 10
+    B, C = 128, 40
     encs = [synth.encoder_frames(u, 2 * C, 512) for u in range(B)]
     for u in range(B):
         dev.init_state(u)
