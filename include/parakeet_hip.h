@@ -155,6 +155,17 @@ PK_API int pk_slot_reset(pk_decoder *dec, int32_t slot);
 PK_API int pk_slot_read(pk_decoder *dec, int32_t slot, float *h, float *c, float *pred, int32_t *ctrl);
 /* Decode one window for every utterance of the batch. */
 PK_API int pk_decode(pk_decoder *dec, const pk_batch *batch);
+/* pk_decode without any device allocation.  No counterpart in the reference:
+ * it is for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  batch->mem must be
+ * PK_MEM_DEVICE (frames and outputs already in device memory).  Every device
+ * buffer of the call beyond its inputs and outputs (descriptors, enc_proj rows,
+ * barrier flags, argmax keys, exchange buffers) comes from one fixed 32 MiB
+ * array per device, held until the process ends; a batch that needs more is
+ * refused with PK_ERR_UNSUPPORTED (about 16,000 frames x 640 joint units at
+ * 64 utterances).  All calls on one device share that array: two calls that
+ * overlap in time on the same device race. */
+PK_API int pk_decode_noalloc(pk_decoder *dec, const pk_batch *batch);
 /* Time, with HIP events on the handle's stream, the last pk_decode's
  * kernels: enc_proj GEMM and the decode loop (milliseconds). */
 PK_API int pk_last_timing(pk_decoder *dec, float *enc_proj_ms, float *loop_ms, int32_t *iterations);

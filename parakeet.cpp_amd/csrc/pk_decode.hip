@@ -254,6 +254,40 @@ int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *
     return 0;
 }
 
+// ---------------------------------------------------------------- fixed scratch
+//
+// pk_decode_noalloc takes every device buffer of a call beyond its inputs and
+// outputs (descriptor block, enc_proj rows, status / barrier flags / argmax
+// keys, exchange buffers) from this array instead of allocating.  Each device
+// holds its own copy for the life of the process; host code never uses the
+// symbol itself, only the address hipGetSymbolAddress returns for the current
+// device (kept per device in g_scratch).
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+struct ScratchTable {
+    std::mutex mu;
+    std::map<int, unsigned char *> ptr;   // device -> address of its scratch array
+};
+ScratchTable g_scratch;
+
+// The current device's scratch address, resolved once per device.
+int scratch_address(int device, unsigned char **out) {
+    std::lock_guard<std::mutex> lk(g_scratch.mu);
+    auto it = g_scratch.ptr.find(device);
+    if (it != g_scratch.ptr.end()) {
+        *out = it->second;
+        return 0;
+    }
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+        return fail(PK_ERR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch.ptr[device] = static_cast<unsigned char *>(ptr);
+    *out = static_cast<unsigned char *>(ptr);
+    return 0;
+}
+
 }  // namespace
 
 struct pk_decoder {
@@ -277,6 +311,7 @@ struct pk_decoder {
     DevBuf d_desc, d_encp, d_clear, d_enc, d_out, d_xchg, d_prof;   // d_clear: status, barrier flags, argmax keys
     std::vector<uint8_t> h_desc;
     HostBuf h_out;             // staging of host-memory outputs
+    unsigned char *scratch = nullptr;   // this device's fixed scratch array (pk_decode_noalloc)
     int last_iters = 0;
 };
 
@@ -370,7 +405,28 @@ Plan plan_domains(int m, int nwg, const std::vector<int32_t> &T) {
     return pl;
 }
 
-int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty);
+// One call's device buffers beyond inputs and outputs: grown handle buffers, or
+// (fixed != nullptr) consecutive 256-byte aligned pieces of the fixed scratch array.
+struct CallScratch {
+    unsigned char *fixed = nullptr;
+    size_t cap = 0, used = 0;
+    int get(DevBuf &buf, size_t bytes, void **out) {
+        if (!fixed) {
+            if (int rc = buf.ensure(std::max<size_t>(bytes, 1))) return rc;
+            *out = buf.p;
+            return 0;
+        }
+        const size_t at = (used + 255) & ~(size_t)255;
+        if (at + bytes > cap)
+            return fail(PK_ERR_UNSUPPORTED, "batch needs more than the %zu B fixed scratch (pk_decode_noalloc limit)",
+                        cap);
+        *out = fixed + at;
+        used = at + bytes;
+        return 0;
+    }
+};
+
+int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratch cs = CallScratch{});
 
 }  // namespace
 
@@ -560,6 +616,7 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
                                                      kBlock, need) != hipSuccess || per_cu < 1)
         return cleanup(fail(PK_ERR_DEVICE, "decode kernel does not fit on a CU"));
     dec->nwg = std::min(dec->n_cu, kBlock);
+    if ((rc = scratch_address(dec->device, &dec->scratch))) return cleanup(rc);
     if (hipStreamCreateWithFlags(&dec->stream, hipStreamNonBlocking) != hipSuccess)
         return cleanup(fail(PK_ERR_DEVICE, "stream"));
     for (auto &e : dec->ev)
@@ -640,6 +697,18 @@ PK_API int pk_decode(pk_decoder *dec, const pk_batch *bt) {
     return decode_impl(dec, bt, false);
 }
 
+PK_API int pk_decode_noalloc(pk_decoder *dec, const pk_batch *bt) {
+    g_err.clear();
+    if (!dec || !bt) return fail(PK_ERR_ARG, "pk_decode_noalloc: null argument");
+    if (bt->mem != PK_MEM_DEVICE)
+        return fail(PK_ERR_ARG, "pk_decode_noalloc takes device frames and device outputs (PK_MEM_DEVICE)");
+    if (!dec->scratch) return fail(PK_ERR_DEVICE, "fixed scratch not resolved for device %d", dec->device);
+    CallScratch cs;
+    cs.fixed = dec->scratch;
+    cs.cap = kScratchBytes;
+    return decode_impl(dec, bt, false, cs);
+}
+
 }  // extern "C"
 
 namespace {
@@ -684,7 +753,7 @@ int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds) {
     return 0;
 }
 
-int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
+int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratch cs) {
     if (!dec || !bt) return fail(PK_ERR_ARG, "pk_decode: null argument");
     KParams &p = dec->kp;
     if (bt->d_enc != dec->desc.d_enc)
@@ -777,7 +846,8 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     const size_t n64 = 2 * (size_t)m, n32 = 4 * (size_t)m + pl.dom_n.size() + pl.dom_list.size() +
                                               pl.wg_dom.size() + pl.wg_rank.size() + pl.dom_wg.size();
     const size_t desc_bytes = n64 * 8 + n32 * 4;
-    if ((rc = dec->d_desc.ensure(desc_bytes))) return rc;
+    void *d_desc = nullptr;
+    if ((rc = cs.get(dec->d_desc, desc_bytes, &d_desc))) return rc;
     dec->h_desc.resize(desc_bytes);
     uint8_t *hd = dec->h_desc.data();
     size_t off = 0;
@@ -785,7 +855,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         memcpy(hd + off, src, bytes);
         const size_t at = off;
         off += bytes;
-        return dec->d_desc.as<uint8_t>() + at;
+        return static_cast<uint8_t *>(d_desc) + at;
     };
     const long long *d_src = reinterpret_cast<const long long *>(put(src_row.data(), 8 * (size_t)m));
     const long long *d_dst = reinterpret_cast<const long long *>(put(dst_row.data(), 8 * (size_t)m));
@@ -798,15 +868,16 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     const int *d_wg_dom = reinterpret_cast<const int *>(put(pl.wg_dom.data(), 4 * pl.wg_dom.size()));
     const int *d_wg_rank = reinterpret_cast<const int *>(put(pl.wg_rank.data(), 4 * pl.wg_rank.size()));
     const int *d_dom_wg = reinterpret_cast<const int *>(put(pl.dom_wg.data(), 4 * pl.dom_wg.size()));
-    HIP_TRY(hipMemcpyAsync(dec->d_desc.p, hd, desc_bytes, hipMemcpyHostToDevice, dec->stream));
+    HIP_TRY(hipMemcpyAsync(d_desc, hd, desc_bytes, hipMemcpyHostToDevice, dec->stream));
 
     HIP_TRY(hipEventRecord(dec->ev[0], dec->stream));
+    float *d_encp = nullptr;
     if (rows > 0) {
-        if ((rc = dec->d_encp.ensure((size_t)rows * J * 4))) return rc;
+        if ((rc = cs.get(dec->d_encp, (size_t)rows * J * 4, reinterpret_cast<void **>(&d_encp)))) return rc;
         // tiles over the packed rows of all utterances
         dim3 grid((unsigned)((rows + pkdev::kEpTile - 1) / pkdev::kEpTile), 1, (J + pkdev::kEpTile - 1) / pkdev::kEpTile);
         pkdev::enc_proj_kernel<<<grid, 256, 0, dec->stream>>>(dec->w_enc_hi, dec->w_enc_lo, J, dec->b_enc, enc, D,
-                                                              d_src, d_dst, m, rows, dec->d_encp.as<float>());
+                                                              d_src, d_dst, m, rows, d_encp);
         HIP_TRY(hipGetLastError());
     }
     HIP_TRY(hipEventRecord(dec->ev[1], dec->stream));
@@ -835,7 +906,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
         o_logits = lrow > 0 ? bt->logits : nullptr;
     }
     p.n_utts = m;
-    p.encp = dec->d_encp.as<float>();
+    p.encp = d_encp;
     p.encp_rows = rows;
     p.encp_row = d_dst;
     p.T = d_T;
@@ -864,23 +935,31 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty) {
     // the words every launch starts from zero, in one allocation cleared by
     // one fill: 64 B of status, the barrier flags, the argmax keys
     const size_t flags_bytes = (size_t)nwg * kFlagStride * 4, clear_bytes = 256 + flags_bytes + keys_bytes;
-    if ((rc = dec->d_clear.ensure(clear_bytes))) return rc;
+    void *d_clear = nullptr, *d_xchg = nullptr;
+    if ((rc = cs.get(dec->d_clear, clear_bytes, &d_clear))) return rc;
     const size_t xh = 2 * (size_t)L * m * H, xp = (size_t)m * J, xr = 2 * (size_t)L * m * 4 * H;
     // the loop addresses the exchange buffers with 32-bit buffer offsets
     if ((2 * xh + xp + xr) * 4 >= (1ull << 31))
         return fail(PK_ERR_UNSUPPORTED, "exchange buffers of %d utterances exceed 2 GiB", m);
-    if ((rc = dec->d_xchg.ensure((2 * xh + xp + xr) * 4))) return rc;
-    p.hx = dec->d_xchg.as<float>();
+    if ((rc = cs.get(dec->d_xchg, (2 * xh + xp + xr) * 4, &d_xchg))) return rc;
+    p.hx = static_cast<float *>(d_xchg);
     p.cx = p.hx + xh;
     p.ppx = p.cx + xh;
     p.rx = p.ppx + xp;
     p.xchg_bytes = (unsigned)((2 * xh + xp + xr) * 4);
-    p.status = dec->d_clear.as<int>() + 4;
-    p.flags = reinterpret_cast<unsigned *>(dec->d_clear.as<uint8_t>() + 256);
-    p.keys = reinterpret_cast<unsigned long long *>(dec->d_clear.as<uint8_t>() + 256 + flags_bytes);
-    HIP_TRY(hipMemsetAsync(dec->d_clear.p, 0, clear_bytes, dec->stream));
+    p.status = static_cast<int *>(d_clear) + 4;
+    p.flags = reinterpret_cast<unsigned *>(static_cast<uint8_t *>(d_clear) + 256);
+    p.keys = reinterpret_cast<unsigned long long *>(static_cast<uint8_t *>(d_clear) + 256 + flags_bytes);
+    if (cs.fixed) {   // the fixed scratch keeps the last call's contents: cleared by a fill kernel
+        const size_t words = clear_bytes / 4;   // clear_bytes is a multiple of 32
+        pkdev::fill_zero_kernel<<<(unsigned)std::min<size_t>((words + 255) / 256, 1024), 256, 0, dec->stream>>>(
+            static_cast<unsigned *>(d_clear), words);
+        HIP_TRY(hipGetLastError());
+    } else {
+        HIP_TRY(hipMemsetAsync(d_clear, 0, clear_bytes, dec->stream));
+    }
     // PK_PROFILE_PHASES=1: workgroup 0 accumulates per-phase wall-clock time (stderr summary)
-    const bool prof = getenv("PK_PROFILE_PHASES") != nullptr;
+    const bool prof = !cs.fixed && getenv("PK_PROFILE_PHASES") != nullptr;
     p.prof = nullptr;
     if (prof) {
         if ((rc = dec->d_prof.ensure((pkdev::kPrN + 9 * pkdev::kTl) * 8))) return rc;

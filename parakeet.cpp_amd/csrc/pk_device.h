@@ -273,6 +273,11 @@ __global__ void __launch_bounds__(256) embed_proj_kernel(const float *__restrict
     }
 }
 
+// Zero n 32-bit words (clears the flags, keys and status words of a call).
+__global__ void __launch_bounds__(256) fill_zero_kernel(unsigned *__restrict p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0u;
+}
+
 // ---------------------------------------------------------------- enc_proj
 
 // encp[rows of utterance u] = b_e + W_e . enc[row] for every frame: an MFMA

@@ -68,7 +68,8 @@ class PkBatch(C.Structure):
 
 
 EXPORTED = ["pk_decoder_create", "pk_decoder_destroy", "pk_slot_init", "pk_slot_reset",
-            "pk_slot_read", "pk_decode", "pk_last_timing", "pk_last_error", "pk_device_info"]
+            "pk_slot_read", "pk_decode", "pk_decode_noalloc", "pk_last_timing", "pk_last_error",
+            "pk_device_info"]
 
 _lib = None
 
@@ -85,6 +86,7 @@ def lib():
         L.pk_slot_reset.argtypes = [C.c_void_p, C.c_int32]
         L.pk_slot_read.argtypes = [C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
         L.pk_decode.argtypes = [C.c_void_p, C.POINTER(PkBatch)]
+        L.pk_decode_noalloc.argtypes = [C.c_void_p, C.POINTER(PkBatch)]
         L.pk_last_timing.argtypes = [C.c_void_p, C.POINTER(C.c_float), C.POINTER(C.c_float),
                                      C.POINTER(C.c_int32)]
         L.pk_last_error.restype = C.c_char_p
@@ -304,10 +306,11 @@ class Decoder:
 
     def decode_device(self, enc_ptr: int, enc_row, n_frames, slots, max_symbols: int,
                       out_ptrs: dict, token_cap: int, blank_bias=None, trace_cap: int = 0,
-                      tokens_base=None):
+                      tokens_base=None, noalloc: bool = False):
         """Device-memory batch (inputs resident in HBM): pointers are device
         addresses; the descriptor arrays (enc_row, n_frames, slots, blank_bias,
-        tokens_base) are host arrays."""
+        tokens_base) are host arrays.  noalloc: pk_decode_noalloc (no device
+        allocation; call scratch from the fixed per-device array)."""
         n = len(n_frames)
         rows = np.ascontiguousarray(enc_row, np.int64)
         T = np.ascontiguousarray(n_frames, np.int32)
@@ -325,7 +328,7 @@ class Decoder:
         b.n_segments = C.c_void_p(out_ptrs["n_segments"]) if out_ptrs.get("n_segments") else None
         b.trace = C.c_void_p(out_ptrs["trace"]) if trace_cap else None
         b.trace_cap = trace_cap
-        check(lib().pk_decode(self.h, C.byref(b)))
+        check((lib().pk_decode_noalloc if noalloc else lib().pk_decode)(self.h, C.byref(b)))
 
     def last_timing(self):
         a, b, it = C.c_float(), C.c_float(), C.c_int32()
