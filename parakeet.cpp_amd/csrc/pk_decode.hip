@@ -222,8 +222,9 @@ int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *
                     uint16_t dh;
                     memcpy(&dh, srow + 34 * kb, 2);
                     out.scale[f * kTile + r] = dh;
-                    for (int g = 0; g < 4; ++g)   // lane r + 16 g holds q[8g .. 8g+8)
-                        memcpy(&out.a[(f * kWave + r + 16 * g) * 8], srow + 34 * kb + 2 + 8 * g, 8);
+                    for (int g = 0; g < 4; ++g)   // lane r + 16 g holds q[8g .. 8g+8) as q ^ 0x80
+                        for (int i = 0; i < 8; ++i)
+                            out.a[(f * kWave + r + 16 * g) * 8 + i] = srow[34 * kb + 2 + 8 * g + i] ^ 0x80;
                 }
             }
     } else {
@@ -978,29 +979,28 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
         p.bias_floats = rows * kTile;
     }
     const size_t lds_base = dec->lds_fixed + st_bytes + (size_t)p.bias_floats * 4;
-    // LDS partial slots.  K-major unit order (activation fragments reused
-    // across a workgroup's tiles) needs one slot per unit of the largest
-    // phase; item-major needs the most items of any phase plus one per wave.
-    // K-major whenever its slots fit.
+    // LDS partial slots: one per (item, K chunk) of a pass.  Every item of the
+    // largest phase in one pass when that fits; otherwise every slot the LDS
+    // holds, and the phase runs in several passes (at least one item each).
     {
         auto items = [&](const pkdev::TMat &m) { return (m.tiles + pl.P - 1) / pl.P; };
         auto units = [&](const pkdev::TMat &m) {
             const int kbe = m.type == PK_TYPE_F32 ? 2 * m.KB : m.KB;
             return (kbe + pkdev::unit_blocks(m.type) - 1) / pkdev::unit_blocks(m.type);
         };
-        int most = items(p.w_out), kslots = items(p.w_out) * units(p.w_out);
+        int kslots = items(p.w_out) * units(p.w_out), min_slots = units(p.w_out);
         for (int l = 0; l < p.L; ++l) {
             const pkdev::TMat &c = l + 1 < p.L ? p.w_ih[l + 1] : p.w_pred;
-            most = std::max(most, items(c) + items(p.w_hh[l]));
             kslots = std::max(kslots, (items(c) + items(p.w_hh[l])) * units(c));
+            min_slots = std::max(min_slots, units(c));
         }
-        p.kmajor = lds_base + (size_t)kslots * kWave * 16 <= dec->lds_bytes ? 1 : 0;
-        p.red_slots = p.kmajor ? kslots : most + kWaves;
+        const size_t fit = dec->lds_bytes > lds_base ? (dec->lds_bytes - lds_base) / (kWave * 16) : 0;
+        if ((int)fit < min_slots)
+            return fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed for %d workgroups per domain, %zu available",
+                        lds_base + (size_t)min_slots * kWave * 16, pl.P, dec->lds_bytes);
+        p.red_slots = std::min<int>(kslots, (int)fit);
     }
     size_t lds = lds_base + (size_t)p.red_slots * kWave * 16;
-    if (lds > dec->lds_bytes)
-        return fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed for %d workgroups per domain, %zu available", lds, pl.P,
-                    dec->lds_bytes);
     // LDS weight cache, phase by phase: the matrices of a phase (the two that
     // consume one layer's output, or W_o) are copied into LDS once per launch
     // when the workgroup's tiles of both fit; the LSTM phases are tried first

@@ -38,12 +38,18 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// A weight matrix [rows][K] laid out as MFMA A fragments: for row tile t and
+// A weight matrix [rows][K] laid out as MFMA fragments: for row tile t and
 // K block kb (32 columns), lane l holds the 8 consecutive weights of row
-// 16t + l%16 starting at column 32kb + 8(l/16).  q8_0: 8 int8 per lane plus
+// 16t + l%16 starting at column 32kb + 8(l/16).  q8_0: 8 bytes q ^ 0x80 per
+// lane (the int8 values offset by 128, so the conversion needs no xor) plus
 // the block scales d[16t + r][kb] (the stored f16 bits) at
 // scale[(t*KB + kb)*16 + r]; f16: 8 halves per lane; f32: two f16 planes
 // holding hi = f16(w), lo = f16(w - hi).
+//
+// Products are computed transposed: the staged activations are the MFMA A
+// operand (rows = utterances) and the weight fragment the B operand (columns =
+// weight rows), so a D fragment lane holds ONE weight row (l%16) for four
+// utterances (4(l/16) .. +3) and a q8_0 block needs one scale per lane.
 struct TMat {
     const void *a;                 // fragment plane
     const void *a_lo;              // f32 weights: low halves
@@ -108,8 +114,7 @@ struct KParams {
     int shards;                  // power of two <= kShards: ranks per shard ~ 8
     int *status;                 // [0] error code, [1] iterations, [2] overflow, [3] trace overflow
     int max_iter;
-    int red_slots;               // LDS partial slots (K-major: items x units per item of the largest phase)
-    int kmajor;                  // unit order of every phase: 1 K-major, 0 item-major
+    int red_slots;               // LDS partial slots: a phase runs in passes of red_slots / (units per item) items
     int st_n, st_k;              // LDS state of layers >= 1: utterance and owned-tile capacity
     int bias_floats;             // LDS bias table size (floats)
     int wcache_bytes;            // LDS weight cache per workgroup (0: weights are read from L2)
@@ -169,10 +174,10 @@ __device__ __forceinline__ void lds_sync() {
 
 // ---------------------------------------------------------------- MFMA tiles
 
-// 8 int8 (two dwords) -> 8 exact f16: byte q ^ 0x80 = q + 128 becomes the low
-// mantissa byte of 1024.0 (0x64xx), then 1152 is subtracted.
+// 8 int8 stored as q ^ 0x80 = q + 128 (two dwords) -> 8 exact f16: the byte
+// becomes the low mantissa byte of 1024.0 (0x64xx), then 1152 is subtracted.
 __device__ __forceinline__ half8 q8_to_half8(uint2 q) {
-    const unsigned x0 = q.x ^ 0x80808080u, x1 = q.y ^ 0x80808080u;
+    const unsigned x0 = q.x, x1 = q.y;
     const half2v off = {(_Float16)1152.0f, (_Float16)1152.0f};
     half2v p0 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u)) - off;
     half2v p1 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u)) - off;
@@ -184,6 +189,31 @@ __device__ __forceinline__ half8 q8_to_half8(uint2 q) {
 __device__ __forceinline__ void split_f16(float x, _Float16 &hi, _Float16 &lo) {
     hi = (_Float16)x;
     lo = (_Float16)(x - (float)hi);
+}
+
+// DPP quad permutation of a float: lane i of each quad reads quad lane perm_i.
+template <int CTRL>
+__device__ __forceinline__ float quad_perm(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// 4x4 transpose inside each quad of lanes: afterwards element j of quad lane p
+// is what element p of quad lane j was.  Two butterfly stages (partner p^1,
+// then p^2), each exchanging the two elements whose index bit differs from p's.
+__device__ __forceinline__ f32x4 quad_transpose(f32x4 a) {
+    const int p = threadIdx.x & 3;
+    {
+        const bool odd = p & 1;
+        const float r0 = quad_perm<0xB1>(odd ? a[0] : a[1]);   // quad_perm [1,0,3,2]
+        const float r1 = quad_perm<0xB1>(odd ? a[2] : a[3]);
+        if (odd) { a[0] = r0; a[2] = r1; } else { a[1] = r0; a[3] = r1; }
+    }
+    {
+        const bool hi = p & 2;
+        const float r0 = quad_perm<0x4E>(hi ? a[0] : a[2]);    // quad_perm [2,3,0,1]
+        const float r1 = quad_perm<0x4E>(hi ? a[1] : a[3]);
+        if (hi) { a[0] = r0; a[1] = r1; } else { a[2] = r0; a[3] = r1; }
+    }
+    return a;
 }
 
 // Staged activation block: 16 utterance rows of K values as f16 (hi, lo).
@@ -546,87 +576,23 @@ __device__ __forceinline__ void stage_act(const Act &x, int K, int n, __amdgpu_b
 // A phase multiplies weight row tiles ("items") by one staged 16-utterance
 // activation block.  Items 0 .. n_a-1 are tiles rank, rank+P, ... of matrix A,
 // items n_a .. n_items-1 the same of matrix B (same storage type and K).  Each
-// item's K blocks are cut into units of at most kUnitOf blocks (f32 weights count
-// every K block twice, once per f16 plane); the units are numbered item-major
-// and every wave takes a contiguous range of them.  A unit's fragments are
-// loaded with one batch of loads and multiplied by straight-line code, so
-// loads, LDS reads and MFMAs of different blocks overlap.  A wave keeps a running
-// partial while its units belong to one item and leaves one partial per
-// (item, wave) in LDS slot item + wave; phase_reduce sums each item's partials
-// in wave order -- a fixed order, so results do not depend on timing.
+// item's K blocks are cut into S units of kUnitOf blocks (f32 weights count
+// every K block twice, once per f16 plane).  Items are taken in passes of as
+// many items as the LDS partial slots hold.  Within a pass the units are
+// numbered K-major -- unit u = chunk * nj + item -- and every wave takes a
+// contiguous range of them, so a wave reads one chunk's activation fragments
+// from LDS once and reuses them from registers for every item of its range.
+// Each unit leaves one 16x16 partial in LDS slot (item - j0) * S + chunk; the
+// pass's reduce sums an item's partials in chunk order (a fixed order, so
+// results do not depend on timing) and runs the epilogue.  The weight
+// fragments of a wave's next unit are loaded before its current unit is
+// multiplied, so one unit's L2 latency hides behind the previous unit's
+// products.
 
 // K blocks per unit, by weight storage.  Measured: q8_0 5 (beats 4, 8 and 10 at B=1/64/256);
 // f16 and f32 4 (TDT-1.1b f16 at B=256: 49.9 vs 60.5 ms per launch with 5).
 template <bool Q8> constexpr int kUnitOf = Q8 ? 5 : 4;
 __host__ __device__ constexpr int unit_blocks(int type) { return type == PK_TYPE_Q8_0 ? 5 : 4; }
-
-// Fragments of one unit: blocks sb0 .. sb0+nb-1 of one tile; blocks past nb
-// read as zero (buffer loads past the range return 0).
-// The fields of a TMat that the unit loop reads, held in registers.
-struct WView {
-    const void *a, *a_lo;
-    const unsigned short *scale;
-    int tiles, KB, lds_off;
-};
-__device__ __forceinline__ WView wview(const TMat &m) { return WView{m.a, m.a_lo, m.scale, m.tiles, m.KB, m.lds_off}; }
-__device__ __forceinline__ WView pick(bool first, const WView &x, const WView &y) {
-    return WView{first ? x.a : y.a, first ? x.a_lo : y.a_lo, first ? x.scale : y.scale,
-                 first ? x.tiles : y.tiles, first ? x.KB : y.KB, first ? x.lds_off : y.lds_off};
-}
-
-template <bool Q8, bool CACHED>
-__device__ __forceinline__ void unit_load(const WView m, bool two, int tile, int li, const unsigned char *wc, int sb0,
-                                          int nb, int lane, uint4 (&f)[kUnitOf<Q8>]) {
-    const unsigned bad = 0x80000000u;
-    if (CACHED) {   // this workgroup's tiles are cached in LDS (local index li)
-        const unsigned char *base = wc + m.lds_off;
-#pragma unroll
-        for (int j = 0; j < kUnitOf<Q8>; ++j) {
-            const bool ok = j < nb;
-            const int sb = ok ? sb0 + j : sb0;
-            uint4 v;
-            if (Q8) {
-                const unsigned char *blk = base + ((size_t)li * m.KB + sb) * 544;
-                const uint2 q = *reinterpret_cast<const uint2 *>(blk + lane * 8);
-                const uint2 d = *reinterpret_cast<const uint2 *>(blk + 512 + (lane >> 4) * 8);
-                v = make_uint4(q.x, q.y, d.x, d.y);
-            } else {
-                const int kb = two ? sb >> 1 : sb;
-                const int plane = two ? (sb & 1) : 0;
-                v = *reinterpret_cast<const uint4 *>(base + (((size_t)li * m.KB + kb) * (two ? 2 : 1) + plane) * 1024 +
-                                                     lane * 16);
-            }
-            f[j] = ok ? v : make_uint4(0u, 0u, 0u, 0u);
-        }
-        return;
-    }
-    if (Q8) {
-        const __amdgpu_buffer_rsrc_t rq = rsrc(m.a, (unsigned)m.tiles * m.KB * kWave * 8u);
-        const __amdgpu_buffer_rsrc_t rs = rsrc(m.scale, (unsigned)m.tiles * m.KB * kTile * 2u);
-        const unsigned f0 = (unsigned)tile * m.KB + sb0;
-#pragma unroll
-        for (int j = 0; j < kUnitOf<Q8>; ++j) {
-            const bool ok = j < nb;
-            const unsigned oq = ok ? ((f0 + j) * kWave + lane) * 8u : bad;
-            const unsigned os = ok ? ((f0 + j) * kTile + (lane >> 4) * 4u) * 2u : bad;
-            const uint2 q = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, oq, 0, 0));
-            const uint2 d = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, os, 0, 0));
-            f[j] = make_uint4(q.x, q.y, d.x, d.y);
-        }
-    } else {
-        const unsigned bytes = (unsigned)m.tiles * m.KB * kWave * 16u;
-        const __amdgpu_buffer_rsrc_t rh = rsrc(m.a, bytes);
-        const __amdgpu_buffer_rsrc_t rl = rsrc(two ? m.a_lo : m.a, bytes);
-#pragma unroll
-        for (int j = 0; j < kUnitOf<Q8>; ++j) {
-            const int sb = sb0 + j;
-            const int kb = two ? sb >> 1 : sb;
-            const unsigned o = j < nb ? (((unsigned)tile * m.KB + kb) * kWave + lane) * 16u : bad;
-            f[j] = __builtin_bit_cast(uint4, (two && (sb & 1)) ? __builtin_amdgcn_raw_buffer_load_b128(rl, o, 0, 0)
-                                                               : __builtin_amdgcn_raw_buffer_load_b128(rh, o, 0, 0));
-        }
-    }
-}
 
 // One matrix's fragment sources for a phase: buffer descriptors (q8_0: the
 // quants and the block scales; f16: the plane twice; f32: the hi and lo
@@ -669,8 +635,8 @@ __device__ __forceinline__ void unit_load_src(const MatSrc &m, bool two, int til
             if (Q8) {
                 const unsigned char *blk = m.lds + ((size_t)li * m.KB + sb) * 544;
                 const uint2 q = *reinterpret_cast<const uint2 *>(blk + lane * 8);
-                const uint2 d = *reinterpret_cast<const uint2 *>(blk + 512 + (lane >> 4) * 8);
-                v = make_uint4(q.x, q.y, d.x, d.y);
+                const unsigned d = *reinterpret_cast<const unsigned short *>(blk + 512 + (lane & 15) * 2);
+                v = make_uint4(q.x, q.y, d, 0u);
             } else {
                 const int kb = two ? sb >> 1 : sb;
                 const int plane = two ? (sb & 1) : 0;
@@ -685,19 +651,19 @@ __device__ __forceinline__ void unit_load_src(const MatSrc &m, bool two, int til
         const int f0 = tile * m.KB + sb0;   // wave-uniform fragment index of block sb0
 #pragma unroll
         for (int j = 0; j < kUnitOf<Q8>; ++j) {
-            uint2 q, d;
+            uint2 q;
+            unsigned d;
             if (FULL) {
                 q = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(m.r0, lane * 8 + j * 512, f0 * 512, 0));
-                d = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(m.r1, (lane >> 4) * 8 + j * 32,
-                                                                                  f0 * 32, 0));
+                d = __builtin_amdgcn_raw_buffer_load_b16(m.r1, (lane & 15) * 2 + j * 32, f0 * 32, 0);
             } else {
                 const bool ok = j < nb;
                 const unsigned oq = ok ? (unsigned)((f0 + j) * kWave + lane) * 8u : kBad;
-                const unsigned os = ok ? (unsigned)((f0 + j) * kTile + (lane >> 4) * 4) * 2u : kBad;
+                const unsigned os = ok ? (unsigned)((f0 + j) * kTile + (lane & 15)) * 2u : kBad;
                 q = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(m.r0, oq, 0, 0));
-                d = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(m.r1, os, 0, 0));
+                d = __builtin_amdgcn_raw_buffer_load_b16(m.r1, os, 0, 0);
             }
-            f[j] = make_uint4(q.x, q.y, d.x, d.y);
+            f[j] = make_uint4(q.x, q.y, d, 0u);
         }
     } else {
 #pragma unroll
@@ -725,34 +691,41 @@ __device__ __forceinline__ void unit_act(const Act &x, int xo, bool two, int sb0
     }
 }
 
-// acc += (unit's weight blocks) . (activation blocks).  Zero blocks past nb
-// add nothing.
+// acc += (unit's weight blocks) . (activation blocks), transposed (lane: one
+// weight row, four utterances).  Zero blocks past nb add nothing.  q8_0: the
+// products of all blocks are issued first (independent MFMA pairs), then each
+// is scaled by its block's d; f16/f32: two independent accumulation chains (hi
+// and lo activations) added at the end.
 template <bool Q8>
 __device__ __forceinline__ f32x4 unit_mma(const uint4 (&f)[kUnitOf<Q8>], const half8 (&ah)[kUnitOf<Q8>],
                                           const half8 (&al)[kUnitOf<Q8>],
                                           bool two, int sb0, f32x4 acc) {
+    if (Q8) {
+        f32x4 p[kUnitOf<Q8>];
+#pragma unroll
+        for (int j = 0; j < kUnitOf<Q8>; ++j) {
+            const half8 w = q8_to_half8(make_uint2(f[j].x, f[j].y));
+            p[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j], w, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            p[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[j], w, p[j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < kUnitOf<Q8>; ++j) {
+            const float d = (float)__builtin_bit_cast(_Float16, (unsigned short)f[j].z);
+            acc += d * p[j];
+        }
+        return acc;
+    }
+    // f16 weights: hi and lo activations; f32 weights: the lo plane (odd
+    // sub-blocks) skips the lo activations (lo x lo is below f32 rounding)
+    f32x4 lo = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < kUnitOf<Q8>; ++j) {
-        const half8 bh = ah[j], bl = al[j];
-        if (Q8) {
-            const half8 w = q8_to_half8(make_uint2(f[j].x, f[j].y));
-            f32x4 p = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bh, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            p = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bl, p, 0, 0, 0);
-            const half2v d01 = __builtin_bit_cast(half2v, f[j].z), d23 = __builtin_bit_cast(half2v, f[j].w);
-            acc[0] = fmaf((float)d01[0], p[0], acc[0]);
-            acc[1] = fmaf((float)d01[1], p[1], acc[1]);
-            acc[2] = fmaf((float)d23[0], p[2], acc[2]);
-            acc[3] = fmaf((float)d23[1], p[3], acc[3]);
-        } else {
-            // f16 weights: hi and lo activations; f32 weights: the lo plane (odd
-            // sub-blocks) skips the lo activations (lo x lo is below f32 rounding)
-            const half8 w = __builtin_bit_cast(half8, f[j]);
-            const half8 b2 = (two && ((sb0 + j) & 1)) ? half8{} : bl;
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, bh, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(w, b2, acc, 0, 0, 0);
-        }
+        const half8 w = __builtin_bit_cast(half8, f[j]);
+        const half8 b2 = (two && ((sb0 + j) & 1)) ? half8{} : al[j];
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j], w, acc, 0, 0, 0);
+        lo = __builtin_amdgcn_mfma_f32_16x16x32_f16(b2, w, lo, 0, 0, 0);
     }
-    return acc;
+    return acc + lo;
 }
 
 // Wave w's unit range [c0, c1) of N units.
@@ -760,8 +733,9 @@ __device__ __forceinline__ int wave_cut(int N, int w) { return (int)(((long long
 
 __device__ __forceinline__ int blocks_per_item(const TMat &m) { return m.type == PK_TYPE_F32 ? 2 * m.KB : m.KB; }
 
-template <bool Q8, bool CACHED, bool KMAJ, bool FULL>
-__device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
+// Partials of items j0 .. j1-1 (one pass), K-major, next unit's weights prefetched.
+template <bool Q8, bool CACHED, bool FULL>
+__device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMat &Bm, int j0, int j1, int rank, int P,
                                                const Act &x, f32x4 *red, const unsigned char *wc) {
     // wave-uniform unit bookkeeping: the weight buffer descriptors stay in SGPRs
     const int lane = threadIdx.x & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -769,121 +743,98 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
     const int KBe = two ? 2 * A.KB : A.KB;
     constexpr int U = kUnitOf<Q8>;
     const int S = (KBe + U - 1) / U;                  // units per item
-    const int N = n_items * S;
+    const int nj = j1 - j0, N = nj * S;
     const int c0 = wave_cut(N, wave), c1 = wave_cut(N, wave + 1);
     if (c0 >= c1) return;
-    // Column c of the product depends only on column c of the activations;
-    // rows past x.n are not staged (they hold older values) and the columns
-    // they feed are never read.
+    // Column c of the product depends only on row c of the activations; rows
+    // past x.n are not staged (they hold older values) and the columns they
+    // feed are never read.
     const int xo = (lane & 15) * x.kp + (lane >> 4) * 8;
+    const MatSrc sA = mat_src<Q8, CACHED>(A, two, wc), sB = mat_src<Q8, CACHED>(Bm, two, wc);
+    auto load = [&](int item, int c, uint4 (&f)[U]) {
+        const bool in_a = item < n_a;
+        const int li = in_a ? item : item - n_a;
+        const int sb0 = c * U;
+        unit_load_src<Q8, CACHED, FULL>(in_a ? sA : sB, two, rank + li * P, li, sb0, min(U, KBe - sb0), lane, f);
+    };
     half8 ah[U], al[U];
-    if (KMAJ) {
-        // unit u = c * n_items + item: a wave's range runs over items at one K
-        // chunk c, so its activation fragments are read once per chunk; one
-        // partial per unit, in slot item * S + c.  Per chunk the wave's items
-        // of A come first, then those of B, each with its matrix's sources
-        // fixed for the whole loop.
-        const MatSrc sA = mat_src<Q8, CACHED>(A, two, wc), sB = mat_src<Q8, CACHED>(Bm, two, wc);
-        for (int u = c0; u < c1;) {
-            const int c = u / n_items, i0 = u - c * n_items, i1 = min(n_items, i0 + (c1 - u));
-            const int sb0 = c * U, nb = min(U, KBe - sb0);
-            unit_act(x, xo, two, sb0, nb, ah, al);
-            for (int item = i0; item < min(i1, n_a); ++item) {
-                uint4 f[U];
-                unit_load_src<Q8, CACHED, FULL>(sA, two, rank + item * P, item, sb0, nb, lane, f);
-                red[(item * S + c) * kWave + lane] = unit_mma<Q8>(f, ah, al, two, sb0, f32x4{0.f, 0.f, 0.f, 0.f});
-            }
-            for (int item = max(i0, n_a); item < i1; ++item) {
-                const int li = item - n_a;
-                uint4 f[U];
-                unit_load_src<Q8, CACHED, FULL>(sB, two, rank + li * P, li, sb0, nb, lane, f);
-                red[(item * S + c) * kWave + lane] = unit_mma<Q8>(f, ah, al, two, sb0, f32x4{0.f, 0.f, 0.f, 0.f});
-            }
-            u += i1 - i0;
+    uint4 fa[U], fb[U];
+    int u = c0, c = u / nj, i = u - c * nj, cur = -1;
+    load(j0 + i, c, fa);
+    // one unit: issue the next unit's loads into fn, then multiply fc
+    auto step = [&](uint4 (&fc)[U], uint4 (&fn)[U]) {
+        int nc = c, ni = i + 1;
+        if (ni == nj) {
+            ni = 0;
+            ++nc;
         }
-    } else {
-        // the two matrices' descriptors, read once (not per unit from the kernel arguments)
-        const WView vA = wview(A), vB = wview(Bm);
-        // unit u = item * S + c: a wave keeps one running partial per item, in
-        // slot item + wave
-        int item = c0 / S, c = c0 - item * S;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int u = c0; u < c1; ++u) {
-            const int sb0 = c * U, nb = min(U, KBe - sb0);
-            const bool in_a = item < n_a;
-            const int li = in_a ? item : item - n_a;
-            uint4 f[U];
-            unit_load<Q8, CACHED>(pick(in_a, vA, vB), two, rank + li * P, li, wc, sb0, nb, lane, f);
-            unit_act(x, xo, two, sb0, nb, ah, al);
-            acc = unit_mma<Q8>(f, ah, al, two, sb0, acc);
-            if (++c == S || u + 1 == c1) {   // this item's last unit in this wave
-                red[(item + wave) * kWave + lane] = acc;
-                acc = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
-            if (c == S) {
-                c = 0;
-                ++item;
-            }
+        if (u + 1 < c1) load(j0 + ni, nc, fn);
+        const int sb0 = c * U;
+        if (c != cur) {
+            unit_act(x, xo, two, sb0, min(U, KBe - sb0), ah, al);
+            cur = c;
         }
+        red[(i * S + c) * kWave + lane] = unit_mma<Q8>(fc, ah, al, two, sb0, f32x4{0.f, 0.f, 0.f, 0.f});
+        ++u;
+        c = nc;
+        i = ni;
+    };
+    while (true) {
+        step(fa, fb);
+        if (u >= c1) break;
+        step(fb, fa);
+        if (u >= c1) break;
     }
     TL(2);
 }
 
-// Sum each item's partials (K-major: in K order; item-major: in wave order)
-// and run epi(item, acc); items are dealt round robin over the waves.  Opens
-// with a barrier (all partials written); the caller's next barrier (before any
-// new partials or staging) closes it.
-template <bool KMAJ, class EpiFn>
-__device__ __forceinline__ void phase_reduce(int n_items, int S, const f32x4 *red, EpiFn epi) {
+// Sum each item's partials of one pass in chunk order and run epi(item, acc);
+// items are dealt round robin over the waves.  Opens with a barrier (all
+// partials written); the caller's next barrier (before any new partials or
+// staging) closes it.
+template <class EpiFn>
+__device__ __forceinline__ void phase_reduce(int j0, int j1, int S, const f32x4 *red, EpiFn epi) {
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int N = n_items * S;
     lds_sync();
     TL(3);
-    for (int it = wave; it < n_items; it += kWaves) {
+    for (int it = j0 + wave; it < j1; it += kWaves) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        if (KMAJ) {
-            for (int c = 0; c < S; ++c) acc += red[(it * S + c) * kWave + lane];
-        } else {
-            for (int w = 0; w < kWaves; ++w) {
-                const int a0 = wave_cut(N, w), a1 = wave_cut(N, w + 1);
-                if (a0 < a1 && a0 < (it + 1) * S && a1 > it * S) acc += red[(it + w) * kWave + lane];
-            }
-        }
+        for (int c = 0; c < S; ++c) acc += red[((it - j0) * S + c) * kWave + lane];
         epi(it, acc);
     }
     TL(4);
 }
 
-// Products of one phase for this workgroup, then the epilogue per item.
-template <bool KMAJ, class EpiFn>
-__device__ __forceinline__ void run_phase_(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
-                                           const Act &x, f32x4 *red, const unsigned char *wc, EpiFn epi) {
+// Products of one phase for this workgroup, then the epilogue per item, in
+// passes of at most red_slots / S items.
+template <class EpiFn>
+__device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
+                                          const Act &x, f32x4 *red, const unsigned char *wc, int red_slots, EpiFn epi) {
+    if (n_items <= 0) return;
     // both matrices of a phase are in the LDS weight cache or neither
     const bool cached = wc != nullptr && A.lds_off >= 0;
     const int KBe = A.type == PK_TYPE_F32 ? 2 * A.KB : A.KB;
-    // K-major with K a whole number of units: the unmasked unit loads
     const int U = unit_blocks(A.type);
-    const bool full = KMAJ && KBe % U == 0;
-    if (A.type == PK_TYPE_Q8_0) {
-        if (cached) {
-            if (full) phase_partials<true, true, KMAJ, true>(A, n_a, Bm, n_items, rank, P, x, red, wc);
-            else phase_partials<true, true, KMAJ, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+    const int S = (KBe + U - 1) / U;
+    const bool full = KBe % U == 0;   // whole units: unmasked unit loads
+    const int batch = red_slots / S;
+    for (int j0 = 0; j0 < n_items; j0 += batch) {
+        const int j1 = min(n_items, j0 + batch);
+        if (j0 > 0) lds_sync();   // the previous pass's reduce has read its slots
+        if (A.type == PK_TYPE_Q8_0) {
+            if (cached) {
+                if (full) phase_partials<true, true, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
+                else phase_partials<true, true, false>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
+            } else {
+                if (full) phase_partials<true, false, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
+                else phase_partials<true, false, false>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
+            }
         } else {
-            if (full) phase_partials<true, false, KMAJ, true>(A, n_a, Bm, n_items, rank, P, x, red, wc);
-            else phase_partials<true, false, KMAJ, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+            if (cached) phase_partials<false, true, false>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
+            else phase_partials<false, false, false>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
         }
-    } else {
-        if (cached) phase_partials<false, true, KMAJ, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
-        else phase_partials<false, false, KMAJ, false>(A, n_a, Bm, n_items, rank, P, x, red, wc);
+        phase_reduce(j0, j1, S, red, epi);
     }
-    phase_reduce<KMAJ>(n_items, (KBe + U - 1) / U, red, epi);
-}
-template <class EpiFn>
-__device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
-                                          const Act &x, f32x4 *red, const unsigned char *wc, bool kmajor, EpiFn epi) {
-    if (n_items <= 0) return;
-    if (kmajor) run_phase_<true>(A, n_a, Bm, n_items, rank, P, x, red, wc, epi);
-    else run_phase_<false>(A, n_a, Bm, n_items, rank, P, x, red, wc, epi);
 }
 
 // Tiles of a matrix with `tiles` row tiles owned by rank r of P: t = r, r+P, ...
@@ -901,7 +852,7 @@ struct Lds {
     Act act[1 + PK_MAX_LAYERS];   // staged activation blocks
     float *st;                    // [L-1][st_n][st_k][kStFloats] LDS state of layers >= 1
     float *bias;                  // epilogue bias rows of this workgroup's tiles (see bias_table)
-    f32x4 *red;                   // [red_slots][kWave] per-(item, wave) partials
+    f32x4 *red;                   // [red_slots][kWave] per-(item, chunk) partials of one pass
     const unsigned char *wcache;  // weight cache (nullptr when the tiles do not fit)
 };
 
@@ -1017,8 +968,10 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         lds_sync();
         TL(0);
         pmark(p, s, tlast, kPrJStage);
-        // the blank offset of this lane's utterance, loaded before the products
-        const int u = lane & 15;
+        // after the epilogue's quad transpose (see quad_transpose) a lane holds
+        // rows 4g .. 4g+3 of a tile for utterance u of the column tile; its blank
+        // offset is loaded before the products
+        const int u = 4 * (lane >> 4) + (lane & 3), g = (lane >> 2) & 3;
         const float bb = u < nc ? s.bbias[s.jst[c0 + u]] : 0.0f;
         // (b_out is zero-padded to whole tiles)
         const float *btab = S.bias + bias_base(p, s.rank, s.P, p.L);
@@ -1029,17 +982,19 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
             const int ul = s.jst[c0 + u], step = s.steps[ul];
             if (step < p.logit_steps) ltap = p.logits + ((size_t)s.b[ul] * p.logit_steps + step) * p.Vo;
         }
-        // each lane keeps its best key per head over all its rows; lanes of one
-        // column then combine, and one LDS atomic per column and head follows
+        // each lane keeps its best key per head over all its rows; the four
+        // lanes of one utterance then combine, and one LDS atomic per utterance
+        // and head follows
         unsigned long long best0 = 0ull, best1 = 0ull;
-        run_phase(p.w_out, n_out, p.w_out, n_out, s.rank, s.P, x, S.red, S.wcache, p.kmajor != 0,
+        run_phase(p.w_out, n_out, p.w_out, n_out, s.rank, s.P, x, S.red, S.wcache, p.red_slots,
                   [&](int k, f32x4 acc) {
+                      acc = quad_transpose(acc);   // every lane of the wave takes part
                       if (u >= nc) return;
                       const int tile = s.rank + k * s.P;
-                      const float4 bias4 = *reinterpret_cast<const float4 *>(btab + k * kTile + (lane >> 4) * 4);
+                      const float4 bias4 = *reinterpret_cast<const float4 *>(btab + k * kTile + g * 4);
 #pragma unroll
                       for (int i = 0; i < 4; ++i) {
-                          const int row = tile * kTile + (lane >> 4) * 4 + i;
+                          const int row = tile * kTile + g * 4 + i;
                           if (row >= p.Vo) continue;
                           const float bias = i == 0 ? bias4.x : i == 1 ? bias4.y : i == 2 ? bias4.z : bias4.w;
                           float v = acc[i] + bias;
@@ -1055,12 +1010,12 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
                       }
                   });
 #pragma unroll
-        for (int m = 16; m < kWave; m <<= 1) {
+        for (int m = 4; m < kTile; m <<= 1) {   // the lanes of utterance u differ in bits 2 and 3
             const unsigned long long o0 = __shfl_xor(best0, m, kWave), o1 = __shfl_xor(best1, m, kWave);
             best0 = o0 > best0 ? o0 : best0;
             best1 = o1 > best1 ? o1 : best1;
         }
-        if (lane < 16 && u < nc) {
+        if (g == 0 && u < nc) {
             if (best0) atomicMax(&s.wgkey[c0 + u][0], best0);
             if (best1) atomicMax(&s.wgkey[c0 + u][1], best1);
         }
@@ -1153,7 +1108,10 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
     const TMat &wc = last ? p.w_pred : p.w_ih[lc + 1];
     const TMat &wr = p.w_hh[lc];
     const int n_c = owned(wc.tiles, s.rank, s.P), n_r = owned(wr.tiles, s.rank, s.P);
-    const int layer = lc + 1, u = lane & 15, g = lane >> 4;
+    // the epilogue quad-transposes the (transposed) D fragment, after which a
+    // lane holds rows 4g .. 4g+3 of a tile (the four gates of one unit, or four
+    // pred rows) for one utterance u of the column tile
+    const int layer = lc + 1, u = 4 * (lane >> 4) + (lane & 3), g = (lane >> 2) & 3;
     // this lane's utterance (a valid index for every lane; lanes u >= nc store nothing)
     const int ul = s.lst[c0 + min(u, nc - 1)], b = s.b[ul], cur = s.cur[ul];
     const bool zero = s.flags[ul] & kFlagZeroHC;
@@ -1161,8 +1119,9 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
     // the pred rows, or the four gates of unit j = row0 / 4
     const float *btab = S.bias + bias_base(p, s.rank, s.P, layer - 1);
     TL(1);
-    run_phase(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache, p.kmajor != 0,
+    run_phase(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache, p.red_slots,
               [&](int it, f32x4 acc) {
+                  acc = quad_transpose(acc);   // every lane of the wave takes part
                   if (u >= nc) return;
                   if (it >= n_c) {          // recurrent product for the next step
                       const int k = it - n_c;
