@@ -1,18 +1,21 @@
-// parakeet_decoder.h -- C++ transducer decoder API, shaped like parakeet.cpp's
-// (src/parakeet_tdt.h, src/parakeet_eou.h, include/parakeet/engine.h), running
-// on the MI355X kernels of libparakeet_hip.so through the C ABI in
-// parakeet_hip.h.
+// parakeet_decoder.h -- standalone C++ transducer decoder API of the MI355X
+// build, shaped like parakeet.cpp's (src/parakeet_tdt.h, src/parakeet_eou.h,
+// include/parakeet/engine.h) and running on the kernels of libparakeet_hip.so
+// through the C ABI in parakeet_hip.h.
 //
-// Same names, argument meanings and status codes as the reference, so the
-// Engine call sites (src/parakeet_engine.cpp:273-297, 409-452, 808-838) keep
-// their shape.  Differences, all on purpose:
-//   - the model is decoder-only: load_from_gguf reads the prediction / joint
-//     tensors and the metadata; encoder tensors are not required;
-//   - decode state lives in a device slot of the runtime (the reference's GPU
-//     path also keeps h/c/pred on the device, src/parakeet_tdt.cpp:845-847, but
-//     shared per runtime; here every TdtDecodeState / EouDecodeState owns its
-//     own slot, which is the reference CPU path's semantics).  The host vectors
-//     h_state / c_state / pred_out stay empty, as on the reference GPU path;
+// Everything here lives in namespace parakeet_hip, so it can sit beside the
+// reference's own headers.  The model is decoder-only (DecoderModel): the
+// loader reads the prediction / joint tensors and the metadata of a GGUF, no
+// encoder tensors.  A caller that keeps parakeet.cpp's own model and Engine
+// uses the drop-in decoder headers in include/dropin/ instead, which declare
+// the reference's decoder functions against its ParakeetCtcModel.
+//
+// Same names, argument meanings and status codes as the reference otherwise.
+// Differences, all on purpose:
+//   - decode state lives in a device slot of the runtime; every TdtDecodeState
+//     / EouDecodeState holds its own (a copy leases a new slot and copies the
+//     state, see parakeet_slot.h).  The host vectors h_state / c_state /
+//     pred_out stay empty, as on the reference GPU path;
 //   - *_decode_batch entry points decode many utterances in one lockstep launch.
 #pragma once
 
@@ -22,9 +25,9 @@
 #include <string>
 #include <vector>
 
-struct pk_decoder;
+#include "parakeet_slot.h"
 
-namespace parakeet {
+namespace parakeet_hip {
 
 enum class ParakeetModelType { CTC, TDT, EOU, SORTFORMER };
 
@@ -50,7 +53,9 @@ struct MelConfig {
     int hop_length = 160;
 };
 
-struct ParakeetCtcModel {
+// The decoder half of a parakeet GGUF: metadata, vocabulary and the tensor
+// directory (the file's bytes stay mapped in impl).
+struct DecoderModel {
     ParakeetModelType model_type = ParakeetModelType::CTC;
     EncoderConfig encoder_cfg;
     MelConfig mel_cfg;
@@ -64,21 +69,18 @@ struct ParakeetCtcModel {
     struct Impl;
     std::shared_ptr<Impl> impl;   // GGUF bytes + tensor directory
 };
-using ParakeetModel = ParakeetCtcModel;
 
 // src/parakeet_ctc.cpp:297.  Returns 0, or the reference's codes: 1 open
 // failure, 2 wrong architecture / missing decoder tensor.
-int load_from_gguf(const std::string &gguf_path, ParakeetCtcModel &out_model, int n_threads = 0,
+int load_from_gguf(const std::string &gguf_path, DecoderModel &out_model, int n_threads = 0,
                    int n_gpu_layers = 1, bool verbose = false);
-
-namespace detail { struct SlotPool; struct SlotLease; }
 
 // ---- TDT (src/parakeet_tdt.h) ----
 
 struct TdtRuntimeWeights {
     int H_pred = 640, H_joint = 640, D_enc = 1024, V_plus_1 = 8193, V_out = 8198, L = 2, num_durations = 5;
-    const ParakeetCtcModel *weights_model = nullptr;
-    std::shared_ptr<detail::SlotPool> pool;   // device decoder + state slots
+    const DecoderModel *weights_model = nullptr;
+    std::shared_ptr<SlotPool> pool;   // device decoder + state slots
     bool ready() const { return pool != nullptr; }
 };
 
@@ -100,19 +102,19 @@ struct TdtDecodeState {
     int symbols_this_step = 0;    // mirrored from the device after every window
     bool initialized = false;
     int carry_frames = 0;
-    std::shared_ptr<detail::SlotLease> slot;
+    SlotHandle slot;               // the device slot holding h, c, pred and the control words
 };
 
 // n_slots: concurrent decode states the runtime can hold (default 1024).
-int tdt_prepare_runtime(const ParakeetCtcModel &model, TdtRuntimeWeights &out, int n_slots = 1024);
+int tdt_prepare_runtime(const DecoderModel &model, TdtRuntimeWeights &out, int n_slots = 1024);
 void tdt_init_state(TdtRuntimeWeights &W, int blank_id, TdtDecodeState &state);
-int tdt_decode_window(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const float *encoder_out_window,
+int tdt_decode_window(const DecoderModel &model, TdtRuntimeWeights &W, const float *encoder_out_window,
                       int n_frames, int D_enc, const TdtDecodeOptions &opts, TdtDecodeState &state,
                       std::vector<int32_t> &out_tokens, int &out_steps);
-int tdt_greedy_decode(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const float *encoder_out, int T_enc,
+int tdt_greedy_decode(const DecoderModel &model, TdtRuntimeWeights &W, const float *encoder_out, int T_enc,
                       int D_enc, const TdtDecodeOptions &opts, TdtDecodeResult &result);
 // Batched: utterance u decodes enc[u][0 .. n_frames[u]) with states[u].
-int tdt_decode_batch(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const std::vector<const float *> &enc,
+int tdt_decode_batch(const DecoderModel &model, TdtRuntimeWeights &W, const std::vector<const float *> &enc,
                      const std::vector<int> &n_frames, int D_enc, const TdtDecodeOptions &opts,
                      const std::vector<TdtDecodeState *> &states, std::vector<std::vector<int32_t>> &out_tokens,
                      std::vector<int> &out_steps);
@@ -122,7 +124,7 @@ int tdt_decode_batch(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const 
 struct EouRuntimeWeights {
     int H_pred = 640, H_joint = 640, D_enc = 512, V_plus_1 = 1027, L = 1;
     int blank_id = 1026, eou_id = 1024, eob_id = 1025;
-    std::shared_ptr<detail::SlotPool> pool;
+    std::shared_ptr<SlotPool> pool;
 };
 
 struct EouDecodeOptions {
@@ -135,7 +137,7 @@ struct EouDecodeState {
     int symbols_this_step = 0;
     bool initialized = false;
     int segment_start_token = 0;
-    std::shared_ptr<detail::SlotLease> slot;
+    SlotHandle slot;               // the device slot holding h, c, pred and the control words
 };
 
 struct EouSegmentBoundary {
@@ -152,15 +154,15 @@ struct EouDecodeResult {
     double decode_ms = 0.0;
 };
 
-int eou_prepare_runtime(const ParakeetCtcModel &model, EouRuntimeWeights &out, int n_slots = 1024);
+int eou_prepare_runtime(const DecoderModel &model, EouRuntimeWeights &out, int n_slots = 1024);
 void eou_init_state(const EouRuntimeWeights &W, EouDecodeState &state);
-int eou_decode_window(const ParakeetCtcModel &model, const EouRuntimeWeights &W, const float *encoder_out_window,
+int eou_decode_window(const DecoderModel &model, const EouRuntimeWeights &W, const float *encoder_out_window,
                       int n_frames, int D_enc, const EouDecodeOptions &opts, EouDecodeState &state,
                       std::vector<int32_t> &out_tokens, std::vector<EouSegmentBoundary> &out_segments,
                       int &out_steps);
-int eou_greedy_decode(const ParakeetCtcModel &model, const EouRuntimeWeights &W, const float *encoder_out,
+int eou_greedy_decode(const DecoderModel &model, const EouRuntimeWeights &W, const float *encoder_out,
                       int T_enc, int D_enc, const EouDecodeOptions &opts, EouDecodeResult &result);
-int eou_decode_batch(const ParakeetCtcModel &model, const EouRuntimeWeights &W, const std::vector<const float *> &enc,
+int eou_decode_batch(const DecoderModel &model, const EouRuntimeWeights &W, const std::vector<const float *> &enc,
                      const std::vector<int> &n_frames, int D_enc, const EouDecodeOptions &opts,
                      const std::vector<EouDecodeState *> &states, std::vector<std::vector<int32_t>> &out_tokens,
                      std::vector<std::vector<EouSegmentBoundary>> &out_segments, std::vector<int> &out_steps);
@@ -181,11 +183,11 @@ struct DeviceEncoderOutput {
     int64_t n_rows = 0;
     int d_model = 0;
 };
-int tdt_decode_batch_device(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const DeviceEncoderOutput &enc,
+int tdt_decode_batch_device(const DecoderModel &model, TdtRuntimeWeights &W, const DeviceEncoderOutput &enc,
                             const std::vector<int64_t> &row_offset, const std::vector<int> &n_frames,
                             const TdtDecodeOptions &opts, const std::vector<TdtDecodeState *> &states,
                             std::vector<std::vector<int32_t>> &out_tokens, std::vector<int> &out_steps);
-int eou_decode_batch_device(const ParakeetCtcModel &model, const EouRuntimeWeights &W, const DeviceEncoderOutput &enc,
+int eou_decode_batch_device(const DecoderModel &model, const EouRuntimeWeights &W, const DeviceEncoderOutput &enc,
                             const std::vector<int64_t> &row_offset, const std::vector<int> &n_frames,
                             const EouDecodeOptions &opts, const std::vector<EouDecodeState *> &states,
                             std::vector<std::vector<int32_t>> &out_tokens,
@@ -278,7 +280,7 @@ private:
 
 // Encoder frame stride in ms: 1000 * hop_length * subsampling / sample_rate
 // (src/parakeet_engine.cpp:35-41).
-double encoder_frame_stride_ms(const ParakeetCtcModel &model);
+double encoder_frame_stride_ms(const DecoderModel &model);
 
 // ---- Engine-shaped front (include/parakeet/engine.h) over encoder features ----
 
@@ -315,11 +317,11 @@ public:
     // The decode half of Engine::stream_start (src/parakeet_engine.cpp:1013-1059).
     std::unique_ptr<FeatureStreamSession> stream_start(const FeatureStreamOptions &opts,
                                                        StreamingCallback on_segment);
-    const ParakeetCtcModel &model() const;
+    const DecoderModel &model() const;
     struct Impl;
 
 private:
     std::unique_ptr<Impl> pimpl_;
 };
 
-}  // namespace parakeet
+}  // namespace parakeet_hip

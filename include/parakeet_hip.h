@@ -136,6 +136,14 @@ typedef struct pk_batch {
      * only; a timed call passes NULL. */
     float *logits;
     int32_t logit_steps;
+    /* [n_utts], nullable: 1 = start utterance u from a fresh state (zero h, c, one
+     * LSTM step on embed[blank], counters reset -- what tdt_init_state /
+     * eou_init_state do, src/parakeet_tdt.cpp:813-863) whatever its slot holds;
+     * the initial step runs inside the same launch. */
+    const uint8_t *reset;
+    /* out [n_utts][PK_CTRL_N], nullable: each utterance's slot control words after
+     * the call (as pk_slot_read returns them), copied back with the other outputs. */
+    int32_t *ctrl_out;
 } pk_batch;
 
 /* Slot control words (pk_slot_read ctrl[]): */
@@ -153,6 +161,10 @@ PK_API int pk_slot_reset(pk_decoder *dec, int32_t slot);
 /* Copy a slot's state to host arrays (each nullable): h, c [L*H], pred [H],
  * ctrl [PK_CTRL_N]. */
 PK_API int pk_slot_read(pk_decoder *dec, int32_t slot, float *h, float *c, float *pred, int32_t *ctrl);
+/* Copy the whole state of slot src into slot dst (device to device): a copy of a
+ * TdtDecodeState / EouDecodeState value (src/parakeet_tdt.h:175-183) that then
+ * decodes independently of the original. */
+PK_API int pk_slot_copy(pk_decoder *dec, int32_t src, int32_t dst);
 /* Decode one window for every utterance of the batch. */
 PK_API int pk_decode(pk_decoder *dec, const pk_batch *batch);
 /* pk_decode without any device allocation.  No counterpart in the reference:

@@ -5,6 +5,9 @@
   libpk_calib.so          copy kernel of known size (csrc/pk_calib.hip), used by bench.py to scale
                           hardware byte counters
   tests/cpp/decoder_api_main  test driver of the C++ API (tests/cpp/decoder_api_main.cpp)
+  tests/cpp/dropin_main   test driver of the drop-in decoder headers (tests/cpp/dropin_main.cpp), built
+                          only where parakeet.cpp's sources are present: it compiles against the
+                          reference's own src/parakeet_ctc.h (headers only, no ggml)
 
 Called by __graft_entry__.build(); every call recompiles.
 """
@@ -17,6 +20,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INC = os.path.join(ROOT, "include")
+REFERENCE_SRC = os.path.join(os.environ.get("PK_REFERENCE", "/root/reference"), "src")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -49,7 +53,7 @@ def build_calib():
 
 
 def build_decoder():
-    srcs = [os.path.join(CSRC, f) for f in ("parakeet_decoder.cpp", "gguf_reader.cpp")]
+    srcs = [os.path.join(CSRC, f) for f in ("parakeet_decoder.cpp", "decoder_core.cpp", "gguf_reader.cpp")]
     if not all(os.path.exists(s) for s in srcs):
         return None
     out = os.path.join(HERE, "libparakeet_decoder.so")
@@ -73,9 +77,26 @@ def build_api_test(name="decoder_api_main", hip=False):
     return out
 
 
+def build_dropin_test():
+    """tests/cpp/dropin_main: include/dropin/ + csrc/dropin/parakeet_dropin.cpp compiled against
+    parakeet.cpp's src/parakeet_ctc.h, the drop-in headers first on the include path (as in
+    parakeet.cpp's build, where they replace src/parakeet_tdt.h and src/parakeet_eou.h)."""
+    if not os.path.exists(os.path.join(REFERENCE_SRC, "parakeet_ctc.h")):
+        return None
+    src = os.path.join(ROOT, "tests", "cpp", "dropin_main.cpp")
+    out = os.path.join(ROOT, "tests", "cpp", "dropin_main")
+    srcs = [src, os.path.join(CSRC, "dropin", "parakeet_dropin.cpp"), os.path.join(CSRC, "decoder_core.cpp"),
+            os.path.join(CSRC, "gguf_reader.cpp")]
+    _run(["g++", "-O2", "-std=c++17", "-Wall", f"-I{os.path.join(INC, 'dropin')}", f"-I{INC}", f"-I{CSRC}",
+          f"-I{os.path.join(CSRC, 'dropin')}", f"-I{REFERENCE_SRC}", *srcs, f"-L{HERE}", "-lparakeet_hip",
+          "-Wl,-rpath,$ORIGIN/../../parakeet.cpp_amd", "-o", out + ".tmp"])
+    os.replace(out + ".tmp", out)
+    return out
+
+
 def build_all():
     return [build_hip(), build_decoder(), build_calib(), build_api_test("decoder_api_main", hip=True),
-            build_api_test("loader_main")]
+            build_api_test("loader_main"), build_dropin_test()]
 
 
 if __name__ == "__main__":

@@ -5,7 +5,7 @@
 #include <cstring>
 #include <fstream>
 
-namespace parakeet {
+namespace parakeet_hip {
 namespace gguf {
 
 namespace {
@@ -181,4 +181,4 @@ std::string File::get_str(const std::string &key, const std::string &def) const 
 }
 
 }  // namespace gguf
-}  // namespace parakeet
+}  // namespace parakeet_hip

@@ -12,7 +12,7 @@
 #include <string>
 #include <vector>
 
-namespace parakeet {
+namespace parakeet_hip {
 namespace gguf {
 
 struct Value {
@@ -55,4 +55,4 @@ private:
 uint64_t tensor_nbytes(uint32_t type, int64_t n_elements);
 
 }  // namespace gguf
-}  // namespace parakeet
+}  // namespace parakeet_hip

@@ -1,5 +1,5 @@
-// parakeet_decoder.cpp -- the reference-shaped C++ decoder API on top of the
-// C ABI (parakeet_hip.h).  See include/parakeet_decoder.h.
+// parakeet_decoder.cpp -- the standalone reference-shaped C++ decoder API on
+// top of the C ABI (parakeet_hip.h).  See include/parakeet_decoder.h.
 #include "parakeet_decoder.h"
 
 #include <algorithm>
@@ -10,50 +10,24 @@
 #include <mutex>
 #include <stdexcept>
 
+#include "decoder_core.h"
 #include "gguf_reader.h"
 #include "parakeet_hip.h"
 
-namespace parakeet {
+namespace parakeet_hip {
 
-struct ParakeetCtcModel::Impl {
+struct DecoderModel::Impl {
     gguf::File file;
 };
 
-namespace detail {
-
-// The device decoder of one runtime and its pool of state slots.
-struct SlotPool {
-    pk_decoder *dec = nullptr;
-    std::mutex mu;
-    std::vector<int> free_slots;
-    ~SlotPool() { if (dec) pk_decoder_destroy(dec); }
-    int acquire() {
-        std::lock_guard<std::mutex> lk(mu);
-        if (free_slots.empty()) return -1;
-        const int s = free_slots.back();
-        free_slots.pop_back();
-        return s;
-    }
-    void release(int s) {
-        std::lock_guard<std::mutex> lk(mu);
-        free_slots.push_back(s);
-    }
-};
-
-// A state's claim on one slot, returned to the pool when the state goes away.
-struct SlotLease {
-    std::shared_ptr<SlotPool> pool;
-    int slot = -1;
-    ~SlotLease() { if (pool && slot >= 0) pool->release(slot); }
-};
-
-}  // namespace detail
-
 namespace {
+
+using core::BatchOut;
+using core::Frames;
 
 const char *prefix(ParakeetModelType t) { return t == ParakeetModelType::EOU ? "eou." : "tdt."; }
 
-pk_tensor tensor_of(const ParakeetCtcModel &m, const std::string &name) {
+pk_tensor tensor_of(const DecoderModel &m, const std::string &name) {
     pk_tensor t{};
     const gguf::Tensor *g = m.impl ? m.impl->file.tensor(name) : nullptr;
     if (!g) return t;
@@ -66,7 +40,7 @@ pk_tensor tensor_of(const ParakeetCtcModel &m, const std::string &name) {
 
 // Decoder description from the loaded model (the tensors bound at
 // src/parakeet_ctc.cpp:603-665 and the metadata read at :418-458).
-int make_pool(const ParakeetCtcModel &m, int n_slots, std::shared_ptr<detail::SlotPool> &out) {
+int make_pool(const DecoderModel &m, int n_slots, std::shared_ptr<SlotPool> &out) {
     pk_decoder_desc d{};
     const bool eou = m.model_type == ParakeetModelType::EOU;
     const EncoderConfig &c = m.encoder_cfg;
@@ -82,11 +56,7 @@ int make_pool(const ParakeetCtcModel &m, int n_slots, std::shared_ptr<detail::Sl
     for (int i = 0; i < d.n_duration_values; ++i) d.durations[i] = m.tdt_durations[i];
     d.eou_id = m.eou_id;
     d.eob_id = m.eob_id;
-    std::vector<uint8_t> special(m.vocab.pieces.size());
-    for (size_t i = 0; i < special.size(); ++i) {
-        const std::string &p = m.vocab.pieces[i];
-        special[i] = (!p.empty() && p.front() == '<' && p.back() == '>') ? 1 : 0;
-    }
+    const std::vector<uint8_t> special = core::special_pieces(m.vocab.pieces);
     d.special = special.empty() ? nullptr : special.data();
     d.n_special = (int32_t)special.size();
     const std::string p = prefix(m.model_type);
@@ -105,140 +75,20 @@ int make_pool(const ParakeetCtcModel &m, int n_slots, std::shared_ptr<detail::Sl
     d.joint_pred_b = tensor_of(m, p + "joint.pred.bias");
     d.joint_out_w = tensor_of(m, p + "joint.out.weight");
     d.joint_out_b = tensor_of(m, p + "joint.out.bias");
-    auto pool = std::make_shared<detail::SlotPool>();
-    if (int rc = pk_decoder_create(&d, n_slots, &pool->dec)) {
-        std::fprintf(stderr, "prepare_runtime: %s\n", pk_last_error());
-        return rc;
-    }
-    for (int s = n_slots - 1; s >= 0; --s) pool->free_slots.push_back(s);
-    out = std::move(pool);
-    return 0;
+    return core::make_pool(d, n_slots, out);
 }
 
-std::shared_ptr<detail::SlotLease> lease(const std::shared_ptr<detail::SlotPool> &pool) {
-    const int s = pool->acquire();
-    if (s < 0) throw std::runtime_error("parakeet: no free decoder state slot");
-    auto l = std::make_shared<detail::SlotLease>();
-    l->pool = pool;
-    l->slot = s;
-    return l;
-}
-
-// Encoder frames of a batch: one host window per utterance (packed into one
-// upload per call), or rows of an encoder output resident in device memory,
-// read in place by the enc_proj kernel.
-struct Frames {
-    bool device = false;
-    std::vector<const float *> host;   // host window of each utterance
-    const float *dev = nullptr;        // device encoder output
-    std::vector<int64_t> dev_row;      // first row of each utterance in it
-    Frames pick(const std::vector<int> &idx, size_t i, size_t j) const {
-        Frames f;
-        f.device = device;
-        f.dev = dev;
-        for (size_t k = i; k < j; ++k) {
-            if (device) f.dev_row.push_back(dev_row[idx[k]]);
-            else f.host.push_back(host[idx[k]]);
-        }
-        return f;
-    }
-};
-
-// One batched device call; fills per-utterance tokens/steps (+ EOU segments).
-int run_batch(detail::SlotPool &pool, int D_enc, int max_symbols, const Frames &fr, const std::vector<int> &n_frames,
-              const std::vector<int> &slots, const std::vector<int> &tokens_base,
-              std::vector<std::vector<int32_t>> &tokens, std::vector<std::vector<int32_t>> *segments,
-              std::vector<int> &steps) {
-    const int n = (int)n_frames.size();
-    int64_t rows = 0;
-    int max_T = 0;
-    std::vector<int64_t> row(n);
-    for (int u = 0; u < n; ++u) {
-        row[u] = rows;
-        rows += std::max(0, n_frames[u]);
-        max_T = std::max(max_T, n_frames[u]);
-    }
-    std::vector<float> packed;
-    if (fr.device) {
-        row = fr.dev_row;
-    } else {
-        packed.resize((size_t)std::max<int64_t>(rows, 1) * D_enc);
-        for (int u = 0; u < n; ++u)
-            if (n_frames[u] > 0)
-                memcpy(packed.data() + (size_t)row[u] * D_enc, fr.host[u], sizeof(float) * (size_t)n_frames[u] * D_enc);
-    }
-    const int cap = max_T * std::max(1, max_symbols) + 1;
-    std::vector<int32_t> tok((size_t)n * cap), ntok(n), st(n), seg((size_t)n * (cap + 1)), nseg(n);
-    std::vector<int32_t> T(n_frames.begin(), n_frames.end()), sl(slots.begin(), slots.end());
-    std::vector<int32_t> base(tokens_base.begin(), tokens_base.end());
-    pk_batch b{};
-    b.n_utts = n;
-    b.mem = fr.device ? PK_MEM_DEVICE_FRAMES : PK_MEM_HOST;
-    b.d_enc = D_enc;
-    b.max_symbols = max_symbols;
-    b.enc = fr.device ? fr.dev : packed.data();
-    b.enc_row = row.data();
-    b.n_frames = T.data();
-    b.slot = sl.data();
-    b.tokens_base = base.empty() ? nullptr : base.data();
-    b.tokens = tok.data();
-    b.token_cap = cap;
-    b.n_tokens = ntok.data();
-    b.steps = st.data();
-    b.segments = seg.data();
-    b.seg_cap = cap + 1;
-    b.n_segments = nseg.data();
-    if (int rc = pk_decode(pool.dec, &b)) {
-        std::fprintf(stderr, "decode: %s\n", pk_last_error());
-        return rc;
-    }
-    tokens.assign(n, {});
-    if (segments) segments->assign(n, {});
-    steps.assign(n, 0);
-    for (int u = 0; u < n; ++u) {
-        tokens[u].assign(tok.begin() + (size_t)u * cap, tok.begin() + (size_t)u * cap + ntok[u]);
-        steps[u] = st[u];
-        if (segments)
-            (*segments)[u].assign(seg.begin() + (size_t)u * (cap + 1), seg.begin() + (size_t)u * (cap + 1) + nseg[u]);
-    }
-    return 0;
-}
-
-// Frames of a device-resident encoder output, checked against its extent.
-// Returns 0, 1 (d_model mismatch, the reference's rc) or 3 (bad rows).
 int device_frames(const DeviceEncoderOutput &enc, const std::vector<int64_t> &row_offset,
                   const std::vector<int> &n_frames, int D_expected, const char *who, Frames &fr) {
-    if (enc.d_model != D_expected) {
-        std::fprintf(stderr, "%s: encoder d_model mismatch (%d vs %d)\n", who, enc.d_model, D_expected);
-        return 1;
-    }
-    if (row_offset.size() != n_frames.size()) return 3;
-    for (size_t u = 0; u < n_frames.size(); ++u) {
-        if (n_frames[u] <= 0) continue;
-        if (!enc.data || row_offset[u] < 0 || row_offset[u] + n_frames[u] > enc.n_rows) {
-            std::fprintf(stderr, "%s: utterance %zu rows [%lld, %lld) outside the encoder output (%lld rows)\n", who,
-                         u, (long long)row_offset[u], (long long)(row_offset[u] + n_frames[u]),
-                         (long long)enc.n_rows);
-            return 3;
-        }
-    }
-    fr.device = true;
-    fr.dev = enc.data;
-    fr.dev_row = row_offset;
-    return 0;
-}
-
-void read_ctrl(detail::SlotPool &pool, int slot, int32_t *ctrl) {
-    if (pk_slot_read(pool.dec, slot, nullptr, nullptr, nullptr, ctrl) != 0)
-        throw std::runtime_error(std::string("parakeet: slot read failed: ") + pk_last_error());
+    return core::device_frames(enc.data, enc.n_rows, enc.d_model, row_offset, n_frames, D_expected, who, fr);
 }
 
 }  // namespace
 
 // ------------------------------------------------------------------ loading
 
-int load_from_gguf(const std::string &gguf_path, ParakeetCtcModel &out, int, int, bool verbose) {
-    auto impl = std::make_shared<ParakeetCtcModel::Impl>();
+int load_from_gguf(const std::string &gguf_path, DecoderModel &out, int, int, bool verbose) {
+    auto impl = std::make_shared<DecoderModel::Impl>();
     std::string err;
     if (impl->file.open(gguf_path, err)) {
         std::fprintf(stderr, "gguf: %s\n", err.c_str());
@@ -249,7 +99,7 @@ int load_from_gguf(const std::string &gguf_path, ParakeetCtcModel &out, int, int
         std::fprintf(stderr, "gguf: expected arch=parakeet-ctc\n");
         return 2;
     }
-    out = ParakeetCtcModel{};
+    out = DecoderModel{};
     out.encoder_cfg.d_model = (int)g.get_u32("parakeet.encoder.d_model", 1024);
     out.encoder_cfg.subsampling_factor = (int)g.get_u32("parakeet.encoder.subsampling_factor", 8);
     out.mel_cfg.sample_rate = (int)g.get_u32("parakeet.preproc.sample_rate", 16000);
@@ -309,31 +159,12 @@ int load_from_gguf(const std::string &gguf_path, ParakeetCtcModel &out, int, int
 }
 
 std::string detokenize(const BpeVocab &vocab, const std::vector<int32_t> &ids) {
-    std::string out;
-    out.reserve(ids.size() * 3);
-    for (int32_t id : ids) {
-        if (id < 0 || id >= (int32_t)vocab.pieces.size()) continue;
-        if (id == vocab.blank_id || id == vocab.bos_id || id == vocab.eos_id || id == vocab.pad_id) continue;
-        const std::string &piece = vocab.pieces[id];
-        for (size_t i = 0; i < piece.size();) {
-            if ((unsigned char)piece[i] == 0xE2 && i + 2 < piece.size() && (unsigned char)piece[i + 1] == 0x96 &&
-                (unsigned char)piece[i + 2] == 0x81) {
-                out.push_back(' ');
-                i += 3;
-            } else {
-                out.push_back(piece[i++]);
-            }
-        }
-    }
-    size_t start = 0;
-    while (start < out.size() && out[start] == ' ') ++start;
-    out.erase(0, start);
-    return out;
+    return core::detokenize(vocab.pieces, vocab.blank_id, vocab.bos_id, vocab.eos_id, vocab.pad_id, ids);
 }
 
 // ------------------------------------------------------------------ TDT
 
-int tdt_prepare_runtime(const ParakeetCtcModel &model, TdtRuntimeWeights &W, int n_slots) {
+int tdt_prepare_runtime(const DecoderModel &model, TdtRuntimeWeights &W, int n_slots) {
     W = TdtRuntimeWeights{};
     if (model.model_type != ParakeetModelType::TDT || !model.impl) return 2;
     const EncoderConfig &c = model.encoder_cfg;
@@ -348,56 +179,21 @@ int tdt_prepare_runtime(const ParakeetCtcModel &model, TdtRuntimeWeights &W, int
     return make_pool(model, n_slots, W.pool);
 }
 
-void tdt_init_state(TdtRuntimeWeights &W, int, TdtDecodeState &state) {
-    if (!state.slot) state.slot = lease(W.pool);
-    if (pk_slot_init(W.pool->dec, state.slot->slot) != 0)
-        throw std::runtime_error(std::string("tdt_init_state: ") + pk_last_error());
-    state.symbols_this_step = 0;
-    state.carry_frames = 0;
-    state.h_state.clear();
-    state.c_state.clear();
-    state.pred_out.clear();
-    state.initialized = true;
-}
+// src/parakeet_tdt.cpp:813-863 (see core::tdt_fresh: the device work runs in
+// the state's next decode launch).
+void tdt_init_state(TdtRuntimeWeights &W, int, TdtDecodeState &state) { core::tdt_fresh(W.pool, state); }
 
 namespace {
 
-int tdt_batch(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const Frames &fr, const std::vector<int> &n_frames,
-              int D_enc, const TdtDecodeOptions &opts, const std::vector<TdtDecodeState *> &states,
+int tdt_batch(TdtRuntimeWeights &W, const Frames &fr, const std::vector<int> &n_frames, int D_enc,
+              const TdtDecodeOptions &opts, const std::vector<TdtDecodeState *> &states,
               std::vector<std::vector<int32_t>> &out_tokens, std::vector<int> &out_steps) {
-    const int n = (int)n_frames.size();
-    std::vector<int> idx, slots, T;
-    for (int u = 0; u < n; ++u) {
-        if (n_frames[u] <= 0) continue;   // src/parakeet_tdt.cpp:879
-        if (!states[u]->initialized) tdt_init_state(W, model.blank_id, *states[u]);
-        idx.push_back(u);
-        slots.push_back(states[u]->slot->slot);
-        T.push_back(n_frames[u]);
-    }
-    for (size_t i = 0; i < idx.size(); i += PK_MAX_BATCH) {
-        const size_t j = std::min(idx.size(), i + PK_MAX_BATCH);
-        std::vector<int> tt(T.begin() + i, T.begin() + j), ss(slots.begin() + i, slots.begin() + j);
-        std::vector<std::vector<int32_t>> toks;
-        std::vector<int> steps;
-        if (int rc = run_batch(*W.pool, D_enc, opts.max_symbols_per_step, fr.pick(idx, i, j), tt, ss, {}, toks,
-                               nullptr, steps))
-            return rc;
-        for (size_t k = i; k < j; ++k) {
-            const int u = idx[k];
-            out_tokens[u] = std::move(toks[k - i]);
-            out_steps[u] = steps[k - i];
-            int32_t ctrl[PK_CTRL_N];
-            read_ctrl(*W.pool, slots[k], ctrl);
-            states[u]->symbols_this_step = ctrl[PK_CTRL_SYM];
-            states[u]->carry_frames = ctrl[PK_CTRL_CARRY];
-        }
-    }
-    return 0;
+    return core::tdt_run(W.pool, D_enc, opts.max_symbols_per_step, fr, n_frames, states, out_tokens, out_steps);
 }
 
 }  // namespace
 
-int tdt_decode_batch(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const std::vector<const float *> &enc,
+int tdt_decode_batch(const DecoderModel &, TdtRuntimeWeights &W, const std::vector<const float *> &enc,
                      const std::vector<int> &n_frames, int D_enc, const TdtDecodeOptions &opts,
                      const std::vector<TdtDecodeState *> &states, std::vector<std::vector<int32_t>> &out_tokens,
                      std::vector<int> &out_steps) {
@@ -411,10 +207,10 @@ int tdt_decode_batch(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const 
     if ((int)n_frames.size() != n || (int)states.size() != n) return 3;
     Frames fr;
     fr.host = enc;
-    return tdt_batch(model, W, fr, n_frames, D_enc, opts, states, out_tokens, out_steps);
+    return tdt_batch(W, fr, n_frames, D_enc, opts, states, out_tokens, out_steps);
 }
 
-int tdt_decode_batch_device(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const DeviceEncoderOutput &enc,
+int tdt_decode_batch_device(const DecoderModel &, TdtRuntimeWeights &W, const DeviceEncoderOutput &enc,
                             const std::vector<int64_t> &row_offset, const std::vector<int> &n_frames,
                             const TdtDecodeOptions &opts, const std::vector<TdtDecodeState *> &states,
                             std::vector<std::vector<int32_t>> &out_tokens, std::vector<int> &out_steps) {
@@ -424,10 +220,10 @@ int tdt_decode_batch_device(const ParakeetCtcModel &model, TdtRuntimeWeights &W,
     if ((int)states.size() != n) return 3;
     Frames fr;
     if (int rc = device_frames(enc, row_offset, n_frames, W.D_enc, "tdt_decode_batch_device", fr)) return rc;
-    return tdt_batch(model, W, fr, n_frames, W.D_enc, opts, states, out_tokens, out_steps);
+    return tdt_batch(W, fr, n_frames, W.D_enc, opts, states, out_tokens, out_steps);
 }
 
-int tdt_decode_window(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const float *encoder_out_window,
+int tdt_decode_window(const DecoderModel &model, TdtRuntimeWeights &W, const float *encoder_out_window,
                       int n_frames, int D_enc, const TdtDecodeOptions &opts, TdtDecodeState &state,
                       std::vector<int32_t> &out_tokens, int &out_steps) {
     std::vector<std::vector<int32_t>> toks;
@@ -438,7 +234,7 @@ int tdt_decode_window(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const
     return rc;
 }
 
-int tdt_greedy_decode(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const float *encoder_out, int T_enc,
+int tdt_greedy_decode(const DecoderModel &model, TdtRuntimeWeights &W, const float *encoder_out, int T_enc,
                       int D_enc, const TdtDecodeOptions &opts, TdtDecodeResult &result) {
     const auto t0 = std::chrono::steady_clock::now();
     TdtDecodeState state;
@@ -454,7 +250,7 @@ int tdt_greedy_decode(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const
 
 // ------------------------------------------------------------------ EOU
 
-int eou_prepare_runtime(const ParakeetCtcModel &model, EouRuntimeWeights &W, int n_slots) {
+int eou_prepare_runtime(const DecoderModel &model, EouRuntimeWeights &W, int n_slots) {
     if (model.model_type != ParakeetModelType::EOU) return 1;   // src/parakeet_eou.cpp:173-175
     const EncoderConfig &c = model.encoder_cfg;
     W = EouRuntimeWeights{};
@@ -469,58 +265,27 @@ int eou_prepare_runtime(const ParakeetCtcModel &model, EouRuntimeWeights &W, int
     return make_pool(model, n_slots, W.pool);
 }
 
-void eou_init_state(const EouRuntimeWeights &W, EouDecodeState &state) {
-    if (!state.slot) state.slot = lease(W.pool);
-    if (pk_slot_init(W.pool->dec, state.slot->slot) != 0)
-        throw std::runtime_error(std::string("eou_init_state: ") + pk_last_error());
-    state.h_state.clear();
-    state.c_state.clear();
-    state.pred_out.clear();
-    state.last_token = -1;
-    state.symbols_this_step = 0;
-    state.segment_start_token = 0;
-    state.initialized = true;
-}
+// src/parakeet_eou.cpp:206-230 (see core::eou_fresh).
+void eou_init_state(const EouRuntimeWeights &W, EouDecodeState &state) { core::eou_fresh(W.pool, state); }
 
 namespace {
 
 int eou_batch(const EouRuntimeWeights &W, const Frames &fr, const std::vector<int> &n_frames, int D_enc,
               const EouDecodeOptions &opts, const std::vector<EouDecodeState *> &states,
-              std::vector<std::vector<int32_t>> &out_tokens, std::vector<std::vector<EouSegmentBoundary>> &out_segments,
-              std::vector<int> &out_steps) {
-    const int n = (int)n_frames.size();
-    std::vector<int> idx(n), slots(n), base(n, 0);
-    for (int u = 0; u < n; ++u) {
-        if (!states[u]->initialized) eou_init_state(W, *states[u]);
-        idx[u] = u;
-        slots[u] = states[u]->slot->slot;
-    }
-    for (int i = 0; i < n; i += PK_MAX_BATCH) {
-        const int j = std::min(n, i + PK_MAX_BATCH);
-        std::vector<int> tt(n_frames.begin() + i, n_frames.begin() + j), ss(slots.begin() + i, slots.begin() + j);
-        std::vector<int> bb(base.begin() + i, base.begin() + j);
-        std::vector<std::vector<int32_t>> toks, segs;
-        std::vector<int> steps;
-        if (int rc = run_batch(*W.pool, D_enc, opts.max_symbols_per_step, fr.pick(idx, i, j), tt, ss, bb, toks, &segs,
-                               steps))
-            return rc;
-        for (int u = i; u < j; ++u) {
-            out_tokens[u] = std::move(toks[u - i]);
-            out_steps[u] = steps[u - i];
-            for (int32_t s : segs[u - i]) out_segments[u].push_back(EouSegmentBoundary{s, true});
-            int32_t ctrl[PK_CTRL_N];
-            read_ctrl(*W.pool, slots[u], ctrl);
-            states[u]->symbols_this_step = ctrl[PK_CTRL_SYM];
-            states[u]->last_token = ctrl[PK_CTRL_LAST];
-            states[u]->segment_start_token = ctrl[PK_CTRL_SEGSTART];
-        }
-    }
+              const std::vector<int> &tokens_base, std::vector<std::vector<int32_t>> &out_tokens,
+              std::vector<std::vector<EouSegmentBoundary>> &out_segments, std::vector<int> &out_steps) {
+    std::vector<std::vector<int32_t>> bounds(n_frames.size());
+    if (int rc = core::eou_run(W.pool, D_enc, opts.max_symbols_per_step, fr, n_frames, states, tokens_base, out_tokens,
+                               bounds, out_steps))
+        return rc;
+    for (size_t u = 0; u < n_frames.size(); ++u)
+        for (int32_t b : bounds[u]) out_segments[u].push_back(EouSegmentBoundary{b, true});
     return 0;
 }
 
 }  // namespace
 
-int eou_decode_batch(const ParakeetCtcModel &, const EouRuntimeWeights &W, const std::vector<const float *> &enc,
+int eou_decode_batch(const DecoderModel &, const EouRuntimeWeights &W, const std::vector<const float *> &enc,
                      const std::vector<int> &n_frames, int D_enc, const EouDecodeOptions &opts,
                      const std::vector<EouDecodeState *> &states, std::vector<std::vector<int32_t>> &out_tokens,
                      std::vector<std::vector<EouSegmentBoundary>> &out_segments, std::vector<int> &out_steps) {
@@ -535,10 +300,10 @@ int eou_decode_batch(const ParakeetCtcModel &, const EouRuntimeWeights &W, const
     if ((int)n_frames.size() != n || (int)states.size() != n) return 3;
     Frames fr;
     fr.host = enc;
-    return eou_batch(W, fr, n_frames, D_enc, opts, states, out_tokens, out_segments, out_steps);
+    return eou_batch(W, fr, n_frames, D_enc, opts, states, {}, out_tokens, out_segments, out_steps);
 }
 
-int eou_decode_batch_device(const ParakeetCtcModel &, const EouRuntimeWeights &W, const DeviceEncoderOutput &enc,
+int eou_decode_batch_device(const DecoderModel &, const EouRuntimeWeights &W, const DeviceEncoderOutput &enc,
                             const std::vector<int64_t> &row_offset, const std::vector<int> &n_frames,
                             const EouDecodeOptions &opts, const std::vector<EouDecodeState *> &states,
                             std::vector<std::vector<int32_t>> &out_tokens,
@@ -550,51 +315,34 @@ int eou_decode_batch_device(const ParakeetCtcModel &, const EouRuntimeWeights &W
     if ((int)states.size() != n) return 3;
     Frames fr;
     if (int rc = device_frames(enc, row_offset, n_frames, W.D_enc, "eou_decode_batch_device", fr)) return rc;
-    return eou_batch(W, fr, n_frames, W.D_enc, opts, states, out_tokens, out_segments, out_steps);
+    return eou_batch(W, fr, n_frames, W.D_enc, opts, states, {}, out_tokens, out_segments, out_steps);
 }
 
-int eou_decode_window(const ParakeetCtcModel &model, const EouRuntimeWeights &W, const float *encoder_out_window,
+int eou_decode_window(const DecoderModel &, const EouRuntimeWeights &W, const float *encoder_out_window,
                       int n_frames, int D_enc, const EouDecodeOptions &opts, EouDecodeState &state,
                       std::vector<int32_t> &out_tokens, std::vector<EouSegmentBoundary> &out_segments,
                       int &out_steps) {
-    (void)model;   // kept for the reference signature; the runtime weights carry every size used here
     if (D_enc != W.D_enc) {
         std::fprintf(stderr, "eou_decode_window: encoder d_model mismatch (%d vs %d)\n", D_enc, W.D_enc);
         return 1;
     }
-    if (!state.initialized) eou_init_state(W, state);
     // segment indices count from the caller's token vector (src/parakeet_eou.cpp:293-298)
-    const int base = (int)out_tokens.size();
-    const int n = std::max(0, n_frames);
-    std::vector<int32_t> toks;
-    std::vector<int> steps;
-    std::vector<std::vector<int32_t>> tv, sv;
+    std::vector<std::vector<int32_t>> tv;
+    std::vector<std::vector<EouSegmentBoundary>> sv(1);
+    std::vector<int> steps(1, 0);
+    tv.assign(1, {});
     Frames fr;
     fr.host = {encoder_out_window};
-    if (int rc = run_batch(*W.pool, D_enc, opts.max_symbols_per_step, fr, {n}, {state.slot->slot}, {base}, tv, &sv,
+    if (int rc = eou_batch(W, fr, {std::max(0, n_frames)}, D_enc, opts, {&state}, {(int)out_tokens.size()}, tv, sv,
                            steps))
         return rc;
     out_steps = steps[0];
     out_tokens.insert(out_tokens.end(), tv[0].begin(), tv[0].end());
-    for (int32_t s : sv[0]) out_segments.push_back(EouSegmentBoundary{s, true});
-    int32_t ctrl[PK_CTRL_N];
-    read_ctrl(*W.pool, state.slot->slot, ctrl);
-    state.symbols_this_step = ctrl[PK_CTRL_SYM];
-    state.last_token = ctrl[PK_CTRL_LAST];
-    state.segment_start_token = ctrl[PK_CTRL_SEGSTART];
+    out_segments.insert(out_segments.end(), sv[0].begin(), sv[0].end());
     return 0;
 }
 
-namespace {
-std::string trim_spaces(const std::string &s) {
-    const size_t a = s.find_first_not_of(" \t\r\n");
-    if (a == std::string::npos) return std::string();
-    const size_t b = s.find_last_not_of(" \t\r\n");
-    return s.substr(a, b - a + 1);
-}
-}  // namespace
-
-int eou_greedy_decode(const ParakeetCtcModel &model, const EouRuntimeWeights &W, const float *encoder_out, int T_enc,
+int eou_greedy_decode(const DecoderModel &model, const EouRuntimeWeights &W, const float *encoder_out, int T_enc,
                       int D_enc, const EouDecodeOptions &opts, EouDecodeResult &result) {
     const auto t0 = std::chrono::steady_clock::now();
     EouDecodeState state;
@@ -604,21 +352,10 @@ int eou_greedy_decode(const ParakeetCtcModel &model, const EouRuntimeWeights &W,
                                    result.segments, result.steps))
         return rc;
     result.eou_count = (int)result.segments.size();
-    // segments joined with '\n' (src/parakeet_eou.cpp:359-382)
-    int seg_start = 0;
-    std::string text;
-    for (size_t i = 0; i <= result.segments.size(); ++i) {
-        const int seg_end = i < result.segments.size() ? result.segments[i].token_index : (int)result.token_ids.size();
-        if (seg_end <= seg_start) { seg_start = seg_end; continue; }
-        std::vector<int32_t> seg(result.token_ids.begin() + seg_start, result.token_ids.begin() + seg_end);
-        std::string s = trim_spaces(detokenize(model.vocab, seg));
-        if (!s.empty()) {
-            if (!text.empty()) text += "\n";
-            text += s;
-        }
-        seg_start = seg_end;
-    }
-    result.text = std::move(text);
+    std::vector<int32_t> bounds;
+    for (const auto &b : result.segments) bounds.push_back(b.token_index);
+    const BpeVocab &v = model.vocab;
+    result.text = core::eou_text(v.pieces, v.blank_id, v.bos_id, v.eos_id, v.pad_id, result.token_ids, bounds);
     result.decode_ms =
         std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::steady_clock::now() - t0).count() / 1000.0;
     return 0;
@@ -628,7 +365,7 @@ int eou_greedy_decode(const ParakeetCtcModel &model, const EouRuntimeWeights &W,
 
 struct Engine::Impl {
     EngineOptions opts;
-    ParakeetCtcModel model;
+    DecoderModel model;
     TdtRuntimeWeights tdt;
     EouRuntimeWeights eou;
 };
@@ -651,7 +388,7 @@ Engine::Engine(const EngineOptions &opts) : pimpl_(std::make_unique<Impl>()) {
 
 Engine::~Engine() = default;
 
-const ParakeetCtcModel &Engine::model() const { return pimpl_->model; }
+const DecoderModel &Engine::model() const { return pimpl_->model; }
 
 EngineResult Engine::transcribe_features(const float *enc, int T_enc, int D_enc) {
     return transcribe_features_batch({enc}, {T_enc}, D_enc)[0];
@@ -664,7 +401,7 @@ std::vector<EngineResult> engine_decode(Engine::Impl &E, const Frames &fr, const
     const auto t0 = std::chrono::steady_clock::now();
     const int n = (int)T_enc.size();
     std::vector<EngineResult> out(n);
-    const ParakeetCtcModel &m = E.model;
+    const DecoderModel &m = E.model;
     if (m.model_type == ParakeetModelType::TDT) {
         std::vector<TdtDecodeState> states(n);
         std::vector<TdtDecodeState *> sp(n);
@@ -672,7 +409,7 @@ std::vector<EngineResult> engine_decode(Engine::Impl &E, const Frames &fr, const
         std::vector<std::vector<int32_t>> toks(n);
         std::vector<int> steps(n, 0);
         int rc = D_enc != E.tdt.D_enc ? 1 : 0;
-        if (rc == 0) rc = tdt_batch(m, E.tdt, fr, T_enc, D_enc, TdtDecodeOptions{}, sp, toks, steps);
+        if (rc == 0) rc = tdt_batch(E.tdt, fr, T_enc, D_enc, TdtDecodeOptions{}, sp, toks, steps);
         if (rc) throw std::runtime_error("parakeet::Engine: tdt decode failed (rc=" + std::to_string(rc) + ")");
         for (int u = 0; u < n; ++u) {
             out[u].token_ids = std::move(toks[u]);
@@ -689,23 +426,15 @@ std::vector<EngineResult> engine_decode(Engine::Impl &E, const Frames &fr, const
         std::vector<std::vector<EouSegmentBoundary>> segs(n);
         std::vector<int> steps(n, 0);
         int rc = D_enc != E.eou.D_enc ? 1 : 0;
-        if (rc == 0) rc = eou_batch(E.eou, fr, T_enc, D_enc, o, sp, toks, segs, steps);
+        if (rc == 0) rc = eou_batch(E.eou, fr, T_enc, D_enc, o, sp, {}, toks, segs, steps);
         if (rc) throw std::runtime_error("parakeet::Engine: eou decode failed (rc=" + std::to_string(rc) + ")");
         for (int u = 0; u < n; ++u) {
             out[u].token_ids = std::move(toks[u]);
             out[u].steps = steps[u];
-            int s0 = 0;
-            std::string text;
-            for (size_t i = 0; i <= segs[u].size(); ++i) {
-                const int e = i < segs[u].size() ? segs[u][i].token_index : (int)out[u].token_ids.size();
-                if (e > s0) {
-                    std::vector<int32_t> seg(out[u].token_ids.begin() + s0, out[u].token_ids.begin() + e);
-                    std::string s = trim_spaces(detokenize(m.vocab, seg));
-                    if (!s.empty()) text += (text.empty() ? "" : "\n") + s;
-                }
-                s0 = e;
-            }
-            out[u].text = std::move(text);
+            std::vector<int32_t> bounds;
+            for (const auto &b : segs[u]) bounds.push_back(b.token_index);
+            const BpeVocab &v = m.vocab;
+            out[u].text = core::eou_text(v.pieces, v.blank_id, v.bos_id, v.eos_id, v.pad_id, out[u].token_ids, bounds);
         }
     }
     const double ms =
@@ -731,17 +460,17 @@ std::vector<EngineResult> Engine::transcribe_features_batch(const std::vector<co
 std::vector<EngineResult> Engine::transcribe_device_batch(const DeviceEncoderOutput &enc,
                                                           const std::vector<int64_t> &row_offset,
                                                           const std::vector<int> &T_enc) {
-    const ParakeetCtcModel &m = pimpl_->model;
+    const DecoderModel &m = pimpl_->model;
     const int D = m.model_type == ParakeetModelType::TDT ? pimpl_->tdt.D_enc : pimpl_->eou.D_enc;
     Frames fr;
-    if (int rc = device_frames(enc, row_offset, T_enc, D, "parakeet::Engine::transcribe_device_batch", fr))
+    if (int rc = device_frames(enc, row_offset, T_enc, D, "parakeet_hip::Engine::transcribe_device_batch", fr))
         throw std::runtime_error("parakeet::Engine: device frames rejected (rc=" + std::to_string(rc) + ")");
     return engine_decode(*pimpl_, fr, T_enc, D);
 }
 
 // ------------------------------------------------------------------ streaming over features
 
-double encoder_frame_stride_ms(const ParakeetCtcModel &m) {
+double encoder_frame_stride_ms(const DecoderModel &m) {
     const int sub = m.encoder_cfg.subsampling_factor > 0 ? m.encoder_cfg.subsampling_factor : 8;
     const int sr = m.mel_cfg.sample_rate > 0 ? m.mel_cfg.sample_rate : 16000;
     return 1000.0 * (double)(m.mel_cfg.hop_length * sub) / (double)sr;
@@ -777,7 +506,7 @@ void FeatureStreamSession::finalize() { pimpl_->finalized = true; }
 
 void FeatureStreamSession::Impl::emit(const std::vector<int32_t> &win_tokens, int n_boundaries, int n_frames,
                                       double decode_ms) {
-    const ParakeetCtcModel &m = engine->model;
+    const DecoderModel &m = engine->model;
     const size_t prev = cum_text.size();
     cum_ids.insert(cum_ids.end(), win_tokens.begin(), win_tokens.end());
     cum_text = detokenize(m.vocab, cum_ids);
@@ -834,7 +563,7 @@ void FeatureStreamSession::feed_frames_batch(const std::vector<FeatureStreamSess
     }
     if (live.empty()) return;
     Engine::Impl &E = *live[0]->engine;
-    const ParakeetCtcModel &m = E.model;
+    const DecoderModel &m = E.model;
     const int n = (int)live.size();
     const auto t0 = std::chrono::steady_clock::now();
     std::vector<std::vector<int32_t>> toks;
@@ -901,4 +630,4 @@ EngineResult Engine::transcribe_features_stream(const float *enc, int T_enc, int
     return result;
 }
 
-}  // namespace parakeet
+}  // namespace parakeet_hip

@@ -682,6 +682,28 @@ PK_API int pk_slot_read(pk_decoder *dec, int32_t slot, float *h, float *c, float
     return 0;
 }
 
+PK_API int pk_slot_copy(pk_decoder *dec, int32_t src, int32_t dst) {
+    g_err.clear();
+    if (!dec || src < 0 || src >= dec->n_slots || dst < 0 || dst >= dec->n_slots)
+        return fail(PK_ERR_ARG, "pk_slot_copy: bad slot");
+    if (src == dst) return 0;
+    HIP_TRY(hipSetDevice(dec->device));
+    const KParams &kp = dec->kp;
+    const size_t hn = (size_t)kp.L * kp.H, rn = (size_t)kp.L * 4 * kp.H;
+    auto cp = [&](void *base, size_t per_slot) {
+        char *b = static_cast<char *>(base);
+        return hipMemcpyAsync(b + (size_t)dst * per_slot, b + (size_t)src * per_slot, per_slot,
+                              hipMemcpyDeviceToDevice, dec->stream);
+    };
+    HIP_TRY(cp(kp.slot_h, hn * 4));
+    HIP_TRY(cp(kp.slot_c, hn * 4));
+    HIP_TRY(cp(kp.slot_pp, (size_t)kp.J * 4));
+    HIP_TRY(cp(kp.slot_r, rn * 4));
+    HIP_TRY(cp(kp.slot_ctrl, PK_CTRL_N * 4));
+    HIP_TRY(hipStreamSynchronize(dec->stream));
+    return 0;
+}
+
 PK_API int pk_last_timing(pk_decoder *dec, float *enc_proj_ms, float *loop_ms, int32_t *iterations) {
     if (!dec) return fail(PK_ERR_ARG, "pk_last_timing: null");
     float a = 0, b = 0;
@@ -787,11 +809,19 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
             bt->steps[u] = 0;
             if (bt->n_segments) bt->n_segments[u] = 0;
         }
+    if (host && bt->ctrl_out && m < n)   // utterances that do not run keep their slot's words (a reset one reads as fresh)
+        for (int u = 0, i = 0; u < n; ++u) {
+            if (i < m && map[i] == u) { ++i; continue; }
+            int32_t *dst = bt->ctrl_out + (size_t)u * PK_CTRL_N;
+            if (bt->reset && bt->reset[u]) memset(dst, 0, PK_CTRL_N * 4);
+            else HIP_TRY(hipMemcpy(dst, p.slot_ctrl + (size_t)bt->slot[u] * PK_CTRL_N, PK_CTRL_N * 4,
+                                   hipMemcpyDeviceToHost));
+        }
     if (m == 0) return 0;
     long long rows = 0;
     int max_T = 0;
     std::vector<long long> src_row(m), dst_row(m);
-    std::vector<int32_t> T(m), slots(m), base(m);
+    std::vector<int32_t> T(m), slots(m), base(m), reset(m);
     std::vector<float> bias(m);
     for (int i = 0; i < m; ++i) {
         const int u = map[i];
@@ -803,6 +833,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
         max_T = std::max(max_T, T[i]);
         bias[i] = bt->blank_bias ? bt->blank_bias[u] : 0.0f;
         base[i] = bt->tokens_base ? bt->tokens_base[u] : 0;
+        reset[i] = bt->reset ? (bt->reset[u] ? 1 : 0) : 0;
     }
     const int max_iter = max_T * (std::max(bt->max_symbols, 1) + 1) + 4;
     // the loop addresses encp with 32-bit buffer offsets below 2^31
@@ -843,8 +874,8 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     for (int d = 0; d < pl.n_dom; ++d)
         if (pl.dom_n[d] > kDomCap) return fail(PK_ERR_UNSUPPORTED, "batch of %d too large for %d compute units", m, dec->nwg);
     // descriptor block (device): int64 src_row, dst_row; int32 T, slot, base; f32 bias;
-    // int32 dom_n, dom_list, wg_dom, wg_rank, dom_wg
-    const size_t n64 = 2 * (size_t)m, n32 = 4 * (size_t)m + pl.dom_n.size() + pl.dom_list.size() +
+    // int32 reset, dom_n, dom_list, wg_dom, wg_rank, dom_wg
+    const size_t n64 = 2 * (size_t)m, n32 = 5 * (size_t)m + pl.dom_n.size() + pl.dom_list.size() +
                                               pl.wg_dom.size() + pl.wg_rank.size() + pl.dom_wg.size();
     const size_t desc_bytes = n64 * 8 + n32 * 4;
     void *d_desc = nullptr;
@@ -864,6 +895,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     const int *d_slot = reinterpret_cast<const int *>(put(slots.data(), 4 * (size_t)m));
     const int *d_base = reinterpret_cast<const int *>(put(base.data(), 4 * (size_t)m));
     const float *d_bias = reinterpret_cast<const float *>(put(bias.data(), 4 * (size_t)m));
+    const int *d_reset = reinterpret_cast<const int *>(put(reset.data(), 4 * (size_t)m));
     const int *d_dom_n = reinterpret_cast<const int *>(put(pl.dom_n.data(), 4 * pl.dom_n.size()));
     const int *d_dom_list = reinterpret_cast<const int *>(put(pl.dom_list.data(), 4 * pl.dom_list.size()));
     const int *d_wg_dom = reinterpret_cast<const int *>(put(pl.wg_dom.data(), 4 * pl.wg_dom.size()));
@@ -887,11 +919,11 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     const int tcap = bt->token_cap, scap = std::max(bt->seg_cap, 0), trcap = bt->trace ? bt->trace_cap : 0;
     const int lsteps = bt->logits ? std::max(bt->logit_steps, 0) : 0;
     const size_t lrow = (size_t)lsteps * p.Vo;   // tapped floats per utterance
-    int *o_tok, *o_ntok, *o_steps, *o_seg = nullptr, *o_nseg = nullptr, *o_trace = nullptr;
+    int *o_tok, *o_ntok, *o_steps, *o_seg = nullptr, *o_nseg = nullptr, *o_trace = nullptr, *o_ctrl = nullptr;
     float *o_logits = nullptr;
     if (host) {
-        const size_t need =
-            ((size_t)m * tcap + 3 * (size_t)m + (size_t)m * scap + (size_t)m * trcap * 2 + (size_t)m * lrow) * 4 + 64;
+        const size_t need = ((size_t)m * tcap + 3 * (size_t)m + (size_t)m * scap + (size_t)m * trcap * 2 +
+                             (size_t)m * PK_CTRL_N + (size_t)m * lrow) * 4 + 64;
         if ((rc = dec->d_out.ensure(need))) return rc;
         int *o = dec->d_out.as<int>();
         o_tok = o; o += (size_t)m * tcap;
@@ -900,10 +932,12 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
         o_nseg = o; o += m;
         o_seg = scap > 0 ? o : nullptr; o += (size_t)m * scap;
         o_trace = trcap > 0 ? o : nullptr; o += (size_t)m * trcap * 2;
+        o_ctrl = bt->ctrl_out ? o : nullptr; o += (size_t)m * PK_CTRL_N;
         o_logits = lrow > 0 ? reinterpret_cast<float *>(o) : nullptr;
     } else {
         o_tok = bt->tokens; o_ntok = bt->n_tokens; o_steps = bt->steps;
         o_seg = bt->segments; o_nseg = bt->n_segments; o_trace = bt->trace;
+        o_ctrl = bt->ctrl_out;
         o_logits = lrow > 0 ? bt->logits : nullptr;
     }
     p.n_utts = m;
@@ -919,6 +953,8 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     p.segs = o_seg; p.seg_cap = scap; p.n_segs = o_nseg;
     p.trace = o_trace; p.trace_cap = trcap;
     p.logits = o_logits; p.logit_steps = lsteps;
+    p.reset = bt->reset ? d_reset : nullptr;
+    p.ctrl_out = o_ctrl;
     p.max_sym = bt->max_symbols;
     p.max_iter = max_iter;
     p.n_dom = pl.n_dom;
@@ -1059,6 +1095,12 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
                 HIP_TRY(hipMemcpy2DAsync(s_tr, 8 * (size_t)wr, o_trace, 8 * (size_t)trcap, 8 * (size_t)wr, m,
                                          hipMemcpyDeviceToHost, dec->stream));
             HIP_TRY(hipStreamSynchronize(dec->stream));
+        }
+        if (o_ctrl) {   // control words of every utterance in one copy
+            std::vector<int32_t> c((size_t)m * PK_CTRL_N);
+            HIP_TRY(hipMemcpy(c.data(), o_ctrl, c.size() * 4, hipMemcpyDeviceToHost));
+            for (int i = 0; i < m; ++i)
+                memcpy(bt->ctrl_out + (size_t)map[i] * PK_CTRL_N, c.data() + (size_t)i * PK_CTRL_N, PK_CTRL_N * 4);
         }
         if (o_logits)   // debug tap: straight into the caller's rows (utterance order may differ)
             for (int i = 0; i < m; ++i)

@@ -95,6 +95,8 @@ struct KParams {
     int *segs; int seg_cap; int *n_segs;
     int *trace; int trace_cap;
     float *logits; int logit_steps;   // nullable debug tap [n_utts][logit_steps][Vo]
+    const int *reset;            // nullable [n_utts]: 1 = fresh state whatever the slot holds
+    int *ctrl_out;               // nullable [n_utts][PK_CTRL_N]: control words after the call
     // exchange buffers of one launch (batch-indexed, written/read coherently)
     float *hx;           // [2][L][n][H] ping-pong by utterance parity
     float *cx;           // [2][L][n][H]
@@ -1377,7 +1379,7 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         const int b = p.dom_list[s.dom * kDomCap + ul];
         const int slot = p.slot[b];
         const int *ctrl = p.slot_ctrl + (size_t)slot * PK_CTRL_N;
-        const bool init = ctrl[PK_CTRL_INIT] != 0;
+        const bool init = ctrl[PK_CTRL_INIT] != 0 && !(p.reset && p.reset[b]);
         s.b[ul] = b;
         s.T[ul] = p.T[b];
         s.erow[ul] = p.encp_row[b];
@@ -1516,14 +1518,17 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
             for (int j = 0; j < kCopyB; ++j)
                 if (q0 + threadIdx.x + j * kBlock < nq) *reinterpret_cast<float4 *>(dst[j]) = v[j];
         }
+        if (threadIdx.x < PK_CTRL_N) {   // the slot's control words (and the caller's copy)
+            const int k = threadIdx.x;
+            const int v = k == PK_CTRL_INIT ? 1
+                        : k == PK_CTRL_SYM ? s.sym[ul]
+                        : k == PK_CTRL_CARRY ? ((p.kind == PK_KIND_TDT) ? max(0, s.t[ul] - s.T[ul]) : 0)
+                        : k == PK_CTRL_LAST ? s.last[ul]
+                        : k == PK_CTRL_SEGSTART ? s.segst[ul] : 0;
+            p.slot_ctrl[(size_t)slot * PK_CTRL_N + k] = v;
+            if (p.ctrl_out) p.ctrl_out[(size_t)b * PK_CTRL_N + k] = v;
+        }
         if (threadIdx.x == 0) {
-            int *ctrl = p.slot_ctrl + (size_t)slot * PK_CTRL_N;
-            ctrl[PK_CTRL_INIT] = 1;
-            ctrl[PK_CTRL_SYM] = s.sym[ul];
-            ctrl[PK_CTRL_CARRY] = (p.kind == PK_KIND_TDT) ? max(0, s.t[ul] - s.T[ul]) : 0;
-            ctrl[PK_CTRL_LAST] = s.last[ul];
-            ctrl[PK_CTRL_SEGSTART] = s.segst[ul];
-            ctrl[PK_CTRL_CUR] = 0;
             p.n_tokens[b] = s.ntok[ul];
             p.steps[b] = s.steps[ul];
             if (p.n_segs) p.n_segs[b] = s.nseg[ul];

@@ -64,11 +64,12 @@ class PkBatch(C.Structure):
                 ("tokens_base", C.c_void_p), ("tokens", C.c_void_p), ("token_cap", C.c_int32),
                 ("n_tokens", C.c_void_p), ("steps", C.c_void_p), ("segments", C.c_void_p),
                 ("seg_cap", C.c_int32), ("n_segments", C.c_void_p), ("trace", C.c_void_p),
-                ("trace_cap", C.c_int32), ("logits", C.c_void_p), ("logit_steps", C.c_int32)]
+                ("trace_cap", C.c_int32), ("logits", C.c_void_p), ("logit_steps", C.c_int32),
+                ("reset", C.c_void_p), ("ctrl_out", C.c_void_p)]
 
 
 EXPORTED = ["pk_decoder_create", "pk_decoder_destroy", "pk_slot_init", "pk_slot_reset",
-            "pk_slot_read", "pk_decode", "pk_decode_noalloc", "pk_last_timing", "pk_last_error",
+            "pk_slot_read", "pk_slot_copy", "pk_decode", "pk_decode_noalloc", "pk_last_timing", "pk_last_error",
             "pk_device_info"]
 
 _lib = None
@@ -85,6 +86,7 @@ def lib():
         L.pk_slot_init.argtypes = [C.c_void_p, C.c_int32]
         L.pk_slot_reset.argtypes = [C.c_void_p, C.c_int32]
         L.pk_slot_read.argtypes = [C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        L.pk_slot_copy.argtypes = [C.c_void_p, C.c_int32, C.c_int32]
         L.pk_decode.argtypes = [C.c_void_p, C.POINTER(PkBatch)]
         L.pk_decode_noalloc.argtypes = [C.c_void_p, C.POINTER(PkBatch)]
         L.pk_last_timing.argtypes = [C.c_void_p, C.POINTER(C.c_float), C.POINTER(C.c_float),
@@ -223,6 +225,9 @@ class Decoder:
     def reset_state(self, slot: int):
         check(lib().pk_slot_reset(self.h, slot))
 
+    def copy_state(self, src: int, dst: int):
+        check(lib().pk_slot_copy(self.h, src, dst))
+
     def read_state(self, slot: int):
         i = self.info
         h = np.zeros(i.L * i.H, np.float32)
@@ -234,7 +239,8 @@ class Decoder:
 
     # ---- decode ----
     def decode(self, encs: list, slots=None, max_symbols: int | None = None, blank_bias=None,
-               tokens_base=None, trace: bool = False, token_cap: int | None = None, logit_steps: int = 0):
+               tokens_base=None, trace: bool = False, token_cap: int | None = None, logit_steps: int = 0,
+               reset=None):
         """Host-memory batch: encs[u] is [T_u, D] f32.  Returns a list of dicts
         (``logits``: [logit_steps, Vo] joint logits of the first steps when
         logit_steps > 0; rows past the utterance's steps are NaN)."""
@@ -249,7 +255,7 @@ class Decoder:
         else:
             enc = np.zeros((1, d_enc), np.float32)
         return self._decode(MEM_HOST, _ptr(enc), rows, T, d_enc, slots, max_symbols, blank_bias, tokens_base,
-                            trace, token_cap, logit_steps)
+                            trace, token_cap, logit_steps, reset)
 
     def decode_device_frames(self, enc_ptr: int, enc_row, n_frames, slots=None, max_symbols: int | None = None,
                              blank_bias=None, tokens_base=None, trace: bool = False, token_cap: int | None = None,
@@ -264,7 +270,7 @@ class Decoder:
                             blank_bias, tokens_base, trace, token_cap, logit_steps)
 
     def _decode(self, mem, enc, rows, T, d_enc, slots, max_symbols, blank_bias, tokens_base, trace, token_cap,
-                logit_steps=0):
+                logit_steps=0, reset=None):
         """One pk_decode call with host outputs; per-utterance result dicts."""
         info = self.info
         n = len(T)
@@ -288,6 +294,9 @@ class Decoder:
         b.tokens, b.token_cap, b.n_tokens, b.steps = _ptr(toks), cap, _ptr(ntok), _ptr(steps)
         b.segments, b.seg_cap, b.n_segments = _ptr(segs), cap + 1, _ptr(nseg)
         b.trace, b.trace_cap = (_ptr(tr) if trace else None), tcap
+        rs = None if reset is None else np.ascontiguousarray(reset, np.uint8)
+        ctrl = np.zeros((n, PK_CTRL_N), np.int32)
+        b.reset, b.ctrl_out = _ptr(rs), _ptr(ctrl)
         lg = None
         if logit_steps > 0:
             lg = np.full((n, logit_steps, info.Vo), np.nan, np.float32)
@@ -295,7 +304,7 @@ class Decoder:
         check(lib().pk_decode(self.h, C.byref(b)))
         # per-utterance views of this call's output arrays
         nt, st, ns = ntok.tolist(), steps.tolist(), nseg.tolist()
-        out = [dict(tokens=toks[u, :nt[u]], steps=st[u], segments=segs[u, :ns[u]]) for u in range(n)]
+        out = [dict(tokens=toks[u, :nt[u]], steps=st[u], segments=segs[u, :ns[u]], ctrl=ctrl[u]) for u in range(n)]
         if trace:
             for u in range(n):
                 out[u]["trace"] = tr[u, :min(st[u], tcap)]

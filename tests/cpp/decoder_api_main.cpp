@@ -65,8 +65,8 @@ void str(const std::string &s) {
 }
 
 struct SegLog {
-    std::vector<parakeet::StreamingSegment> segs;
-    std::vector<parakeet::StreamEvent> events;
+    std::vector<parakeet_hip::StreamingSegment> segs;
+    std::vector<parakeet_hip::StreamEvent> events;
 };
 
 void print_log(const SegLog &l) {
@@ -125,12 +125,12 @@ void int_lists(const std::vector<std::vector<int32_t>> &v) {
 }
 
 int device_section(const char *tdt_path, const char *eou_path, const Frames &ft, const Frames &fe) {
-    using namespace parakeet;
+    using namespace parakeet_hip;
     int rc;
     DeviceCopy dt(ft), de(fe);
     if (!dt.ok || !de.ok) return fail("device copy of the frames", -1);
     // TDT: host windows and device rows, fresh states each
-    ParakeetCtcModel tdt;
+    DecoderModel tdt;
     if ((rc = load_from_gguf(tdt_path, tdt)) != 0) return fail("load_from_gguf(tdt)", rc);
     TdtRuntimeWeights tw;
     if ((rc = tdt_prepare_runtime(tdt, tw, 2 * ft.n + 4)) != 0) return fail("tdt_prepare_runtime", rc);
@@ -177,7 +177,7 @@ int device_section(const char *tdt_path, const char *eou_path, const Frames &ft,
         printf(",\"rc_range\":%d,\"rc_dim\":%d", rc_range, rc_dim);
     }
     // EOU: the same with segment boundaries
-    ParakeetCtcModel eou;
+    DecoderModel eou;
     if ((rc = load_from_gguf(eou_path, eou)) != 0) return fail("load_from_gguf(eou)", rc);
     EouRuntimeWeights ew;
     if ((rc = eou_prepare_runtime(eou, ew, 2 * fe.n + 4)) != 0) return fail("eou_prepare_runtime", rc);
@@ -253,11 +253,11 @@ int main(int argc, char **argv) {
     const int W = atoi(argv[5]);
     Frames ft, fe;
     if (!read_frames(argv[2], ft) || !read_frames(argv[4], fe)) return fail("read frames", -1);
-    using namespace parakeet;
+    using namespace parakeet_hip;
     int rc;
 
     // ---- TDT ----
-    ParakeetCtcModel tdt;
+    DecoderModel tdt;
     if ((rc = load_from_gguf(argv[1], tdt)) != 0) return fail("load_from_gguf(tdt)", rc);
     TdtRuntimeWeights tw;
     if ((rc = tdt_prepare_runtime(tdt, tw, 2 * ft.n + 4)) != 0) return fail("tdt_prepare_runtime", rc);
@@ -324,7 +324,7 @@ int main(int argc, char **argv) {
     printf("},");
 
     // ---- EOU ----
-    ParakeetCtcModel eou;
+    DecoderModel eou;
     if ((rc = load_from_gguf(argv[3], eou)) != 0) return fail("load_from_gguf(eou)", rc);
     EouRuntimeWeights ew;
     if ((rc = eou_prepare_runtime(eou, ew, 2 * fe.n + 4)) != 0) return fail("eou_prepare_runtime", rc);

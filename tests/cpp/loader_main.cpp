@@ -27,8 +27,8 @@ int main(int argc, char **argv) {
         fprintf(stderr, "usage: %s MODEL.gguf [id ...]\n", argv[0]);
         return 2;
     }
-    using namespace parakeet;
-    ParakeetCtcModel m;
+    using namespace parakeet_hip;
+    DecoderModel m;
     const int rc = load_from_gguf(argv[1], m);
     printf("{\"rc\":%d", rc);
     if (rc == 0) {

@@ -50,6 +50,6 @@ def test_decoder_library_exports_device_handoff(pkg):
     if nm is None or not os.path.exists(lib):
         pytest.skip("nm or the built library is missing")
     syms = subprocess.run([nm, "-DC", "--defined-only", lib], capture_output=True, text=True, check=True).stdout
-    for name in ("parakeet::tdt_decode_batch_device(", "parakeet::eou_decode_batch_device(",
-                 "parakeet::Engine::transcribe_device_batch("):
+    for name in ("parakeet_hip::tdt_decode_batch_device(", "parakeet_hip::eou_decode_batch_device(",
+                 "parakeet_hip::Engine::transcribe_device_batch("):
         assert name in syms, name
