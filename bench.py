@@ -36,6 +36,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 
+EXTRAS = ("b1", "b256", "ragged_b512", "tdt11b_f16_b256", "eou_stream_b128")
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -45,6 +48,9 @@ def parse():
     ap.add_argument("--frames", type=int, default=750)
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=EXTRAS, default=None,
+                    help="run one of the other workload shapes alone and print its result (for per-workload "
+                         "kernel traces); the metric line is not produced")
     ap.add_argument("--cpu-utts", type=int, default=64)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run a plain device copy of MIB MiB (calibrates hardware byte counters)")
@@ -261,6 +267,43 @@ def eou_stream_extra(pk, hipmem, roofline, gguf, synth, tmp, B=128, chunks=40, F
             "roofline": {"bound": bound, "t_roof_over_t_kernel": round(t_roof / (loop * 1e-3), 5)}}
 
 
+def run_extra(name, pk, hipmem, roofline, gguf, synth, dec, cost, tmp, D, MS, base, n_b1):
+    """One of the other workload shapes on the q8_0 0.6b decoder `dec` (slots from `base` on),
+    or on a decoder of its own."""
+    if name == "b1":
+        # B=1, T=125 (10 s of audio): per-step latency
+        wl1 = Workload(pk, hipmem, dec, np.full(1, 125), D, MS, n_b1, base)
+        wall1, loop1, enc1, it1 = timed(wl1, 2, 20)
+        st1 = int(wl1.steps().sum())
+        wl1.free()
+        return {"frames": 125, "decode_steps": st1, "us_per_step_loop": round(loop1 * 1e3 / st1, 3),
+                "us_per_step_incl_enc_proj": round((loop1 + enc1) * 1e3 / st1, 3),
+                "us_per_step_wall": round(wall1 / 20 * 1e6 / st1, 3)}
+    base += n_b1
+    if name == "b256":
+        # B=256, T=750: lockstep throughput on the same decoder
+        return lockstep_extra(pk, hipmem, roofline, dec, cost, np.full(256, 750), D, MS, base)
+    base += 256 * 4
+    if name == "ragged_b512":
+        # B=512, T ~ U{50..1500}, blank-logit offsets {0, +2, +4}
+        Tr = synth.ragged_lengths(512)
+        return lockstep_extra(pk, hipmem, roofline, dec, cost, Tr, D, MS, base, blank_bias=synth.blank_offsets(512))
+    if name == "tdt11b_f16_b256":
+        # TDT-1.1b shapes, f16 weights, B=256, T=375
+        p11 = os.path.join(tmp, "tdt-1.1b-f16.gguf")
+        synth.make_shape(p11, "tdt-1.1b")
+        rd11 = gguf.GGUFReader(p11)
+        dec11 = pk.Decoder(rd11, n_slots=256 * 4)
+        cost11 = roofline.DecoderCost(dec11.info, matrix_types(rd11, "tdt"))
+        r = lockstep_extra(pk, hipmem, roofline, dec11, cost11, np.full(256, 375), dec11.info.D, MS, 0)
+        dec11.close()
+        return r
+    if name == "eou_stream_b128":
+        # EOU-120m shapes, q8_0: 128 sessions x 40 chunks of 2 frames, state carried
+        return eou_stream_extra(pk, hipmem, roofline, gguf, synth, tmp)
+    raise ValueError(name)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -296,6 +339,12 @@ def main():
     dec = pk.Decoder(rd, n_slots=B * n_calls + (0 if args.no_extras else n_b1 + 256 * 4 + 512 * 4))
     info = dec.info
     cost = roofline.DecoderCost(info, matrix_types(rd, "tdt"))
+
+    if args.only:
+        r = run_extra(args.only, pk, hipmem, roofline, gguf, synth, dec, cost, tmp, D, MS, B * n_calls, n_b1)
+        print(json.dumps({"workload": args.only, **r}), flush=True)
+        dec.close()
+        return
 
     wl = Workload(pk, hipmem, dec, np.full(B, T), D, MS, n_calls, 0)
     wl.run(trace=True)                                     # untimed: decisions for the cost model
@@ -391,35 +440,11 @@ def main():
                                        sample=(0, 21, 42, 63), max_symbols=MS)
 
     if not args.no_extras:
-        # B=1, T=125 (10 s of audio): per-step latency
-        wl1 = Workload(pk, hipmem, dec, np.full(1, 125), D, MS, n_b1, B * n_calls)
-        wall1, loop1, enc1, it1 = timed(wl1, 2, 20)
-        st1 = int(wl1.steps().sum())
-        out["b1"] = {"frames": 125, "decode_steps": st1, "us_per_step_loop": round(loop1 * 1e3 / st1, 3),
-                     "us_per_step_incl_enc_proj": round((loop1 + enc1) * 1e3 / st1, 3),
-                     "us_per_step_wall": round(wall1 / 20 * 1e6 / st1, 3)}
-        wl1.free()
-        base = B * n_calls + n_b1
-        wl.free()
-        # B=256, T=750: lockstep throughput on the same decoder
-        out["b256"] = lockstep_extra(pk, hipmem, roofline, dec, cost, np.full(256, 750), D, MS, base)
-        base += 256 * 4
-        # B=512, T ~ U{50..1500}, blank-logit offsets {0, +2, +4}
-        Tr = synth.ragged_lengths(512)
-        out["ragged_b512"] = lockstep_extra(pk, hipmem, roofline, dec, cost, Tr, D, MS, base,
-                                             blank_bias=synth.blank_offsets(512))
-        # TDT-1.1b shapes, f16 weights, B=256, T=375
-        p11 = os.path.join(tmp, "tdt-1.1b-f16.gguf")
-        synth.make_shape(p11, "tdt-1.1b")
-        rd11 = gguf.GGUFReader(p11)
-        dec11 = pk.Decoder(rd11, n_slots=256 * 4)
-        cost11 = roofline.DecoderCost(dec11.info, matrix_types(rd11, "tdt"))
-        out["tdt11b_f16_b256"] = lockstep_extra(pk, hipmem, roofline, dec11, cost11, np.full(256, 375),
-                                                dec11.info.D, MS, 0)
-        dec11.close()
-        # EOU-120m shapes, q8_0: 128 sessions x 40 chunks of 2 frames, state carried
-        out["eou_stream_b128"] = eou_stream_extra(pk, hipmem, roofline, gguf, synth, tmp)
-
+        base = B * n_calls
+        for name in EXTRAS:
+            out[name] = run_extra(name, pk, hipmem, roofline, gguf, synth, dec, cost, tmp, D, MS, base, n_b1)
+            if name == "b1":
+                wl.free()   # the B=64 frames are not needed past here
     print(json.dumps(out), flush=True)
     # every device buffer is released before the interpreter exits (no HIP call
     # runs from a finaliser after the runtime has been torn down)

@@ -36,6 +36,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -761,7 +762,15 @@ int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds) {
     void *args[] = {&p};
     const void *fn = reinterpret_cast<const void *>(pkdev::decode_loop_kernel);
     bool &refused = g_loops.coop_refused[dec->device];
-    if (!refused) {
+    // PK_LOOP_DISPATCH=1: ordinary dispatch from the first launch on.  For
+    // profiler runs: rocprofv3 (ROCm 7.2) ends with SIGSEGV in the HIP
+    // runtime's exit-time teardown of any process that made a cooperative
+    // launch, a one-kernel program included; the kernel is the same either way.
+    static const bool force_dispatch = [] {
+        const char *v = std::getenv("PK_LOOP_DISPATCH");
+        return v && v[0] == '1';
+    }();
+    if (!refused && !force_dispatch) {
         const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(nwg), dim3(kBlock), args, lds, dec->stream);
         if (e != hipErrorIllegalState) {
             HIP_TRY(e);
