@@ -7,7 +7,9 @@
  *   pk_decoder_create   <- tdt_prepare_runtime (src/parakeet_tdt.cpp:585-718)
  *                          and eou_prepare_runtime (src/parakeet_eou.cpp:172-204):
  *                          uploads the GGUF decoder tensors once, q8_0/f16 kept
- *                          at their stored precision.
+ *                          at their stored precision (q4_0 / q5_0 blocks become
+ *                          q8_0 blocks with the same scale: their weights are
+ *                          exact int8 values).
  *   pk_decoder_destroy  <- ~TdtRuntimeWeights (src/parakeet_tdt.cpp:560-583)
  *   pk_slot_init        <- tdt_init_state (src/parakeet_tdt.cpp:813-863),
  *                          eou_init_state (src/parakeet_eou.cpp:206-230)
@@ -46,7 +48,7 @@ extern "C" {
 #define PK_MAX_BATCH 512   /* utterances per pk_decode call */
 
 enum { PK_KIND_TDT = 0, PK_KIND_EOU = 1 };
-enum { PK_TYPE_F32 = 0, PK_TYPE_F16 = 1, PK_TYPE_Q8_0 = 8 };   /* ggml type ids */
+enum { PK_TYPE_F32 = 0, PK_TYPE_F16 = 1, PK_TYPE_Q4_0 = 2, PK_TYPE_Q5_0 = 6, PK_TYPE_Q8_0 = 8 };   /* ggml type ids */
 /* pk_batch.mem: where the frames and the outputs live.
  *   PK_MEM_HOST           frames and outputs in host memory (frames uploaded per call)
  *   PK_MEM_DEVICE         frames and outputs in device memory
@@ -72,7 +74,7 @@ enum {
 /* One GGUF tensor as stored: ne0 = innermost (in) length, ne1 = rows (out). */
 typedef struct pk_tensor {
     const void *data;   /* host pointer to the stored bytes */
-    int32_t type;       /* PK_TYPE_* */
+    int32_t type;       /* PK_TYPE_*: f32 / f16 / q4_0 / q5_0 / q8_0 (biases f32 / f16) */
     int64_t ne0;
     int64_t ne1;        /* 1 for vectors */
 } pk_tensor;

@@ -73,8 +73,15 @@ float ora_f16_to_f32(uint16_t h) {
     return f;
 }
 
-/* ggml to_float as used by dequantize_to_f32 (src/parakeet_tdt.cpp:78-95):
- * type 0 = f32 copy, 1 = f16, 8 = q8_0 blocks {f16 d; int8 q[32]} -> q*d. */
+/* ggml to_float as used by dequantize_to_f32 (src/parakeet_tdt.cpp:78-95).
+ * ggml is not vendored in the reference (scripts/setup-ggml.sh:32 pins upstream
+ * commit 58c38058); its published block formats, 32 weights per block:
+ *   type 0 = f32 copy, 1 = f16,
+ *   8 = q8_0 {f16 d; int8 q[32]}              -> q*d,
+ *   6 = q5_0 {f16 d; u8 qh[4]; u8 qs[16]}     -> ((nibble | bit << 4) - 16)*d,
+ *   2 = q4_0 {f16 d; u8 qs[16]}               -> (nibble - 8)*d,
+ * where weight j (< 16) takes the low nibble of qs[j] and bit j of qh, and
+ * weight j + 16 the high nibble of qs[j] and bit j + 16 of qh (little endian). */
 void ora_dequant(const void *src, int ggml_type, int64_t n, float *dst) {
     if (ggml_type == 0) {
         memcpy(dst, src, (size_t)n * sizeof(float));
@@ -89,6 +96,27 @@ void ora_dequant(const void *src, int ggml_type, int64_t n, float *dst) {
             const float d = ora_f16_to_f32(dh);
             const int8_t *q = (const int8_t *)(s + 34 * b + 2);
             for (int j = 0; j < 32; ++j) dst[32 * b + j] = q[j] * d;
+        }
+    } else if (ggml_type == 6 || ggml_type == 2) {
+        const int five = ggml_type == 6, bytes = five ? 22 : 18;
+        const uint8_t *s = (const uint8_t *)src;
+        for (int64_t b = 0; b < n / 32; ++b) {
+            const uint8_t *blk = s + (size_t)bytes * b;
+            uint16_t dh;
+            memcpy(&dh, blk, 2);
+            const float d = ora_f16_to_f32(dh);
+            uint32_t qh = 0;
+            const uint8_t *qs = blk + 2;
+            if (five) {
+                qh = (uint32_t)blk[2] | (uint32_t)blk[3] << 8 | (uint32_t)blk[4] << 16 | (uint32_t)blk[5] << 24;
+                qs = blk + 6;
+            }
+            for (int j = 0; j < 16; ++j) {
+                const int lo = (qs[j] & 15) | (int)((qh >> j) & 1u) << 4;
+                const int hi = (qs[j] >> 4) | (int)((qh >> (j + 16)) & 1u) << 4;
+                dst[32 * b + j] = (float)(lo - (five ? 16 : 8)) * d;
+                dst[32 * b + j + 16] = (float)(hi - (five ? 16 : 8)) * d;
+            }
         }
     }
 }

@@ -84,7 +84,7 @@ int  ora_argmax(const float *data, int n);
 /* src/parakeet_tdt.cpp:47-68 */
 void ora_gemv(const float *W, const float *x, const float *b, float *y, int out_dim, int in_dim);
 void ora_gemv_add(const float *W, const float *x, float *y, int out_dim, int in_dim);
-/* ggml to_float for f16 and q8_0, as called at src/parakeet_tdt.cpp:86-94 */
+/* ggml to_float for f16, q8_0, q5_0 and q4_0, as called at src/parakeet_tdt.cpp:86-94 */
 float ora_f16_to_f32(uint16_t h);
 void ora_dequant(const void *src, int ggml_type, int64_t n, float *dst);
 /* src/parakeet_tdt.cpp:106-142 (TDT) == src/parakeet_eou.cpp:78-116 (EOU) */

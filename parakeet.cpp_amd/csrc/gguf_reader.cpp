@@ -70,15 +70,20 @@ bool read_value(Cursor &c, uint32_t t, Value &v) {
         v.arr_type = c.get<uint32_t>();
         const uint64_t n = c.get<uint64_t>();
         if (!c.ok) return false;
+        // an element takes at least its size in the file (a string its 8-byte
+        // length), so a count past what remains is a corrupt header
+        const uint64_t left = (uint64_t)(c.end - c.p);
         if (v.arr_type == T_STR) {
+            if (n > left / 8) return false;
             v.arr_s.reserve(n);
             for (uint64_t i = 0; i < n && c.ok; ++i) v.arr_s.push_back(c.str());
         } else if (v.arr_type == T_F32 || v.arr_type == T_F64) {
             const size_t sz = scalar_size(v.arr_type);
-            if ((uint64_t)(c.end - c.p) < n * sz) return false;
+            if (n > left / sz) return false;
             c.p += n * sz;   // float arrays are not used by the decoder
         } else {
-            if (scalar_size(v.arr_type) == 0) return false;
+            const size_t sz = scalar_size(v.arr_type);
+            if (sz == 0 || n > left / sz) return false;
             v.arr_i.reserve(n);
             for (uint64_t i = 0; i < n && c.ok; ++i) v.arr_i.push_back(read_int(c, v.arr_type));
         }
@@ -91,10 +96,15 @@ bool read_value(Cursor &c, uint32_t t, Value &v) {
 }  // namespace
 
 uint64_t tensor_nbytes(uint32_t type, int64_t n) {
+    if (n < 0) return 0;
+    const uint64_t blocks = (uint64_t)n / 32;
+    const bool whole = n % 32 == 0;
     switch (type) {
-        case 0: return 4ull * n;
-        case 1: return 2ull * n;
-        case 8: return (uint64_t)(n / 32) * 34ull;
+        case 0: return 4ull * (uint64_t)n;
+        case 1: return 2ull * (uint64_t)n;
+        case 2: return whole ? blocks * 18ull : 0;   // q4_0 {f16 d; u8 qs[16]}
+        case 6: return whole ? blocks * 22ull : 0;   // q5_0 {f16 d; u8 qh[4]; u8 qs[16]}
+        case 8: return whole ? blocks * 34ull : 0;   // q8_0 {f16 d; i8 q[32]}
         default: return 0;
     }
 }
@@ -103,6 +113,7 @@ int File::open(const std::string &path, std::string &err) {
     std::ifstream f(path, std::ios::binary | std::ios::ate);
     if (!f) { err = "cannot open " + path; return 1; }
     const std::streamsize size = f.tellg();
+    if (size < 0) { err = "cannot size " + path; return 1; }
     f.seekg(0);
     bytes_.resize((size_t)size);
     if (!f.read(reinterpret_cast<char *>(bytes_.data()), size)) { err = "short read " + path; return 1; }
@@ -121,14 +132,21 @@ int File::open(const std::string &path, std::string &err) {
         kv_[key] = std::move(v);
     }
     uint64_t align = 32;
-    if (const Value *a = find("general.alignment")) align = (uint64_t)a->i;
+    if (const Value *a = find("general.alignment")) {
+        if (a->i < 1 || a->i > (1 << 20)) { err = "bad general.alignment"; return 1; }
+        align = (uint64_t)a->i;
+    }
     std::vector<Tensor> infos;
     for (uint64_t i = 0; i < n_tensors && c.ok; ++i) {
         Tensor t;
         t.name = c.str();
         const uint32_t nd = c.get<uint32_t>();
         if (nd > 4) { err = "tensor rank > 4"; return 1; }
-        for (uint32_t d = 0; d < nd; ++d) t.ne.push_back((int64_t)c.get<uint64_t>());
+        for (uint32_t d = 0; d < nd; ++d) {
+            const uint64_t v = c.get<uint64_t>();
+            if (v > (1ull << 32)) { err = "tensor dimension out of range"; return 1; }
+            t.ne.push_back((int64_t)v);
+        }
         t.type = c.get<uint32_t>();
         t.offset = c.get<uint64_t>();
         infos.push_back(std::move(t));
@@ -137,10 +155,15 @@ int File::open(const std::string &path, std::string &err) {
     const uint64_t base = ((uint64_t)(c.p - bytes_.data()) + align - 1) / align * align;
     for (auto &t : infos) {
         int64_t n = 1;
-        for (int64_t v : t.ne) n *= v;
+        for (int64_t v : t.ne) {
+            n *= v;
+            if (n > (1ll << 40)) { err = "tensor " + t.name + " too large"; return 1; }
+        }
         t.nbytes = tensor_nbytes(t.type, n);
+        const uint64_t size = bytes_.size();
+        if (t.offset > size || base > size - t.offset) { err = "tensor " + t.name + " out of file bounds"; return 1; }
         t.offset += base;
-        if (t.nbytes == 0 || t.offset + t.nbytes > bytes_.size()) {
+        if (t.nbytes == 0 || t.nbytes > size - t.offset) {
             err = "tensor " + t.name + " out of file bounds or of unsupported type";
             return 1;
         }

@@ -3,7 +3,7 @@
 // Reads the metadata and tensor directory of a GGUF file and keeps the file
 // bytes in memory.  Covers what the reference's loader reads for the
 // transducer decoders (src/parakeet_ctc.cpp:297-682): scalar / string / array
-// metadata and f32 / f16 / q8_0 tensors (ggml type ids 0, 1, 8).
+// metadata and f32 / f16 / q4_0 / q5_0 / q8_0 tensors (ggml type ids 0, 1, 2, 6, 8).
 #pragma once
 
 #include <cstdint>

@@ -142,27 +142,61 @@ struct HostBuf {
     template <class T> T *as() const { return static_cast<T *>(p); }
 };
 
+// Block-quantized ggml types: 32 weights per block, one f16 scale d, weight = d * q.
+//   q8_0 {f16 d; int8 q[32]}                      q in -128 .. 127 (34 bytes)
+//   q5_0 {f16 d; u8 qh[4]; u8 qs[16]}             q = (nibble | high bit << 4) - 16 (22 bytes)
+//   q4_0 {f16 d; u8 qs[16]}                       q = nibble - 8 (18 bytes)
+// Nibbles: qs[j] & 15 is weight j, qs[j] >> 4 is weight j + 16; bit j of the
+// little-endian word qh is the high bit of weight j (ggml's block formats; the
+// reference converter writes all three, scripts/convert-nemo-to-gguf.py:90-103).
+bool quantized(int type) { return type == PK_TYPE_Q8_0 || type == PK_TYPE_Q5_0 || type == PK_TYPE_Q4_0; }
+int block_bytes(int type) { return type == PK_TYPE_Q8_0 ? 34 : type == PK_TYPE_Q5_0 ? 22 : 18; }
+
+// One block as its scale bits and 32 exact int8 weights: q4_0 and q5_0 blocks
+// become q8_0 blocks with the same scale, so the device runs one exact path.
+void block_q(const uint8_t *blk, int type, uint16_t &dh, int8_t (&q)[32]) {
+    memcpy(&dh, blk, 2);
+    if (type == PK_TYPE_Q8_0) {
+        memcpy(q, blk + 2, 32);
+        return;
+    }
+    uint32_t qh = 0;
+    const uint8_t *qs = blk + 2;
+    if (type == PK_TYPE_Q5_0) {
+        memcpy(&qh, blk + 2, 4);
+        qs = blk + 6;
+    }
+    const int bias = type == PK_TYPE_Q5_0 ? 16 : 8;
+    for (int j = 0; j < 16; ++j) {
+        const int lo = (qs[j] & 15) | (int)(((qh >> j) & 1u) << 4);
+        const int hi = (qs[j] >> 4) | (int)(((qh >> (j + 16)) & 1u) << 4);
+        q[j] = (int8_t)(lo - bias);
+        q[j + 16] = (int8_t)(hi - bias);
+    }
+}
+
 int check_tensor(const pk_tensor &t, int rows, int cols, const char *name) {
     if (!t.data) return fail(PK_ERR_TENSOR, "missing tensor %s", name);
     if (t.ne0 != cols || t.ne1 != rows)
         return fail(PK_ERR_TENSOR, "%s: ne=[%lld,%lld], expected [%d,%d]", name, (long long)t.ne0, (long long)t.ne1,
                     cols, rows);
-    if (t.type != PK_TYPE_F32 && t.type != PK_TYPE_F16 && t.type != PK_TYPE_Q8_0)
+    if (t.type != PK_TYPE_F32 && t.type != PK_TYPE_F16 && !quantized(t.type))
         return fail(PK_ERR_UNSUPPORTED, "%s: ggml type %d not supported", name, t.type);
-    if (t.type == PK_TYPE_Q8_0 && cols % 32) return fail(PK_ERR_TENSOR, "%s: q8_0 row length %d", name, cols);
+    if (quantized(t.type) && cols % 32) return fail(PK_ERR_TENSOR, "%s: block-quantized row length %d", name, cols);
     return 0;
 }
 
-// Stored row sr of a tensor as f32 (ggml to_float: q8_0 -> d*q, f16 -> f32).
+// Stored row sr of a tensor as f32 (ggml to_float: d*q per block, f16 -> f32).
 void row_f32(const pk_tensor &t, int cols, int sr, float *out) {
     const uint8_t *src = static_cast<const uint8_t *>(t.data);
-    if (t.type == PK_TYPE_Q8_0) {
-        const uint8_t *row = src + (size_t)sr * (cols / 32) * 34;
+    if (quantized(t.type)) {
+        const int bb = block_bytes(t.type);
+        const uint8_t *row = src + (size_t)sr * (cols / 32) * bb;
         for (int b = 0; b < cols / 32; ++b) {
             uint16_t dh;
-            memcpy(&dh, row + 34 * b, 2);
+            int8_t q[32];
+            block_q(row + (size_t)bb * b, t.type, dh, q);
             const float d = f16_to_f32(dh);
-            const int8_t *q = reinterpret_cast<const int8_t *>(row + 34 * b + 2);
             for (int j = 0; j < 32; ++j) out[32 * b + j] = (float)q[j] * d;
         }
     } else if (t.type == PK_TYPE_F16) {
@@ -204,28 +238,30 @@ struct HostTiled {
 int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *map, HostTiled &out, const char *name) {
     if (int rc = check_tensor(t, rows, cols, name)) return rc;
     if (cols % 32) return fail(PK_ERR_UNSUPPORTED, "%s: row length %d not a multiple of 32", name, cols);
-    out.type = t.type;
+    out.type = quantized(t.type) ? PK_TYPE_Q8_0 : t.type;   // q4_0 / q5_0 repacked exactly as q8_0
     out.rows = rows;
     out.tiles = (rows + kTile - 1) / kTile;
     out.KB = cols / 32;
     const size_t frags = (size_t)out.tiles * out.KB;
     const uint8_t *src = static_cast<const uint8_t *>(t.data);
-    if (t.type == PK_TYPE_Q8_0) {
+    if (quantized(t.type)) {
+        const int bb = block_bytes(t.type);
         out.a.assign(frags * kWave * 8, 0);
         out.scale.assign(frags * kTile, 0);
         for (int tile = 0; tile < out.tiles; ++tile)
             for (int r = 0; r < kTile; ++r) {
                 const int row = tile * kTile + r;
                 if (row >= rows) continue;
-                const uint8_t *srow = src + (size_t)(map ? (*map)[row] : row) * out.KB * 34;
+                const uint8_t *srow = src + (size_t)(map ? (*map)[row] : row) * out.KB * bb;
                 for (int kb = 0; kb < out.KB; ++kb) {
                     const size_t f = (size_t)tile * out.KB + kb;
                     uint16_t dh;
-                    memcpy(&dh, srow + 34 * kb, 2);
+                    int8_t q[32];
+                    block_q(srow + (size_t)bb * kb, t.type, dh, q);
                     out.scale[f * kTile + r] = dh;
                     for (int g = 0; g < 4; ++g)   // lane r + 16 g holds q[8g .. 8g+8) as q ^ 0x80
                         for (int i = 0; i < 8; ++i)
-                            out.a[(f * kWave + r + 16 * g) * 8 + i] = srow[34 * kb + 2 + 8 * g + i] ^ 0x80;
+                            out.a[(f * kWave + r + 16 * g) * 8 + i] = (uint8_t)q[8 * g + i] ^ 0x80;
                 }
             }
     } else {

@@ -1,7 +1,8 @@
 """Minimal GGUF v3 reader/writer for parakeet decoder checkpoints.
 
 Implements the subset of the GGUF container used by parakeet.cpp decoder
-GGUFs: scalar/string/array metadata and f32 / f16 / q8_0 tensors.  The
+GGUFs: scalar/string/array metadata and f32 / f16 / q8_0 / q5_0 / q4_0
+tensors (the five ``--quant`` choices of scripts/convert-nemo-to-gguf.py:90-103).  The
 tensor naming, shapes and the q8_0-when-``in % 32 == 0`` rule follow the
 reference converter (scripts/convert-nemo-to-gguf.py:405-413, 506-525,
 563-582); the metadata keys follow its writer (:293-352) and the reader's
@@ -24,9 +25,16 @@ import numpy as np
 
 GGML_F32 = 0
 GGML_F16 = 1
+GGML_Q4_0 = 2
+GGML_Q5_0 = 6
 GGML_Q8_0 = 8
 QK8_0 = 32
 Q8_0_BLOCK_BYTES = 34
+# 32-weight blocks of ggml's block-quantized types (ggml, pinned by the reference at commit
+# 58c38058, scripts/setup-ggml.sh:32): q8_0 {f16 d; i8 q[32]}, q5_0 {f16 d; u8 qh[4]; u8 qs[16]},
+# q4_0 {f16 d; u8 qs[16]}
+BLOCK_BYTES = {GGML_Q8_0: 34, GGML_Q5_0: 22, GGML_Q4_0: 18}
+QUANT_TYPES = {"q8_0": GGML_Q8_0, "q5_0": GGML_Q5_0, "q4_0": GGML_Q4_0}
 
 # GGUF metadata value types
 T_U8, T_I8, T_U16, T_I16, T_U32, T_I32, T_F32, T_BOOL, T_STR, T_ARR, T_U64, T_I64, T_F64 = range(13)
@@ -42,10 +50,10 @@ def tensor_nbytes(ggml_type: int, n_elements: int) -> int:
         return 4 * n_elements
     if ggml_type == GGML_F16:
         return 2 * n_elements
-    if ggml_type == GGML_Q8_0:
+    if ggml_type in BLOCK_BYTES:
         if n_elements % QK8_0:
-            raise ValueError("q8_0 tensor size must be a multiple of 32")
-        return (n_elements // QK8_0) * Q8_0_BLOCK_BYTES
+            raise ValueError("block-quantized tensor size must be a multiple of 32")
+        return (n_elements // QK8_0) * BLOCK_BYTES[ggml_type]
     raise ValueError(f"unsupported ggml type {ggml_type}")
 
 
@@ -65,18 +73,80 @@ def quantize_q8_0(x: np.ndarray) -> bytes:
     return out.tobytes()
 
 
+def _blocks(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if x.shape[-1] % QK8_0:
+        raise ValueError("block quantization needs the innermost dimension to be a multiple of 32")
+    return x.reshape(-1, QK8_0)
+
+
+def _signed_absmax(blocks: np.ndarray) -> np.ndarray:
+    """Per block, the element of largest magnitude with its sign (the first one on ties)."""
+    return blocks[np.arange(blocks.shape[0]), np.abs(blocks).argmax(axis=1)]
+
+
+def quantize_q4_0(x: np.ndarray) -> bytes:
+    """ggml's reference q4_0 rule: d = max / -8 (max: the signed value of largest magnitude),
+    q = min(15, trunc(x / d + 8.5)); weight j in the low nibble of qs[j], weight j + 16 in the
+    high nibble."""
+    b = _blocks(x)
+    d = (_signed_absmax(b) / np.float32(-8.0)).astype(np.float32)
+    inv = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, np.float32(1.0)), np.float32(0.0))
+    q = np.minimum(15, np.trunc(b * inv[:, None].astype(np.float32) + np.float32(8.5))).astype(np.uint8)
+    out = np.empty((b.shape[0], BLOCK_BYTES[GGML_Q4_0]), dtype=np.uint8)
+    out[:, 0:2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = q[:, :16] | (q[:, 16:] << 4)
+    return out.tobytes()
+
+
+def quantize_q5_0(x: np.ndarray) -> bytes:
+    """ggml's reference q5_0 rule: d = max / -16, q = min(31, trunc(x / d + 16.5)); low 4 bits
+    packed as in q4_0, bit 4 of weight j is bit j of the little-endian word qh."""
+    b = _blocks(x)
+    d = (_signed_absmax(b) / np.float32(-16.0)).astype(np.float32)
+    inv = np.where(d != 0, np.float32(1.0) / np.where(d != 0, d, np.float32(1.0)), np.float32(0.0))
+    q = np.minimum(31, np.trunc(b * inv[:, None].astype(np.float32) + np.float32(16.5))).astype(np.uint32)
+    qh = ((q >> 4) & 1) << np.arange(32, dtype=np.uint32)
+    qh = np.bitwise_or.reduce(qh, axis=1).astype(np.uint32)
+    out = np.empty((b.shape[0], BLOCK_BYTES[GGML_Q5_0]), dtype=np.uint8)
+    out[:, 0:2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    out[:, 2:6] = qh.astype("<u4").view(np.uint8).reshape(-1, 4)
+    out[:, 6:] = ((q[:, :16] & 15) | ((q[:, 16:] & 15) << 4)).astype(np.uint8)
+    return out.tobytes()
+
+
+QUANTIZE = {GGML_Q8_0: quantize_q8_0, GGML_Q5_0: quantize_q5_0, GGML_Q4_0: quantize_q4_0}
+
+
+def block_ints(raw: bytes | np.ndarray, ggml_type: int, n_blocks: int) -> tuple[np.ndarray, np.ndarray]:
+    """Scales (float32) and integer weights [n_blocks, 32] of a block-quantized buffer."""
+    buf = np.frombuffer(raw, dtype=np.uint8) if not isinstance(raw, np.ndarray) else raw.view(np.uint8)
+    blocks = buf[: n_blocks * BLOCK_BYTES[ggml_type]].reshape(n_blocks, BLOCK_BYTES[ggml_type])
+    d = blocks[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1)
+    if ggml_type == GGML_Q8_0:
+        return d, blocks[:, 2:].view(np.int8).astype(np.int32)
+    if ggml_type == GGML_Q5_0:
+        qh = blocks[:, 2:6].copy().view("<u4").astype(np.uint32).reshape(-1, 1)
+        qs = blocks[:, 6:].astype(np.int32)
+        hi = ((qh >> np.arange(32, dtype=np.uint32)) & 1).astype(np.int32) << 4
+        q = np.concatenate([qs & 15, qs >> 4], axis=1) | hi
+        return d, q - 16
+    qs = blocks[:, 2:].astype(np.int32)
+    return d, np.concatenate([qs & 15, qs >> 4], axis=1) - 8
+
+
 def dequantize(raw: bytes | np.ndarray, ggml_type: int, n_elements: int) -> np.ndarray:
-    """ggml ``to_float`` for the three supported types (float32 result)."""
+    """ggml ``to_float`` for the supported types (float32 result)."""
     buf = np.frombuffer(raw, dtype=np.uint8) if not isinstance(raw, np.ndarray) else raw.view(np.uint8)
     if ggml_type == GGML_F32:
         return buf.view(np.float32)[:n_elements].copy()
     if ggml_type == GGML_F16:
         return buf.view(np.float16)[:n_elements].astype(np.float32)
-    if ggml_type == GGML_Q8_0:
-        blocks = buf[: tensor_nbytes(GGML_Q8_0, n_elements)].reshape(-1, Q8_0_BLOCK_BYTES)
-        d = blocks[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1)
-        q = blocks[:, 2:].view(np.int8).astype(np.float32)
-        return (q * d[:, None]).reshape(-1)
+    if ggml_type in BLOCK_BYTES:
+        if n_elements % QK8_0:
+            raise ValueError("block-quantized tensor size must be a multiple of 32")
+        d, q = block_ints(buf, ggml_type, n_elements // QK8_0)
+        return (q.astype(np.float32) * d[:, None]).reshape(-1)
     raise ValueError(f"unsupported ggml type {ggml_type}")
 
 

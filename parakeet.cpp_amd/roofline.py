@@ -25,9 +25,14 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 FP32_PEAK_TFLOPS = 157.3       # MI355X fp32 (vector and matrix), TFLOP/s
 
 
+BLOCK_BYTES = {8: 34, 6: 22, 2: 18}   # q8_0, q5_0, q4_0: bytes per 32 stored weights
+
+
 def wbytes(rows: int, cols: int, ggml_type: int) -> int:
-    if ggml_type == 8:
-        return rows * (cols // 32) * 34
+    """Stored bytes of a matrix (the algorithmic weight bytes; q5_0 / q4_0 are read as
+    their exact q8_0 repacking, 34 bytes per block)."""
+    if ggml_type in BLOCK_BYTES:
+        return rows * (cols // 32) * BLOCK_BYTES[ggml_type]
     return rows * cols * (2 if ggml_type == 1 else 4)
 
 

@@ -4,9 +4,9 @@ Writes decoder-only GGUFs in the reference converter's layout
 (scripts/convert-nemo-to-gguf.py:293-352 metadata, :506-525 EOU tensors,
 :563-582 TDT tensors) with random weights N(0, 1/sqrt(fan_in)), fan_in being
 the ``in`` dimension of each matrix (the embedding uses its row length H).
-Biases are drawn the same way and stored f32.  Matrices are q8_0 when
-``in % 32 == 0`` (otherwise f16), or f16 / f32 for those quantisation modes,
-as in the converter's ``add_2d``.
+Biases are drawn the same way and stored f32.  Matrices are q8_0 / q5_0 /
+q4_0 when ``in % 32 == 0`` (otherwise f16), or f16 / f32 for those
+quantisation modes, as in the converter's ``add_2d``.
 
 The files carry only the prediction/joint network: the encoder is not part of
 the decode path and its tensors are absent (readers run in decoder-only mode).
@@ -32,8 +32,9 @@ SHAPES = {
 
 def _matrix(w: G.GGUFWriter, name: str, arr: np.ndarray, quant: str):
     out_dim, in_dim = arr.shape
-    if quant == "q8_0" and in_dim % 32 == 0:
-        w.add_tensor(name, G.quantize_q8_0(arr), (in_dim, out_dim), G.GGML_Q8_0)
+    if quant in G.QUANT_TYPES and in_dim % 32 == 0:
+        t = G.QUANT_TYPES[quant]
+        w.add_tensor(name, G.QUANTIZE[t](arr), (in_dim, out_dim), t)
     elif quant == "f32":
         w.add_tensor(name, arr.astype(np.float32).tobytes(), (in_dim, out_dim), G.GGML_F32)
     else:

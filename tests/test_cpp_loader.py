@@ -134,3 +134,17 @@ def test_detokenize(tmp_path):
     assert _load(p, 8)["detok"] == "x" and _load(p, 9)["detok"] == "y "    # leading trimmed, trailing kept
     assert _load(p, 11, 11, 10)["detok"] == "\xe9"
     assert _load(p)["detok"] == ""
+
+
+@pytest.mark.parametrize("quant", ["q4_0", "q5_0", "q8_0"])
+def test_block_quantized_files_load(tmp_path, quant):
+    """Decoder GGUFs with q4_0 / q5_0 / q8_0 matrices (18 / 22 / 34 bytes per 32 weights):
+    the reader sizes every tensor from its type, so the whole file loads; the same file cut
+    by one byte does not (its last tensor runs past the end)."""
+    path = str(tmp_path / "m.gguf")
+    small_tdt(path, quant=quant)
+    assert _load(path)["rc"] == 0
+    raw = open(path, "rb").read()
+    cut = str(tmp_path / "cut.gguf")
+    open(cut, "wb").write(raw[:-1])
+    assert _load(cut)["rc"] == 1

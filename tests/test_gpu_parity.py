@@ -1,6 +1,6 @@
 """Device decode vs oracle: tokens/durations per step (teacher-forced replay,
 zero unexplained mismatches), final LSTM state within 1e-3, across TDT and
-EOU decoders, q8_0 / f16 / f32 weights, batches, streaming windows."""
+EOU decoders, q8_0 / q5_0 / q4_0 / f16 / f32 weights, batches, streaming windows."""
 import os
 
 import numpy as np
@@ -19,7 +19,7 @@ def _models(path, writer, **kw):
     return pk.Decoder.from_gguf(path, n_slots=8), oracle.OracleModel.from_gguf(path, gguf)
 
 
-@pytest.mark.parametrize("quant", ["q8_0", "f16", "f32"])
+@pytest.mark.parametrize("quant", ["q8_0", "f16", "f32", "q5_0", "q4_0"])
 def test_tdt_small_batch(tmp_path, quant):
     from parakeet_amd import synth
     dev, om = _models(str(tmp_path / "m.gguf"), small_tdt, quant=quant)
@@ -42,9 +42,10 @@ def test_tdt_free_run_matches(tmp_path):
     dev.close()
 
 
-def test_eou_small_batch(tmp_path):
+@pytest.mark.parametrize("quant", ["q8_0", "q5_0", "q4_0"])
+def test_eou_small_batch(tmp_path, quant):
     from parakeet_amd import synth
-    dev, om = _models(str(tmp_path / "e.gguf"), small_eou)
+    dev, om = _models(str(tmp_path / "e.gguf"), small_eou, quant=quant)
     encs = [synth.encoder_frames(200 + u, T, 64) for u, T in enumerate([5, 17, 2, 30])]
     res = dev.decode(encs, trace=True, max_symbols=5)
     for u, enc in enumerate(encs):
@@ -66,4 +67,22 @@ def test_tdt_06b_b1(tmp_path):
     st = om.new_state()
     stats = check_window(om, dev, 0, enc, res, st, 10)
     print("tdt-0.6b B=1:", res["steps"], "steps", stats)
+    dev.close()
+
+
+@pytest.mark.parametrize("quant", ["q5_0", "q4_0"])
+def test_tdt_06b_block_quant(tmp_path, quant):
+    """TDT-0.6b-v3 shapes with q5_0 / q4_0 matrices (the reference converter's --quant
+    choices): B=4 x 60 frames, every utterance replayed through the oracle."""
+    from parakeet_amd import gguf, pk, synth
+    import oracle
+    path = str(tmp_path / f"tdt06-{quant}.gguf")
+    synth.make_shape(path, "tdt-0.6b-v3", quant=quant)
+    dev = pk.Decoder.from_gguf(path, n_slots=4)
+    om = oracle.OracleModel.from_gguf(path, gguf)
+    encs = [synth.encoder_frames(300 + u, 60, 1024) for u in range(4)]
+    print(f"tdt-0.6b {quant}: B=4 T=60", flush=True)
+    res = dev.decode(encs, trace=True, max_symbols=10)
+    for u, enc in enumerate(encs):
+        check_window(om, dev, u, enc, res[u], om.new_state(), 10)
     dev.close()

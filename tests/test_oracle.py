@@ -53,6 +53,90 @@ def test_q8_0_quantizer_roundtrip(pkg):
     assert np.all(err <= amax / 127 * 0.5 * 1.01 + 1e-7)
 
 
+def _blocks(d, body):
+    """Raw blocks: f16 scale d then the body bytes of each block."""
+    d = np.asarray(d, np.float16)
+    body = np.asarray(body, np.uint8)
+    return np.concatenate([d.view(np.uint8).reshape(-1, 2), body], axis=1)
+
+
+def _oracle_dequant(oracle_mod, raw, t, n):
+    out = np.zeros(n, np.float32)
+    raw = np.ascontiguousarray(raw)
+    oracle_mod.lib().ora_dequant(raw.ctypes.data, t, n, oracle_mod.fptr(out))
+    return out
+
+
+def test_q4_0_dequant_known_blocks(oracle_mod, pkg):
+    """q4_0 {f16 d; u8 qs[16]}: weight j = (low nibble of qs[j] - 8) d, weight j+16 = (high
+    nibble - 8) d.  Each block has one obvious answer: all-zero bytes give -8d, all-0xFF
+    give +7d, low nibble 1 / high nibble 2 give -7d then -6d (a swap of the halves fails),
+    and nibble j in the low half with 15-j in the high half walks -8..7 then 7..-8."""
+    from parakeet_amd import gguf
+    qs = np.stack([np.zeros(16), np.full(16, 0xFF), np.full(16, 0x21),
+                   np.arange(16) | ((15 - np.arange(16)) << 4)]).astype(np.uint8)
+    raw = _blocks([0.5, 2.0, -0.25, 1.0], qs)
+    want = np.concatenate([np.full(32, -4.0), np.full(32, 14.0),
+                           np.r_[np.full(16, 1.75), np.full(16, 1.5)],
+                           np.r_[np.arange(-8, 8), np.arange(7, -9, -1)]]).astype(np.float32)
+    assert np.array_equal(_oracle_dequant(oracle_mod, raw, 2, 128), want)
+    assert np.array_equal(gguf.dequantize(raw.tobytes(), gguf.GGML_Q4_0, 128), want)
+
+
+def test_q5_0_dequant_known_blocks(oracle_mod, pkg):
+    """q5_0 {f16 d; u8 qh[4]; u8 qs[16]}: weight j = ((nibble | bit j of qh << 4) - 16) d, the
+    high nibbles and bits 16..31 of qh for weights 16..31.  All-zero gives -16d, all-ones
+    +15d; qh = 0x0000FFFF (only the first half high) gives 0 then -16d; qh = 0x00010000
+    raises weight 16 alone (a wrong bit index or half fails)."""
+    from parakeet_amd import gguf
+    def body(qh, qs):
+        return np.concatenate([np.frombuffer(np.uint32(qh).tobytes(), np.uint8), np.full(16, qs, np.uint8)])
+    raw = _blocks([1.0, 0.5, 2.0, 1.0], np.stack([body(0, 0), body(0xFFFFFFFF, 0xFF), body(0x0000FFFF, 0),
+                                                    body(0x00010000, 0)]))
+    want = np.concatenate([np.full(32, -16.0), np.full(32, 7.5), np.r_[np.zeros(16), np.full(16, -32.0)],
+                           np.r_[np.full(16, -16.0), [0.0], np.full(15, -16.0)]]).astype(np.float32)
+    assert np.array_equal(_oracle_dequant(oracle_mod, raw, 6, 128), want)
+    assert np.array_equal(gguf.dequantize(raw.tobytes(), gguf.GGML_Q5_0, 128), want)
+
+
+@pytest.mark.parametrize("qtype,lo,hi", [(2, -8, 7), (6, -16, 15)])
+def test_q4_q5_quantizer_exact_on_grid(oracle_mod, pkg, qtype, lo, hi):
+    """Values k*d with k in the type's integer range and one element at the most negative k:
+    the reference rule d = max / lo recovers d exactly (d a power of two), so quantize then
+    dequantize returns the input bit for bit, through the Python and the C paths alike."""
+    from parakeet_amd import gguf
+    rng = np.random.default_rng(qtype)
+    k = rng.integers(lo, hi + 1, size=(6, 32))
+    k[:, 5] = lo
+    d = 2.0 ** rng.integers(-6, 3, size=(6, 1))
+    x = (k * d).astype(np.float32)
+    raw = gguf.QUANTIZE[qtype](x)
+    assert len(raw) == 6 * gguf.BLOCK_BYTES[qtype]
+    assert np.array_equal(gguf.dequantize(raw, qtype, x.size).reshape(x.shape), x)
+    assert np.array_equal(_oracle_dequant(oracle_mod, np.frombuffer(raw, np.uint8), qtype, x.size).reshape(x.shape), x)
+
+
+@pytest.mark.parametrize("qtype,levels", [(2, 8), (6, 16)])
+def test_q4_q5_quantizer_error_bound_and_paths_agree(oracle_mod, pkg, qtype, levels):
+    """Random rows: every weight within half a step of its input (except the clamped top
+    code, within one step), and the C oracle, the Python reader and the integer view agree."""
+    from parakeet_amd import gguf
+    rng = np.random.default_rng(10 + qtype)
+    x = rng.standard_normal((9, 64)).astype(np.float32)
+    raw = gguf.QUANTIZE[qtype](x)
+    y = gguf.dequantize(raw, qtype, x.size).reshape(x.shape)
+    b = x.reshape(-1, 32)
+    step = np.abs(b).max(1) / levels
+    err = np.abs(b - y.reshape(-1, 32))
+    assert np.all(err <= step[:, None] * 1.0 + 1e-6)
+    assert np.mean(err <= step[:, None] * 0.5 * 1.01 + 1e-7) > 0.95
+    c = _oracle_dequant(oracle_mod, np.frombuffer(raw, np.uint8), qtype, x.size).reshape(x.shape)
+    assert np.array_equal(c, y)
+    d, q = gguf.block_ints(raw, qtype, x.size // 32)
+    assert q.min() >= -levels and q.max() <= levels - 1
+    assert np.array_equal((q * d[:, None]).astype(np.float32).reshape(x.shape), y)
+
+
 def test_argmax_first_index(oracle_mod):
     am = lambda a: oracle_mod.lib().ora_argmax(oracle_mod.fptr(np.asarray(a, np.float32)), len(a))
     assert am([1, 3, 3, 2]) == 1
