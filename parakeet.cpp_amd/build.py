@@ -9,6 +9,11 @@
                           only where parakeet.cpp's sources are present: it compiles against the
                           reference's own src/parakeet_ctc.h (headers only, no ggml)
 
+  tests/cpp/oracle_asan, oracle_tsan, gguf_fuzz_asan
+                          host-only sanitizer builds (g++/gcc, no device code): the oracle under
+                          AddressSanitizer + UBSan and ThreadSanitizer, and the GGUF reader and
+                          decoder loader under a mutation fuzzer with AddressSanitizer + UBSan
+
 Called by __graft_entry__.build(); every call recompiles.
 """
 from __future__ import annotations
@@ -94,9 +99,35 @@ def build_dropin_test():
     return out
 
 
+SAN_FLAGS = ["-O1", "-g", "-fno-omit-frame-pointer", "-fno-sanitize-recover=all"]
+
+
+def build_sanitizers():
+    """Host code only, compiled by gcc / g++ (never hipcc): the oracle and its driver, and the
+    GGUF reader + decoder loader with the fuzz driver."""
+    oracle = os.path.join(ROOT, "oracle")
+    cpp = os.path.join(ROOT, "tests", "cpp")
+    outs = []
+    o_src = [os.path.join(cpp, "oracle_sanitize_main.c"), os.path.join(oracle, "pk_oracle.c")]
+    for name, san in (("oracle_asan", "-fsanitize=address,undefined"), ("oracle_tsan", "-fsanitize=thread")):
+        out = os.path.join(cpp, name)
+        _run(["gcc", "-std=c11", *SAN_FLAGS, san, f"-I{oracle}", *o_src, "-lm", "-lpthread", "-o", out + ".tmp"])
+        os.replace(out + ".tmp", out)
+        outs.append(out)
+    if os.path.exists(os.path.join(HERE, "libparakeet_hip.so")):
+        out = os.path.join(cpp, "gguf_fuzz_asan")
+        srcs = [os.path.join(cpp, "gguf_fuzz_main.cpp")] + [os.path.join(CSRC, f) for f in
+                                                           ("gguf_reader.cpp", "parakeet_decoder.cpp", "decoder_core.cpp")]
+        _run(["g++", "-std=c++17", *SAN_FLAGS, "-fsanitize=address,undefined", f"-I{INC}", f"-I{CSRC}", *srcs,
+              f"-L{HERE}", "-lparakeet_hip", "-Wl,-rpath,$ORIGIN/../../parakeet.cpp_amd", "-o", out + ".tmp"])
+        os.replace(out + ".tmp", out)
+        outs.append(out)
+    return outs
+
+
 def build_all():
     return [build_hip(), build_decoder(), build_calib(), build_api_test("decoder_api_main", hip=True),
-            build_api_test("loader_main"), build_dropin_test()]
+            build_api_test("loader_main"), build_dropin_test(), *build_sanitizers()]
 
 
 if __name__ == "__main__":

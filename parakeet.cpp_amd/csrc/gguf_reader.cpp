@@ -115,10 +115,21 @@ int File::open(const std::string &path, std::string &err) {
     const std::streamsize size = f.tellg();
     if (size < 0) { err = "cannot size " + path; return 1; }
     f.seekg(0);
-    bytes_.resize((size_t)size);
-    if (!f.read(reinterpret_cast<char *>(bytes_.data()), size)) { err = "short read " + path; return 1; }
+    std::vector<uint8_t> bytes((size_t)size);
+    if (!f.read(reinterpret_cast<char *>(bytes.data()), size)) { err = "short read " + path; return 1; }
+    if (parse(std::move(bytes), err)) {
+        err = path + ": " + err;
+        return 1;
+    }
+    return 0;
+}
+
+int File::parse(std::vector<uint8_t> bytes, std::string &err) {
+    bytes_ = std::move(bytes);
+    kv_.clear();
+    tensors_.clear();
     Cursor c{bytes_.data(), bytes_.data() + bytes_.size()};
-    if (bytes_.size() < 24 || memcmp(bytes_.data(), "GGUF", 4) != 0) { err = path + ": not GGUF"; return 1; }
+    if (bytes_.size() < 24 || memcmp(bytes_.data(), "GGUF", 4) != 0) { err = "not GGUF"; return 1; }
     c.p += 4;
     const uint32_t version = c.get<uint32_t>();
     if (version != 2 && version != 3) { err = "unsupported GGUF version"; return 1; }

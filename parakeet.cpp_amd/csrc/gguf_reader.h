@@ -38,6 +38,8 @@ class File {
 public:
     // Returns 0 on success, non-zero with a message in err otherwise.
     int open(const std::string &path, std::string &err);
+    // The same over the bytes of a file already in memory (kept by the File).
+    int parse(std::vector<uint8_t> bytes, std::string &err);
     const Value *find(const std::string &key) const;
     const Tensor *tensor(const std::string &name) const;
     uint32_t get_u32(const std::string &key, uint32_t def) const;

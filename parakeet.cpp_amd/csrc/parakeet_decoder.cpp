@@ -130,6 +130,22 @@ int load_from_gguf(const std::string &gguf_path, DecoderModel &out, int, int, bo
         out.eou_id = g.find("parakeet.eou.eou_id") ? g.get_i32("parakeet.eou.eou_id", -1) : -1;
         out.eob_id = g.find("parakeet.eou.eob_id") ? g.get_i32("parakeet.eou.eob_id", -1) : -1;
     }
+    // sizes the decoder can hold; a corrupt file asking for more is refused here,
+    // before anything is sized from it
+    {
+        const bool tdt = out.model_type == ParakeetModelType::TDT;
+        const int L = tdt ? c.tdt_pred_rnn_layers : c.eou_pred_rnn_layers;
+        const int H = tdt ? c.tdt_pred_hidden : c.eou_pred_hidden;
+        const int J = tdt ? c.tdt_joint_hidden : c.eou_joint_hidden;
+        const bool dec = tdt || out.model_type == ParakeetModelType::EOU;
+        if (dec && (L < 1 || L > PK_MAX_LAYERS || H < 1 || H > (1 << 16) || J < 1 || J > (1 << 16) ||
+                    c.d_model < 1 || c.d_model > (1 << 16) || out.vocab_size < 1 || out.vocab_size > (1 << 20) ||
+                    (tdt && (c.tdt_num_durations < 0 || c.tdt_num_durations > PK_MAX_DURATIONS ||
+                             out.tdt_durations.size() > (size_t)PK_MAX_DURATIONS)))) {
+            std::fprintf(stderr, "gguf: decoder sizes out of range\n");
+            return 2;
+        }
+    }
     out.vocab.blank_id = out.blank_id;
     if (const gguf::Value *v = g.find("tokenizer.ggml.tokens")) out.vocab.pieces = v->arr_s;
     out.vocab.unk_id = (int32_t)g.get_u32("tokenizer.ggml.unk_token_id", (uint32_t)-1);

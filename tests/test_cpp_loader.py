@@ -148,3 +148,15 @@ def test_block_quantized_files_load(tmp_path, quant):
     cut = str(tmp_path / "cut.gguf")
     open(cut, "wb").write(raw[:-1])
     assert _load(cut)["rc"] == 1
+
+
+@pytest.mark.parametrize("key,value", [("parakeet.tdt.pred_rnn_layers", 0x7FFFFFFF), ("parakeet.tdt.pred_rnn_layers", 9),
+                                       ("parakeet.tdt.pred_hidden", 0), ("parakeet.tdt.vocab_size", 1 << 24),
+                                       ("parakeet.tdt.num_durations", 17), ("parakeet.encoder.d_model", 0)])
+def test_decoder_sizes_out_of_range(tmp_path, key, value):
+    """Sizes the decoder cannot hold are refused with rc 2 before anything is sized from them
+    (a corrupt layer count once made the loader build billions of tensor names)."""
+    meta = {"parakeet.model.type": "tdt", key: value}
+    path = str(tmp_path / "m.gguf")
+    _gguf(path, meta, _decoder_tensors("tdt", 2))
+    assert _load(path)["rc"] == 2
