@@ -424,9 +424,13 @@ def main():
                                          f"{threads} threads, oracle built with -O3 -ffast-math -funroll-loops",
                                "host_cpus": host_cpus, "cpu_model": cpu_model()}
         # the same utterances decoded on the device emit the same tokens
-        dev_tok = wl.out["n_tokens"].to_numpy(np.int32, B)[:nu]
-        out["cpu_baseline"]["token_counts_equal"] = bool(
-            all(len(r["tokens"][u]) == dev_tok[u] for u in range(nu)))
+        # every utterance's full token sequence against the device's (free-running on both
+        # sides: a differing utterance would need a near-tie, which the parity sample counts)
+        dev_n = wl.out["n_tokens"].to_numpy(np.int32, B)
+        dev_t = wl.out["tokens"].to_numpy(np.int32, B * wl.cap).reshape(B, wl.cap)
+        same = sum(int(np.array_equal(r["tokens"][u], dev_t[u, :dev_n[u]])) for u in range(nu))
+        out["cpu_baseline"]["token_sequences_equal"] = f"{same}/{nu}"
+        out["cpu_baseline"]["steps_equal"] = bool(np.array_equal(r["steps"][:nu], wl.steps()[:nu]))
         # B=1 latency of the scalar reference loop: one thread, the 125-frame utterance
         e1 = synth.encoder_frames(0, 125, D)
         t0 = time.perf_counter()

@@ -33,6 +33,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cerrno>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -43,6 +44,11 @@
 #include <numeric>
 #include <string>
 #include <vector>
+
+#include <fcntl.h>
+#include <sys/file.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 #include "parakeet_hip.h"
 #include "pk_device.h"
@@ -351,6 +357,7 @@ struct pk_decoder {
     HostBuf h_out;             // staging of host-memory outputs
     unsigned char *scratch = nullptr;   // this device's fixed scratch array (pk_decode_noalloc)
     int last_iters = 0;
+    int lock_fd = -1;          // this GPU's cross-process loop lock (see DeviceLoopLock), -1: none
 };
 
 namespace {
@@ -465,6 +472,7 @@ struct CallScratch {
 };
 
 int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratch cs = CallScratch{});
+int open_loop_lock(int device);
 
 }  // namespace
 
@@ -655,6 +663,7 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
         return cleanup(fail(PK_ERR_DEVICE, "decode kernel does not fit on a CU"));
     dec->nwg = std::min(dec->n_cu, kBlock);
     if ((rc = scratch_address(dec->device, &dec->scratch))) return cleanup(rc);
+    dec->lock_fd = open_loop_lock(dec->device);
     if (hipStreamCreateWithFlags(&dec->stream, hipStreamNonBlocking) != hipSuccess)
         return cleanup(fail(PK_ERR_DEVICE, "stream"));
     for (auto &e : dec->ev)
@@ -669,6 +678,7 @@ PK_API int pk_decoder_destroy(pk_decoder *dec) {
     if (dec->stream) (void)hipStreamSynchronize(dec->stream);
     for (auto &e : dec->ev) if (e) (void)hipEventDestroy(e);
     if (dec->stream) (void)hipStreamDestroy(dec->stream);
+    if (dec->lock_fd >= 0) close(dec->lock_fd);
     delete dec;
     return 0;
 }
@@ -772,6 +782,37 @@ PK_API int pk_decode_noalloc(pk_decoder *dec, const pk_batch *bt) {
 }  // extern "C"
 
 namespace {
+
+// The decode loop needs every CU of its GPU at once, so two processes must not
+// run it on one GPU together: an exclusive flock on a per-GPU file
+// (/tmp/parakeet_hip-<PCI bus id>.lock, opened once per decoder) is held from a
+// call's loop launch to its last stream synchronisation.  Advisory and
+// best-effort: without the file (no /tmp, no permission) calls are not
+// serialised across processes, and overlapping loops end with PK_ERR_TIMEOUT.
+struct DeviceLoopLock {
+    int fd;
+    explicit DeviceLoopLock(int f) : fd(f) {
+        if (fd >= 0)
+            while (flock(fd, LOCK_EX) != 0 && errno == EINTR) {
+            }
+    }
+    ~DeviceLoopLock() {
+        if (fd >= 0) (void)flock(fd, LOCK_UN);
+    }
+    DeviceLoopLock(const DeviceLoopLock &) = delete;
+    DeviceLoopLock &operator=(const DeviceLoopLock &) = delete;
+};
+
+int open_loop_lock(int device) {
+    char bus[64] = {0};
+    if (hipDeviceGetPCIBusId(bus, sizeof bus, device) != hipSuccess) return -1;
+    char path[128];
+    snprintf(path, sizeof path, "/tmp/parakeet_hip-%s.lock", bus);
+    int fd = open(path, O_RDWR | O_CREAT | O_CLOEXEC, 0666);
+    if (fd < 0) fd = open(path, O_RDONLY | O_CLOEXEC);   // created by another user: a shared lock file
+    if (fd >= 0) (void)fchmod(fd, 0666);
+    return fd;
+}
 
 // Decode-loop launches of this process, per device: the loop's workgroups
 // wait on one another, so two loops must never share a device.  Every launch
@@ -1106,6 +1147,9 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
         p.wcache_bytes = (int)off;
         lds += off;
     }
+    // held until this call's last stream synchronisation (scope end): another
+    // process's decode loop on this GPU waits here instead of sharing the CUs
+    const DeviceLoopLock cross_process(dec->lock_fd);
     if ((rc = launch_loop(dec, nwg, p, lds))) return rc;
     HIP_TRY(hipEventRecord(dec->ev[2], dec->stream));
     int status[4] = {0, 0, 0, 0};
