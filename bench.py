@@ -13,6 +13,9 @@ decode loop), the CPU baseline (the oracle, a C restatement of the
 reference's scalar decoder, timed on this host on a bounded sample), and the
 other workload shapes (--no-extras skips them):
   b1                 B=1, T=125 on the same decoder: latency per step
+  b1_blank4          the same with the blank logit raised by 4 (blank-dominated decoding, as a
+                     trained model's is): latency per step with runs of blanks walked over
+                     the joint tile's spare columns, and without them (PK_SPEC=0)
   b256               B=256, T=750 on the same decoder
   ragged_b512        B=512, T ~ U{50..1500}, blank-logit offsets {0, +2, +4}
   tdt11b_f16_b256    TDT-1.1b shapes (vocab 1024), f16 weights, B=256, T=375
@@ -36,7 +39,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 
-EXTRAS = ("b1", "b256", "ragged_b512", "tdt11b_f16_b256", "eou_stream_b128")
+EXTRAS = ("b1", "b1_blank4", "b256", "ragged_b512", "tdt11b_f16_b256", "eou_stream_b128")
 
 
 def parse():
@@ -280,6 +283,25 @@ def run_extra(name, pk, hipmem, roofline, gguf, synth, dec, cost, tmp, D, MS, ba
                 "us_per_step_incl_enc_proj": round((loop1 + enc1) * 1e3 / st1, 3),
                 "us_per_step_wall": round(wall1 / 20 * 1e6 / st1, 3)}
     base += n_b1
+    if name == "b1_blank4":
+        res = {}
+        for label, env in (("", None), ("_without_runs", "0")):
+            if env is not None:
+                os.environ["PK_SPEC"] = env
+            try:
+                wlb = Workload(pk, hipmem, dec, np.full(1, 125), D, MS, n_b1, base,
+                               blank_bias=np.full(1, 4.0, np.float32))
+                wallb, loopb, encb, itb = timed(wlb, 2, 20)
+                stb = int(wlb.steps().sum())
+                wlb.free()
+            finally:
+                os.environ.pop("PK_SPEC", None)
+            base += n_b1
+            res["us_per_step_loop" + label] = round(loopb * 1e3 / stb, 3)
+            res["iterations" + label] = itb
+        res.update(frames=125, blank_bias=4.0, decode_steps=stb)
+        return res
+    base += 2 * n_b1
     if name == "b256":
         # B=256, T=750: lockstep throughput on the same decoder
         return lockstep_extra(pk, hipmem, roofline, dec, cost, np.full(256, 750), D, MS, base)
@@ -336,7 +358,7 @@ def main():
     rd = gguf.GGUFReader(path)
     n_calls = args.warmup + args.steps + 1
     n_b1 = 24
-    dec = pk.Decoder(rd, n_slots=B * n_calls + (0 if args.no_extras else n_b1 + 256 * 4 + 512 * 4))
+    dec = pk.Decoder(rd, n_slots=B * n_calls + (0 if args.no_extras and not args.only else 3 * n_b1 + 256 * 4 + 512 * 4))
     info = dec.info
     cost = roofline.DecoderCost(info, matrix_types(rd, "tdt"))
 

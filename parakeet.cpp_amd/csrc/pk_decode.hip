@@ -1045,6 +1045,12 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     p.max_iter = max_iter;
     p.n_dom = pl.n_dom;
     p.dom_size = pl.P;
+    // blank runs over the joint tile's spare columns (not while the logit tap records
+    // per-step rows; PK_SPEC=0 turns them off for comparisons)
+    {
+        const char *v = std::getenv("PK_SPEC");
+        p.spec = (lsteps == 0 && !(v && v[0] == '0')) ? 1 : 0;
+    }
     p.nt = pl.nt;
     p.dom_n = d_dom_n;
     p.dom_list = d_dom_list;
@@ -1054,7 +1060,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     // argmax shards: about 8 ranks per shard
     p.shards = 1;
     while (p.shards < pkdev::kShards && p.shards * 8 < pl.P) p.shards *= 2;
-    const size_t keys_bytes = (size_t)2 * m * p.shards * 2 * 8;
+    const size_t keys_bytes = (size_t)2 * pl.n_dom * pkdev::kColCap * p.shards * 2 * 8;
     // the words every launch starts from zero, in one allocation cleared by
     // one fill: 64 B of status, the barrier flags, the argmax keys
     const size_t flags_bytes = (size_t)nwg * kFlagStride * 4, clear_bytes = 256 + flags_bytes + keys_bytes;

@@ -19,6 +19,7 @@ constexpr int kWaves = kBlock / kWave;
 constexpr int kTile = 16;                   // MFMA tile edge (rows = outputs, columns = utterances)
 constexpr int kMaxNT = 2;                   // utterance tiles per domain
 constexpr int kDomCap = kTile * kMaxNT;     // utterances per domain
+constexpr int kColCap = kDomCap;            // joint columns per domain and iteration (argmax key slots)
 constexpr int kSmallB = 4;                  // LSTM batch at or below which layer 0 runs redundantly
 constexpr int kIdxBits = 14;                // argmax key: index field
 constexpr int kStampShift = 46;             // argmax key: 14 index + 32 value bits below the stamp
@@ -112,9 +113,10 @@ struct KParams {
     const int *dom_wg;           // [n_dom][dom_size] workgroup of each rank
     // sync
     unsigned *flags;             // [nwg * kFlagStride]
-    unsigned long long *keys;    // [2][n_utts][shards][2] best keys, by iteration parity
+    unsigned long long *keys;    // [2][n_dom][kColCap][shards][2] best keys per joint column, by iteration parity
     int shards;                  // power of two <= kShards: ranks per shard ~ 8
     int *status;                 // [0] error code, [1] iterations, [2] overflow, [3] trace overflow
+    int spec;                    // blank-run columns: spare joint columns evaluate later frames
     int max_iter;
     int red_slots;               // LDS partial slots: a phase runs in passes of red_slots / (units per item) items
     int st_n, st_k;              // LDS state of layers >= 1: utterance and owned-tile capacity
@@ -411,13 +413,18 @@ struct Ctl {                      // per-workgroup copy of its domain's control 
     int t[kDomCap], T[kDomCap], sym[kDomCap], pend[kDomCap], flags[kDomCap];
     int ntok[kDomCap], steps[kDomCap], nseg[kDomCap], segst[kDomCap], last[kDomCap], cur[kDomCap];
     int lst[kDomCap], jst[kDomCap];
+    // joint columns: column i < nj is joint-list utterance i at its frame t; columns
+    // sbase[i] .. sbase[i] + sn[i] - 1 are the same utterance at frames t + 1 .. t + sn[i]
+    int cu[kColCap], co[kColCap], sbase[kDomCap], sn[kDomCap];
+    int brun[kDomCap];            // 1: the utterance's last decision kept the prediction output
+    int ncol;
     long long erow[kDomCap];      // first encp row of each utterance
     float bbias[kDomCap];         // blank logit offset of each utterance
     int tbase[kDomCap];           // tokens before this call (EOU segment indices)
     int dur[PK_MAX_DURATIONS];    // duration values (the decision step reads them from LDS)
     int n, nl, nj;
     int dom, rank, P;
-    unsigned long long wgkey[kDomCap][2];   // this workgroup's best key per utterance and head
+    unsigned long long wgkey[kColCap][2];   // this workgroup's best key per joint column and head
     unsigned long long prof[kPrN];
 };
 
@@ -454,18 +461,58 @@ __device__ __forceinline__ unsigned long long *tl_t0() { __shared__ unsigned lon
 #define TLA(k) TLX(k, 0)
 
 // Compact the LSTM list (pending token) and the joint list (frames left).
-__device__ __forceinline__ void build_lists(Ctl &s) {
+// Then the joint columns: one per joint-list utterance at its frame t, and
+// (spec) the column tiles' spare columns dealt out evenly as frames t + 1,
+// t + 2, ... to the utterances in a run of blanks (last decision kept the
+// prediction output), up to their last frame.  A blank decision keeps the
+// prediction output, so the logits of the next frame are already in a spare
+// column: the decision step walks a run of blanks in one iteration instead of
+// one iteration per blank.
+__device__ __forceinline__ void build_lists(Ctl &s, bool spec) {
     if (threadIdx.x < kWave) {
         const int lane = threadIdx.x;
         const bool fl = lane < s.n && s.pend[lane] >= 0;
         const bool fj = lane < s.n && s.t[lane] < s.T[lane];
         const unsigned long long bl = __ballot(fl), bj = __ballot(fj);
         const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-        if (fl) s.lst[__popcll(bl & below)] = lane;
-        if (fj) s.jst[__popcll(bj & below)] = lane;
+        const int il = __popcll(bl & below), ij = __popcll(bj & below);
+        if (fl) s.lst[il] = lane;
+        if (fj) s.jst[ij] = lane;
+        const int nj = __popcll(bj);
+        // an utterance in a blank run takes q spare columns: an even share of the
+        // spare columns of the tiles, capped at the frames it has left
+        const int spare = spec && nj > 0 ? ((nj + kTile - 1) / kTile) * kTile - nj : 0;
+        const bool fe = fj && spare > 0 && s.brun[lane] != 0;
+        const unsigned long long be = __ballot(fe);
+        const int ne = __popcll(be), ie = __popcll(be & below);
+        int q = 0;
+        if (fe) {
+            q = spare / ne + (ie < spare % ne ? 1 : 0);
+            q = min(q, s.T[lane] - s.t[lane] - 1);
+        }
+        // exclusive prefix sum of q over the joint list (lanes in list order)
+        int incl = q;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int v = __shfl_up(incl, d, kWave);
+            if (lane >= d) incl += v;
+        }
+        if (fj) {
+            const int base = nj + incl - q;
+            s.cu[ij] = lane;
+            s.co[ij] = 0;
+            s.sbase[ij] = base;
+            s.sn[ij] = q;
+            for (int o = 1; o <= q; ++o) {
+                s.cu[base + o - 1] = lane;
+                s.co[base + o - 1] = o;
+            }
+        }
+        const int total = __shfl(incl, kWave - 1, kWave);
         if (lane == 0) {
             s.nl = __popcll(bl);
-            s.nj = __popcll(bj);
+            s.nj = nj;
+            s.ncol = nj + total;
         }
     }
     lds_sync();
@@ -927,10 +974,10 @@ __device__ __forceinline__ void cache_matrix(const TMat &m, int rank, int P, uns
 __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned stamp,
                             unsigned long long &tlast) {
     const int J = p.J, lane = threadIdx.x & (kWave - 1);
-    if (threadIdx.x < 2 * kDomCap) s.wgkey[threadIdx.x / 2][threadIdx.x % 2] = 0ull;
+    if (threadIdx.x < 2 * kColCap) s.wgkey[threadIdx.x / 2][threadIdx.x % 2] = 0ull;
     const int n_out = owned(p.w_out.tiles, s.rank, s.P);
-    for (int c0 = 0; c0 < s.nj; c0 += kTile) {
-        const int nc = min(kTile, s.nj - c0);
+    for (int c0 = 0; c0 < s.ncol; c0 += kTile) {
+        const int nc = min(kTile, s.ncol - c0);
         Act x = S.act[0];
         x.n = nc;
         // stage hidden = relu(encp[t] + pp) for this column tile (row mapping as in stage_act)
@@ -939,8 +986,9 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
             for (int u0 = 0; u0 < nc; u0 += kBlock / kStageTpr) {
                 const int u = u0 + threadIdx.x / kStageTpr;
                 const bool live = u < nc;
-                const int ul = s.jst[c0 + (live ? u : nc - 1)];
-                const unsigned erow = (unsigned)((size_t)(s.erow[ul] + s.t[ul]) * J * 4);
+                const int col = c0 + (live ? u : nc - 1);
+                const int ul = s.cu[col];
+                const unsigned erow = (unsigned)((size_t)(s.erow[ul] + s.t[ul] + s.co[col]) * J * 4);
                 const unsigned prow = (unsigned)((size_t)s.b[ul] * J * 4);
                 for (int k0 = 0; k0 < per; k0 += kStageTpr * kStageMax) {
                     float4 e[kStageMax], q[kStageMax];
@@ -974,14 +1022,14 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         // rows 4g .. 4g+3 of a tile for utterance u of the column tile; its blank
         // offset is loaded before the products
         const int u = 4 * (lane >> 4) + (lane & 3), g = (lane >> 2) & 3;
-        const float bb = u < nc ? s.bbias[s.jst[c0 + u]] : 0.0f;
+        const float bb = u < nc ? s.bbias[s.cu[c0 + u]] : 0.0f;
         // (b_out is zero-padded to whole tiles)
         const float *btab = S.bias + bias_base(p, s.rank, s.P, p.L);
         TL(1);
         // debug logit tap: this lane's utterance row of the current step
         float *ltap = nullptr;
-        if (p.logits && u < nc) {
-            const int ul = s.jst[c0 + u], step = s.steps[ul];
+        if (p.logits && u < nc) {   // (no spare columns while the tap is on: column = joint-list index)
+            const int ul = s.cu[c0 + u], step = s.steps[ul];
             if (step < p.logit_steps) ltap = p.logits + ((size_t)s.b[ul] * p.logit_steps + step) * p.Vo;
         }
         // each lane keeps its best key per head over all its rows; the four
@@ -1028,12 +1076,12 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
     // one device-scope max per utterance and head into shard rank % kShards
     // (spreads the atomics of many workgroups over several words); the stamp
     // keeps keys of iteration `stamp` above every older key in the same parity
-    unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * p.shards * 2;
-    if (threadIdx.x < 2 * s.nj) {
+    unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_dom * kColCap * p.shards * 2;
+    if (threadIdx.x < 2 * s.ncol) {
         const int u = threadIdx.x / 2, head = threadIdx.x % 2;
         const unsigned long long k = s.wgkey[u][head];
         if (k != 0ull)
-            __hip_atomic_fetch_max(&keys[((size_t)s.b[s.jst[u]] * p.shards + s.rank % p.shards) * 2 + head],
+            __hip_atomic_fetch_max(&keys[((size_t)(s.dom * kColCap + u) * p.shards + s.rank % p.shards) * 2 + head],
                                    ((unsigned long long)stamp << kStampShift) | k, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -1210,22 +1258,22 @@ __device__ __forceinline__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bu
 
 // Apply the argmax results of iteration `stamp` to every utterance of the joint
 // list: src/parakeet_tdt.cpp:936-967 (TDT) and src/parakeet_eou.cpp:275-332 (EOU).
-// The domain's best key per joint utterance and head: the maximum over the
+// The domain's best key per joint column and head: the maximum over the
 // shards that carry this iteration's stamp (shards no rank wrote this
 // iteration hold older stamps and are skipped).  Lane groups of p.shards
-// reduce one (utterance, head) with shuffles; results go to s.wgkey.
+// reduce one (column, head) with shuffles; results go to s.wgkey.
 __device__ __forceinline__ void gather_shards(const KParams &p, Ctl &s, unsigned stamp) {
     const int G = p.shards;
-    const unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_utts * G * 2;
+    const unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_dom * kColCap * G * 2;
     const int lane = threadIdx.x & (kWave - 1);
-    const int n = s.nj * 2 * G;
+    const int n = s.ncol * 2 * G;
     for (int e0 = 0; e0 < n; e0 += kBlock) {      // e = (pair, shard); whole waves stay together
         const int e = e0 + threadIdx.x;
         unsigned long long k = 0ull;
         if (e < n) {
             const int pair = e / G, sh = e - pair * G;
-            const int b = s.b[s.jst[pair >> 1]];
-            k = __hip_atomic_load(&keys[((size_t)b * G + sh) * 2 + (pair & 1)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const size_t col = (size_t)s.dom * kColCap + (pair >> 1);
+            k = __hip_atomic_load(&keys[(col * G + sh) * 2 + (pair & 1)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (key_stamp(k) != stamp) k = 0ull;
         }
         for (int m = 1; m < G; m <<= 1) {
@@ -1240,84 +1288,101 @@ __device__ __forceinline__ void gather_shards(const KParams &p, Ctl &s, unsigned
     lds_sync();
 }
 
+// One utterance per thread.  Its first decision is column i (frame t); while
+// the decision keeps the prediction output (a TDT blank; an EOU blank, <EOB>
+// or special piece) and the next frame's column was evaluated, the walk goes
+// on with that column, one step per column, exactly as later iterations would.
 __device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp) {
     gather_shards(p, s, stamp);
     TLA(30);
     for (int i = threadIdx.x; i < s.nj; i += kBlock) {
         const int ul = s.jst[i], b = s.b[ul];
-        const unsigned long long kt = s.wgkey[i][0], kd = s.wgkey[i][1];
-        if (key_stamp(kt) != stamp || (p.Dn > 0 && key_stamp(kd) != stamp)) {
-            __hip_atomic_store(p.status, PK_ERR_DEVICE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            s.t[ul] = s.T[ul];
-            continue;
-        }
-        const int tok = key_index(kt);
-        const int di = p.Dn > 0 ? key_index(kd) : -1;
         const bool writer = (ul % s.P) == s.rank;
-        const int step = s.steps[ul]++;
-        if (writer && p.trace) {
-            if (step < p.trace_cap) {
-                p.trace[((size_t)b * p.trace_cap + step) * 2] = tok;
-                p.trace[((size_t)b * p.trace_cap + step) * 2 + 1] = di;
-            } else {
-                s.flags[ul] |= kFlagTraceOverflow;
+        const int t0 = s.t[ul];
+        int col = i;
+        while (true) {
+            const unsigned long long kt = s.wgkey[col][0], kd = s.wgkey[col][1];
+            if (key_stamp(kt) != stamp || (p.Dn > 0 && key_stamp(kd) != stamp)) {
+                __hip_atomic_store(p.status, PK_ERR_DEVICE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                s.t[ul] = s.T[ul];
+                break;
             }
-        }
-        if (p.kind == PK_KIND_TDT) {
-            const int dur = p.n_dur > 0 ? s.dur[di] : di;
-            const int adv = dur > 1 ? dur : 1;
-            if (tok == p.blank) {
-                s.t[ul] += adv;
-                s.sym[ul] = 0;
-                continue;
+            const int tok = key_index(kt);
+            const int di = p.Dn > 0 ? key_index(kd) : -1;
+            const int step = s.steps[ul]++;
+            if (writer && p.trace) {
+                if (step < p.trace_cap) {
+                    p.trace[((size_t)b * p.trace_cap + step) * 2] = tok;
+                    p.trace[((size_t)b * p.trace_cap + step) * 2 + 1] = di;
+                } else {
+                    s.flags[ul] |= kFlagTraceOverflow;
+                }
             }
-            const int n = s.ntok[ul]++;
-            if (writer) {
-                if (n < p.token_cap) p.tokens[(size_t)b * p.token_cap + n] = tok;
-                else s.flags[ul] |= kFlagTokOverflow;
-            }
-            s.pend[ul] = tok;
-            s.sym[ul] += 1;
-            if (dur > 0 || s.sym[ul] >= p.max_sym) {
-                s.t[ul] += adv;
-                s.sym[ul] = 0;
-            }
-        } else {
-            const int max_syms = p.max_sym > 1 ? p.max_sym : 1;
-            bool frame_done = false;
-            if (tok == p.blank || tok == p.eob) {
-                frame_done = true;
-            } else if (tok == p.eou) {
-                const int total = s.tbase[ul] + s.ntok[ul];
-                if (total > s.segst[ul]) {
-                    const int ns = s.nseg[ul]++;
+            bool keep = false;   // the prediction output stays: the next frame may follow at once
+            if (p.kind == PK_KIND_TDT) {
+                const int dur = p.n_dur > 0 ? s.dur[di] : di;
+                const int adv = dur > 1 ? dur : 1;
+                if (tok == p.blank) {
+                    s.t[ul] += adv;
+                    s.sym[ul] = 0;
+                    keep = true;
+                } else {
+                    const int n = s.ntok[ul]++;
                     if (writer) {
-                        if (p.segs && ns < p.seg_cap) p.segs[(size_t)b * p.seg_cap + ns] = total;
-                        else s.flags[ul] |= kFlagSegOverflow;
+                        if (n < p.token_cap) p.tokens[(size_t)b * p.token_cap + n] = tok;
+                        else s.flags[ul] |= kFlagTokOverflow;
                     }
-                    s.segst[ul] = total;
+                    s.pend[ul] = tok;
+                    s.sym[ul] += 1;
+                    if (dur > 0 || s.sym[ul] >= p.max_sym) {
+                        s.t[ul] += adv;
+                        s.sym[ul] = 0;
+                    }
                 }
-                s.flags[ul] |= kFlagZeroHC;
-                s.pend[ul] = p.blank;
-                s.last[ul] = p.blank;
-                frame_done = true;
-            } else if (tok >= 0 && tok < p.n_special && p.special[tok]) {
-                frame_done = true;
             } else {
-                const int n = s.ntok[ul]++;
-                if (writer) {
-                    if (n < p.token_cap) p.tokens[(size_t)b * p.token_cap + n] = tok;
-                    else s.flags[ul] |= kFlagTokOverflow;
+                const int max_syms = p.max_sym > 1 ? p.max_sym : 1;
+                bool frame_done = false;
+                if (tok == p.blank || tok == p.eob) {
+                    frame_done = true;
+                    keep = true;
+                } else if (tok == p.eou) {
+                    const int total = s.tbase[ul] + s.ntok[ul];
+                    if (total > s.segst[ul]) {
+                        const int ns = s.nseg[ul]++;
+                        if (writer) {
+                            if (p.segs && ns < p.seg_cap) p.segs[(size_t)b * p.seg_cap + ns] = total;
+                            else s.flags[ul] |= kFlagSegOverflow;
+                        }
+                        s.segst[ul] = total;
+                    }
+                    s.flags[ul] |= kFlagZeroHC;
+                    s.pend[ul] = p.blank;
+                    s.last[ul] = p.blank;
+                    frame_done = true;
+                } else if (tok >= 0 && tok < p.n_special && p.special[tok]) {
+                    frame_done = true;
+                    keep = true;
+                } else {
+                    const int n = s.ntok[ul]++;
+                    if (writer) {
+                        if (n < p.token_cap) p.tokens[(size_t)b * p.token_cap + n] = tok;
+                        else s.flags[ul] |= kFlagTokOverflow;
+                    }
+                    s.pend[ul] = tok;
+                    s.last[ul] = tok;
+                    s.sym[ul] += 1;
+                    if (s.sym[ul] >= max_syms) frame_done = true;
                 }
-                s.pend[ul] = tok;
-                s.last[ul] = tok;
-                s.sym[ul] += 1;
-                if (s.sym[ul] >= max_syms) frame_done = true;
+                if (frame_done) {          // the next frame starts with sym = 0 (src/parakeet_eou.cpp:269)
+                    s.t[ul] += 1;
+                    if (s.t[ul] < s.T[ul]) s.sym[ul] = 0;
+                }
             }
-            if (frame_done) {          // the next frame starts with sym = 0 (src/parakeet_eou.cpp:269)
-                s.t[ul] += 1;
-                if (s.t[ul] < s.T[ul]) s.sym[ul] = 0;
-            }
+            // the next decision's frame offset from t0, if its column was evaluated
+            const int o = s.t[ul] - t0;
+            s.brun[ul] = keep ? 1 : 0;
+            if (!keep || s.t[ul] >= s.T[ul] || o > s.sn[i]) break;
+            col = s.sbase[i] + o - 1;
         }
     }
 }
@@ -1396,6 +1461,7 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         const int carry = init ? ctrl[PK_CTRL_CARRY] : 0;
         s.pend[ul] = init ? -1 : p.blank;
         s.flags[ul] = init ? 0 : kFlagZeroHC;
+        s.brun[ul] = 0;
         if (p.kind == PK_KIND_TDT) s.t[ul] = carry > 0 ? min(carry, s.T[ul]) : 0;
         else s.t[ul] = 0;
     }
@@ -1442,7 +1508,7 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         cache_matrix(p.w_pred, s.rank, s.P, wcache);
         cache_matrix(p.w_out, s.rank, s.P, wcache);
     }
-    build_lists(s);
+    build_lists(s, p.spec != 0);
     bool ok = dom_sync(p, s, epoch);
 
     unsigned iter = 0;
@@ -1478,7 +1544,7 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
             decide(p, s, iter);
         }
         lds_sync();
-        build_lists(s);
+        build_lists(s, p.spec != 0);
         TLA(31);
         pmark(p, s, tlast, kPrDecide);
     }
