@@ -358,6 +358,7 @@ struct pk_decoder {
     unsigned char *scratch = nullptr;   // this device's fixed scratch array (pk_decode_noalloc)
     int last_iters = 0;
     int lock_fd = -1;          // this GPU's cross-process loop lock (see DeviceLoopLock), -1: none
+    const void *loop_fn = nullptr;   // the decode-loop instantiation for this decoder's weight storage
 };
 
 namespace {
@@ -645,8 +646,23 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
         return cleanup(fail(PK_ERR_UNSUPPORTED, "hidden sizes above 4096"));
     dec->lds_fixed = act;
     // dynamic LDS bound of any launch: the block's LDS less the kernel's static LDS
+    // the loop instantiation for this decoder's weight storage (all q8_0; all f16 / f32; mixed)
+    {
+        bool all_q8 = true, all_half = true;
+        auto see = [&](const pkdev::TMat &m) {
+            all_q8 = all_q8 && m.type == PK_TYPE_Q8_0;
+            all_half = all_half && m.type != PK_TYPE_Q8_0;
+        };
+        for (int l = 0; l < kp.L; ++l) see(kp.w_hh[l]);
+        for (int l = 1; l < kp.L; ++l) see(kp.w_ih[l]);
+        see(kp.w_pred);
+        see(kp.w_out);
+        dec->loop_fn = all_q8 ? reinterpret_cast<const void *>(pkdev::decode_loop_kernel<pkdev::kWcQ8>)
+                     : all_half ? reinterpret_cast<const void *>(pkdev::decode_loop_kernel<pkdev::kWcHalf>)
+                                : reinterpret_cast<const void *>(pkdev::decode_loop_kernel<pkdev::kWcAny>);
+    }
     hipFuncAttributes fa{};
-    if (hipFuncGetAttributes(&fa, reinterpret_cast<const void *>(pkdev::decode_loop_kernel)) != hipSuccess)
+    if (hipFuncGetAttributes(&fa, dec->loop_fn) != hipSuccess)
         return cleanup(fail(PK_ERR_DEVICE, "hipFuncGetAttributes"));
     const size_t stat = fa.sharedSizeBytes;
     const size_t need = (size_t)dec->lds_block > stat ? (size_t)dec->lds_block - stat : 0;
@@ -654,12 +670,10 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
         return cleanup(fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed, %d available", dec->lds_fixed + stat,
                             dec->lds_block));
     dec->lds_bytes = need;
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(pkdev::decode_loop_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)need) != hipSuccess)
+    if (hipFuncSetAttribute(dec->loop_fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)need) != hipSuccess)
         return cleanup(fail(PK_ERR_DEVICE, "hipFuncSetAttribute"));
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(pkdev::decode_loop_kernel),
-                                                     kBlock, need) != hipSuccess || per_cu < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, dec->loop_fn, kBlock, need) != hipSuccess || per_cu < 1)
         return cleanup(fail(PK_ERR_DEVICE, "decode kernel does not fit on a CU"));
     dec->nwg = std::min(dec->n_cu, kBlock);
     if ((rc = scratch_address(dec->device, &dec->scratch))) return cleanup(rc);
@@ -837,7 +851,7 @@ int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds) {
     if (!last) HIP_TRY(hipEventCreateWithFlags(&last, hipEventDisableTiming));
     HIP_TRY(hipStreamWaitEvent(dec->stream, last, 0));
     void *args[] = {&p};
-    const void *fn = reinterpret_cast<const void *>(pkdev::decode_loop_kernel);
+    const void *fn = dec->loop_fn;
     bool &refused = g_loops.coop_refused[dec->device];
     // PK_LOOP_DISPATCH=1: ordinary dispatch from the first launch on.  For
     // profiler runs: rocprofv3 (ROCm 7.2) ends with SIGSEGV in the HIP

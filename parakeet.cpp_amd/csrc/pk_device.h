@@ -416,6 +416,8 @@ struct Ctl {                      // per-workgroup copy of its domain's control 
     // joint columns: column i < nj is joint-list utterance i at its frame t; columns
     // sbase[i] .. sbase[i] + sn[i] - 1 are the same utterance at frames t + 1 .. t + sn[i]
     int cu[kColCap], co[kColCap], sbase[kDomCap], sn[kDomCap];
+    long long crow[kColCap];      // encp row of each column (utterance's first row + t + offset)
+    int cb[kColCap];              // batch index of each column's utterance
     int brun[kDomCap];            // 1: the utterance's last decision kept the prediction output
     int ncol;
     long long erow[kDomCap];      // first encp row of each utterance
@@ -484,31 +486,40 @@ __device__ __forceinline__ void build_lists(Ctl &s, bool spec) {
         const int spare = spec && nj > 0 ? ((nj + kTile - 1) / kTile) * kTile - nj : 0;
         const bool fe = fj && spare > 0 && s.brun[lane] != 0;
         const unsigned long long be = __ballot(fe);
-        const int ne = __popcll(be), ie = __popcll(be & below);
-        int q = 0;
-        if (fe) {
-            q = spare / ne + (ie < spare % ne ? 1 : 0);
-            q = min(q, s.T[lane] - s.t[lane] - 1);
-        }
-        // exclusive prefix sum of q over the joint list (lanes in list order)
-        int incl = q;
-#pragma unroll
-        for (int d = 1; d < kWave; d <<= 1) {
-            const int v = __shfl_up(incl, d, kWave);
-            if (lane >= d) incl += v;
-        }
+        int total = 0;
         if (fj) {
-            const int base = nj + incl - q;
             s.cu[ij] = lane;
             s.co[ij] = 0;
-            s.sbase[ij] = base;
-            s.sn[ij] = q;
-            for (int o = 1; o <= q; ++o) {
-                s.cu[base + o - 1] = lane;
-                s.co[base + o - 1] = o;
-            }
+            s.crow[ij] = s.erow[lane] + s.t[lane];
+            s.cb[ij] = s.b[lane];
         }
-        const int total = __shfl(incl, kWave - 1, kWave);
+        if (be != 0ull) {   // some utterance is in a run of blanks (wave-uniform)
+            const int ne = __popcll(be), ie = __popcll(be & below);
+            int q = 0;
+            if (fe) {
+                q = spare / ne + (ie < spare % ne ? 1 : 0);
+                q = min(q, s.T[lane] - s.t[lane] - 1);
+            }
+            // exclusive prefix sum of q over the joint list (lanes in list order)
+            int incl = q;
+#pragma unroll
+            for (int d = 1; d < kWave; d <<= 1) {
+                const int v = __shfl_up(incl, d, kWave);
+                if (lane >= d) incl += v;
+            }
+            if (fj) {
+                const int base = nj + incl - q;
+                s.sbase[ij] = base;
+                s.sn[ij] = q;
+                for (int o = 1; o <= q; ++o) {
+                    s.cu[base + o - 1] = lane;
+                    s.co[base + o - 1] = o;
+                    s.crow[base + o - 1] = s.erow[lane] + s.t[lane] + o;
+                    s.cb[base + o - 1] = s.b[lane];
+                }
+            }
+            total = __shfl(incl, kWave - 1, kWave);
+        }
         if (lane == 0) {
             s.nl = __popcll(bl);
             s.nj = nj;
@@ -854,9 +865,14 @@ __device__ __forceinline__ void phase_reduce(int j0, int j1, int S, const f32x4 
     TL(4);
 }
 
+// Weight classes the decode loop is compiled for: each instantiation carries
+// only the phase engines its matrices need (a smaller kernel with its own
+// register allocation).  kWcAny serves models whose phases mix storage types.
+enum { kWcQ8 = 0, kWcHalf = 1, kWcAny = 2 };
+
 // Products of one phase for this workgroup, then the epilogue per item, in
 // passes of at most red_slots / S items.
-template <class EpiFn>
+template <int WC, class EpiFn>
 __device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
                                           const Act &x, f32x4 *red, const unsigned char *wc, int red_slots, EpiFn epi) {
     if (n_items <= 0) return;
@@ -870,7 +886,7 @@ __device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm
     for (int j0 = 0; j0 < n_items; j0 += batch) {
         const int j1 = min(n_items, j0 + batch);
         if (j0 > 0) lds_sync();   // the previous pass's reduce has read its slots
-        if (A.type == PK_TYPE_Q8_0) {
+        auto q8 = [&]() {
             if (cached) {
                 if (full) phase_partials<true, true, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
                 else phase_partials<true, true, false>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
@@ -878,10 +894,15 @@ __device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm
                 if (full) phase_partials<true, false, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
                 else phase_partials<true, false, false>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
             }
-        } else {
+        };
+        auto half = [&]() {
             if (cached) phase_partials<false, true, false>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
             else phase_partials<false, false, false>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
-        }
+        };
+        if constexpr (WC == kWcQ8) q8();
+        else if constexpr (WC == kWcHalf) half();
+        else if (A.type == PK_TYPE_Q8_0) q8();
+        else half();
         phase_reduce(j0, j1, S, red, epi);
     }
 }
@@ -971,6 +992,7 @@ __device__ __forceinline__ void cache_matrix(const TMat &m, int rank, int P, uns
 
 // Joint + argmax for this workgroup's output tiles.  Utterances are processed
 // 16 at a time (one MFMA column tile).
+template <int WC>
 __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned stamp,
                             unsigned long long &tlast) {
     const int J = p.J, lane = threadIdx.x & (kWave - 1);
@@ -987,9 +1009,8 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
                 const int u = u0 + threadIdx.x / kStageTpr;
                 const bool live = u < nc;
                 const int col = c0 + (live ? u : nc - 1);
-                const int ul = s.cu[col];
-                const unsigned erow = (unsigned)((size_t)(s.erow[ul] + s.t[ul] + s.co[col]) * J * 4);
-                const unsigned prow = (unsigned)((size_t)s.b[ul] * J * 4);
+                const unsigned erow = (unsigned)((size_t)s.crow[col] * J * 4);
+                const unsigned prow = (unsigned)((size_t)s.cb[col] * J * 4);
                 for (int k0 = 0; k0 < per; k0 += kStageTpr * kStageMax) {
                     float4 e[kStageMax], q[kStageMax];
 #pragma unroll
@@ -1036,7 +1057,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         // lanes of one utterance then combine, and one LDS atomic per utterance
         // and head follows
         unsigned long long best0 = 0ull, best1 = 0ull;
-        run_phase(p.w_out, n_out, p.w_out, n_out, s.rank, s.P, x, S.red, S.wcache, p.red_slots,
+        run_phase<WC>(p.w_out, n_out, p.w_out, n_out, s.rank, s.P, x, S.red, S.wcache, p.red_slots,
                   [&](int k, f32x4 acc) {
                       acc = quad_transpose(acc);   // every lane of the wave takes part
                       if (u >= nc) return;
@@ -1151,6 +1172,7 @@ __device__ __forceinline__ float *st_at(const KParams &p, const Lds &S, int l, i
     return S.st + ((size_t)((l - 1) * p.st_n + ul) * p.st_k + k) * kStFloats;
 }
 
+template <int WC>
 __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Lds &S, const Bufs &B, const Act &x,
                                               int lc, int c0, int nc) {
     const int lane = threadIdx.x & (kWave - 1);
@@ -1169,7 +1191,7 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
     // the pred rows, or the four gates of unit j = row0 / 4
     const float *btab = S.bias + bias_base(p, s.rank, s.P, layer - 1);
     TL(1);
-    run_phase(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache, p.red_slots,
+    run_phase<WC>(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache, p.red_slots,
               [&](int it, f32x4 acc) {
                   acc = quad_transpose(acc);   // every lane of the wave takes part
                   if (u >= nc) return;
@@ -1214,6 +1236,7 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
 // layers 0 and 1); otherwise layer 0 is split by unit tiles and followed by a
 // barrier.  Each later phase stages one layer's full new output and runs the
 // tiles that consume it.
+template <int WC>
 __device__ __forceinline__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned &epoch,
                               unsigned long long &tlast) {
     const int H = p.H, L = p.L;
@@ -1239,7 +1262,7 @@ __device__ __forceinline__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bu
             lds_sync();
             TL(0);
             pmark(p, s, tlast, kPrStageL);
-            consume_layer(p, s, S, B, x, lc, c0, nc);
+            consume_layer<WC>(p, s, S, B, x, lc, c0, nc);
             TL(6);
         }
         pmark(p, s, tlast, lc == L - 1 ? kPrPred : kPrL1);
@@ -1292,9 +1315,10 @@ __device__ __forceinline__ void gather_shards(const KParams &p, Ctl &s, unsigned
 // the decision keeps the prediction output (a TDT blank; an EOU blank, <EOB>
 // or special piece) and the next frame's column was evaluated, the walk goes
 // on with that column, one step per column, exactly as later iterations would.
-__device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp) {
-    gather_shards(p, s, stamp);
-    TLA(30);
+// CHAIN: spare columns were evaluated this iteration (otherwise sbase / sn are
+// stale and every utterance takes exactly one step).
+template <bool CHAIN>
+__device__ __forceinline__ void decide_steps(const KParams &p, Ctl &s, unsigned stamp) {
     for (int i = threadIdx.x; i < s.nj; i += kBlock) {
         const int ul = s.jst[i], b = s.b[ul];
         const bool writer = (ul % s.P) == s.rank;
@@ -1379,14 +1403,23 @@ __device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp)
                 }
             }
             // the next decision's frame offset from t0, if its column was evaluated
-            const int o = s.t[ul] - t0;
             s.brun[ul] = keep ? 1 : 0;
-            if (!keep || s.t[ul] >= s.T[ul] || o > s.sn[i]) break;
+            if (!CHAIN || !keep || s.t[ul] >= s.T[ul]) break;
+            const int o = s.t[ul] - t0;
+            if (o > s.sn[i]) break;
             col = s.sbase[i] + o - 1;
         }
     }
 }
 
+__device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp) {
+    gather_shards(p, s, stamp);
+    TLA(30);
+    if (s.ncol > s.nj) decide_steps<true>(p, s, stamp);
+    else decide_steps<false>(p, s, stamp);
+}
+
+template <int WC>
 __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
     __shared__ Ctl s;
@@ -1532,11 +1565,11 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         }
 #endif
         if (s.nl > 0) {
-            ok = lstm_and_pred(p, s, B, S, epoch, tlast);
+            ok = lstm_and_pred<WC>(p, s, B, S, epoch, tlast);
             if (!ok) break;
         }
         if (s.nj > 0) {
-            joint_phase(p, s, B, S, iter, tlast);
+            joint_phase<WC>(p, s, B, S, iter, tlast);
             ok = dom_sync(p, s, epoch);
             TLA(29);
             pmark(p, s, tlast, kPrJSync);
