@@ -828,7 +828,13 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
             ni = 0;
             ++nc;
         }
+        // q8_0 from L2: issued on every step (the last one reloads the current
+        // unit).  With a conditional prefetch the compiler's wait counts after
+        // the join assume no prefetch, so each unit's products would also wait
+        // for the next unit's first loads.  (Measured: B=256 q8_0 -6 %; the f16
+        // and LDS-cached paths are faster with the conditional form.)
         if (u + 1 < c1) load(j0 + ni, nc, fn);
+        else if (Q8 && !CACHED) load(j0 + i, c, fn);
         const int sb0 = c * U;
         if (c != cur) {
             unit_act(x, xo, two, sb0, min(U, KBe - sb0), ah, al);
