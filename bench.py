@@ -23,6 +23,11 @@ other workload shapes (--no-extras skips them):
                      state carried between chunk calls
 Each carries its own roofline ratio (roofline time of its lockstep
 iterations over the measured loop time).
+
+roofline.traffic (HBM bytes per launch of the decode loop) comes from two
+rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) that the default run makes in
+child processes before it touches the GPU, each one step of the same workload
+with a 256 MiB copy for calibration (--no-traffic skips them).
 """
 from __future__ import annotations
 
@@ -60,7 +65,43 @@ def parse():
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="counter_collection.csv of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
                          "this bench with --copy-probe 256: fills roofline.traffic")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc passes the default run makes for roofline.traffic")
     return ap.parse_args()
+
+
+def traffic_passes(args) -> tuple[list[str] | None, str | None]:
+    """HBM traffic of the decode loop at this workload: two rocprofv3 --pmc
+    passes (FETCH_SIZE, then WRITE_SIZE), each a child process running this
+    bench for one step with the copy calibration (--copy-probe 256), started
+    before this process touches the GPU.  Returns the two counter CSVs, or
+    None and the reason they are missing (no rocprofv3, already under a
+    profiler, or a failed pass)."""
+    import glob
+    import shutil
+    import subprocess
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None, "rocprofv3 not found"
+    if any(k.startswith("ROCPROF") for k in os.environ) or "rocprof" in os.environ.get("LD_PRELOAD", ""):
+        return None, "already running under a profiler"
+    out = tempfile.mkdtemp(prefix="pk_traffic_", dir="/tmp")
+    env = dict(os.environ, PK_LOOP_DISPATCH="1", TMPDIR="/tmp")
+    csvs = []
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = os.path.join(out, ctr)
+        cmd = ["timeout", "-s", "KILL", "180", exe, "--pmc", ctr, "--output-format", "csv", "-d", d, "-o", "c",
+               "--", sys.executable, os.path.abspath(__file__), "--batch", str(args.batch), "--frames",
+               str(args.frames), "--steps", "1", "--warmup", "0", "--no-extras", "--no-cpu", "--no-traffic",
+               "--copy-probe", "256"]
+        print(f"[bench] traffic pass {ctr}", file=sys.stderr, flush=True)
+        r = subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE,
+                           text=True, errors="replace")
+        found = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if r.returncode != 0 or not found:
+            return None, f"{ctr} pass failed (status {r.returncode}): {r.stderr[-300:]}"
+        csvs.append(found[0])
+    return csvs, None
 
 
 class Workload:
@@ -332,6 +373,11 @@ def main():
         print(json.dumps({"error": "this build measures one GPU: the decode path shards as independent "
                                    "utterances per GPU with no collective, and only --gpus 1 is run"}))
         sys.exit(2)
+    traffic_csvs, traffic_note = None, None
+    if args.traffic:
+        traffic_csvs = list(args.traffic)
+    elif not (args.no_traffic or args.no_extras or args.only):
+        traffic_csvs, traffic_note = traffic_passes(args)
     import __graft_entry__ as graft
     graft.load_package()
     from parakeet_amd import gguf, hipmem, pk, roofline, synth
@@ -417,12 +463,16 @@ def main():
 
     if copy_probe:
         out["copy_probe"] = copy_probe
-    if args.traffic:
-        tr = roofline.pmc_traffic(*args.traffic)
+    if traffic_csvs:
+        tr = roofline.pmc_traffic(*traffic_csvs)
         out["roofline"]["traffic"] = round(tr["bytes_per_launch"], 0)
         out["roofline"]["traffic_detail"] = {
             k: {"kib_per_dispatch": round(v["kib_per_dispatch"], 1), "copy_factor": round(v["factor"], 4)}
             for k, v in tr.items() if k != "bytes_per_launch"}
+        out["roofline"]["traffic_detail"]["source"] = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, one pass each, "
+                                                       "one step of this workload, scaled by a 256 MiB copy")
+    elif traffic_note:
+        out["roofline"]["traffic_detail"] = {"missing": traffic_note}
 
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
