@@ -236,7 +236,7 @@ int vec_f32(const pk_tensor &t, int n, const std::vector<int> *map, std::vector<
 
 // A matrix tiled as MFMA A fragments (see TMat in pk_device.h), host side.
 struct HostTiled {
-    int type = 0, rows = 0, tiles = 0, KB = 0;
+    int type = 0, rows = 0, tiles = 0, KB = 0, KBa = 0;
     std::vector<uint8_t> a, a_lo;
     std::vector<uint16_t> scale;   // q8_0 block scales as stored (f16 bits)
 };
@@ -247,7 +247,11 @@ int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *
     out.type = quantized(t.type) ? PK_TYPE_Q8_0 : t.type;   // q4_0 / q5_0 repacked exactly as q8_0
     out.rows = rows;
     out.tiles = (rows + kTile - 1) / kTile;
-    out.KB = cols / 32;
+    out.KBa = cols / 32;
+    // q8_0: stored with whole units of K blocks (zero quants and scales past K / 32),
+    // so the decode loop's q8_0 products never mask a unit
+    const int ub = pkdev::unit_blocks(out.type);
+    out.KB = out.type == PK_TYPE_Q8_0 ? (out.KBa + ub - 1) / ub * ub : out.KBa;
     const size_t frags = (size_t)out.tiles * out.KB;
     const uint8_t *src = static_cast<const uint8_t *>(t.data);
     if (quantized(t.type)) {
@@ -258,8 +262,8 @@ int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *
             for (int r = 0; r < kTile; ++r) {
                 const int row = tile * kTile + r;
                 if (row >= rows) continue;
-                const uint8_t *srow = src + (size_t)(map ? (*map)[row] : row) * out.KB * bb;
-                for (int kb = 0; kb < out.KB; ++kb) {
+                const uint8_t *srow = src + (size_t)(map ? (*map)[row] : row) * out.KBa * bb;
+                for (int kb = 0; kb < out.KBa; ++kb) {
                     const size_t f = (size_t)tile * out.KB + kb;
                     uint16_t dh;
                     int8_t q[32];
@@ -392,6 +396,7 @@ void arena_tiled(Arena &ar, HostTiled &h, TMat &m) {
     m.rows = h.rows;
     m.tiles = h.tiles;
     m.KB = h.KB;
+    m.KBa = h.KBa;
     ar.add(h.a.data(), h.a.size(), &m.a);
     ar.add(h.a_lo.data(), h.a_lo.size(), &m.a_lo);
     ar.add(h.scale.data(), h.scale.size() * 2, reinterpret_cast<const void **>(&m.scale));

@@ -56,7 +56,8 @@ struct TMat {
     const void *a_lo;              // f32 weights: low halves
     const unsigned short *scale;   // q8_0 block scales, f16 bits
     int type;                      // PK_TYPE_Q8_0, PK_TYPE_F16, PK_TYPE_F32
-    int rows, tiles, KB;
+    int rows, tiles, KB;           // KB: stored K blocks of 32 per tile row (q8_0: padded to whole units)
+    int KBa;                       // K blocks that hold weights (K / 32); blocks KBa .. KB-1 are zero
     int lds_off;                   // byte offset of this workgroup's tiles in its LDS weight cache, -1: not cached
 };
 
@@ -791,8 +792,6 @@ __device__ __forceinline__ f32x4 unit_mma(const uint4 (&f)[kUnitOf<Q8>], const h
 // Wave w's unit range [c0, c1) of N units.
 __device__ __forceinline__ int wave_cut(int N, int w) { return (int)(((long long)N * w) / kWaves); }
 
-__device__ __forceinline__ int blocks_per_item(const TMat &m) { return m.type == PK_TYPE_F32 ? 2 * m.KB : m.KB; }
-
 // Partials of items j0 .. j1-1 (one pass), K-major, next unit's weights prefetched.
 template <bool Q8, bool CACHED, bool FULL>
 __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMat &Bm, int j0, int j1, int rank, int P,
@@ -801,6 +800,7 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
     const int lane = threadIdx.x & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const bool two = !Q8 && A.type == PK_TYPE_F32;
     const int KBe = two ? 2 * A.KB : A.KB;
+    const int KBa = two ? 2 * A.KBa : A.KBa;          // blocks with weights (activations past them are never read)
     constexpr int U = kUnitOf<Q8>;
     const int S = (KBe + U - 1) / U;                  // units per item
     const int nj = j1 - j0, N = nj * S;
@@ -837,7 +837,7 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
         else if (Q8 && !CACHED) load(j0 + i, c, fn);
         const int sb0 = c * U;
         if (c != cur) {
-            unit_act(x, xo, two, sb0, min(U, KBe - sb0), ah, al);
+            unit_act(x, xo, two, sb0, min(U, KBa - sb0), ah, al);
             cur = c;
         }
         red[(i * S + c) * kWave + lane] = unit_mma<Q8>(fc, ah, al, two, sb0, f32x4{0.f, 0.f, 0.f, 0.f});
@@ -887,19 +887,15 @@ __device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm
     const int KBe = A.type == PK_TYPE_F32 ? 2 * A.KB : A.KB;
     const int U = unit_blocks(A.type);
     const int S = (KBe + U - 1) / U;
-    const bool full = KBe % U == 0;   // whole units: unmasked unit loads
     const int batch = red_slots / S;
     for (int j0 = 0; j0 < n_items; j0 += batch) {
         const int j1 = min(n_items, j0 + batch);
         if (j0 > 0) lds_sync();   // the previous pass's reduce has read its slots
+        // q8_0 matrices are stored with whole units of K blocks (zero blocks past
+        // K / 32), so their unit loads are never masked
         auto q8 = [&]() {
-            if (cached) {
-                if (full) phase_partials<true, true, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
-                else phase_partials<true, true, false>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
-            } else {
-                if (full) phase_partials<true, false, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
-                else phase_partials<true, false, false>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
-            }
+            if (cached) phase_partials<true, true, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
+            else phase_partials<true, false, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
         };
         auto half = [&]() {
             if (cached) phase_partials<false, true, false>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
