@@ -237,7 +237,7 @@ int vec_f32(const pk_tensor &t, int n, const std::vector<int> *map, std::vector<
 // A matrix tiled as MFMA A fragments (see TMat in pk_device.h), host side.
 struct HostTiled {
     int type = 0, rows = 0, tiles = 0, KB = 0, KBa = 0;
-    std::vector<uint8_t> a, a_lo;
+    std::vector<uint8_t> a;   // f32: the hi plane, then the lo plane
     std::vector<uint16_t> scale;   // q8_0 block scales as stored (f16 bits)
 };
 
@@ -248,10 +248,10 @@ int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *
     out.rows = rows;
     out.tiles = (rows + kTile - 1) / kTile;
     out.KBa = cols / 32;
-    // q8_0: stored with whole units of K blocks (zero quants and scales past K / 32),
-    // so the decode loop's q8_0 products never mask a unit
-    const int ub = pkdev::unit_blocks(out.type);
-    out.KB = out.type == PK_TYPE_Q8_0 ? (out.KBa + ub - 1) / ub * ub : out.KBa;
+    // stored with whole units of K blocks (zero weights and scales past K / 32; an f32
+    // block counts twice, once per plane), so the decode loop's products never mask a unit
+    const int ub = out.type == PK_TYPE_F32 ? pkdev::unit_blocks(out.type) / 2 : pkdev::unit_blocks(out.type);
+    out.KB = (out.KBa + ub - 1) / ub * ub;
     const size_t frags = (size_t)out.tiles * out.KB;
     const uint8_t *src = static_cast<const uint8_t *>(t.data);
     if (quantized(t.type)) {
@@ -276,14 +276,14 @@ int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *
             }
     } else {
         std::vector<float> row(cols);
-        out.a.assign(frags * kWave * 16, 0);
-        if (t.type == PK_TYPE_F32) out.a_lo.assign(frags * kWave * 16, 0);
+        const size_t plane = frags * kWave * 16;   // bytes of one f16 plane
+        out.a.assign(t.type == PK_TYPE_F32 ? 2 * plane : plane, 0);
         for (int tile = 0; tile < out.tiles; ++tile)
             for (int r = 0; r < kTile; ++r) {
                 const int rr = tile * kTile + r;
                 if (rr >= rows) continue;
                 row_f32(t, cols, map ? (*map)[rr] : rr, row.data());
-                for (int kb = 0; kb < out.KB; ++kb) {
+                for (int kb = 0; kb < out.KBa; ++kb) {
                     const size_t f = (size_t)tile * out.KB + kb;
                     for (int g = 0; g < 4; ++g)
                         for (int i = 0; i < 8; ++i) {
@@ -293,7 +293,7 @@ int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *
                             memcpy(&out.a[at], &hi, 2);
                             if (t.type == PK_TYPE_F32) {
                                 const _Float16 lo = (_Float16)(w - (float)hi);
-                                memcpy(&out.a_lo[at], &lo, 2);
+                                memcpy(&out.a[plane + at], &lo, 2);
                             }
                         }
                 }
@@ -398,7 +398,6 @@ void arena_tiled(Arena &ar, HostTiled &h, TMat &m) {
     m.KB = h.KB;
     m.KBa = h.KBa;
     ar.add(h.a.data(), h.a.size(), &m.a);
-    ar.add(h.a_lo.data(), h.a_lo.size(), &m.a_lo);
     ar.add(h.scale.data(), h.scale.size() * 2, reinterpret_cast<const void **>(&m.scale));
 }
 
@@ -588,6 +587,19 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     ar.add(w_enc_hi.data(), w_enc_hi.size() * 2, reinterpret_cast<const void **>(&dec->w_enc_hi));
     ar.add(w_enc_lo.data(), w_enc_lo.size() * 2, reinterpret_cast<const void **>(&dec->w_enc_lo));
     if ((rc = ar.upload(dec->arena))) return cleanup(rc);
+    // f32 matrices: the lo plane follows the hi plane in the same upload
+    {
+        auto lo_plane = [](pkdev::TMat &m) {
+            m.a_lo = m.type == PK_TYPE_F32 ? static_cast<const uint8_t *>(m.a) + (size_t)m.tiles * m.KB * kWave * 16
+                                           : nullptr;
+        };
+        for (int l = 0; l < L; ++l) {
+            lo_plane(kp.w_ih[l]);
+            lo_plane(kp.w_hh[l]);
+        }
+        lo_plane(kp.w_pred);
+        lo_plane(kp.w_out);
+    }
 
     // layer-0 input projection of every token: E'[v] = W_ih0 . embed[v] + b_ih0 + b_hh0 (f32)
     {

@@ -52,8 +52,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // weight rows), so a D fragment lane holds ONE weight row (l%16) for four
 // utterances (4(l/16) .. +3) and a q8_0 block needs one scale per lane.
 struct TMat {
-    const void *a;                 // fragment plane
-    const void *a_lo;              // f32 weights: low halves
+    const void *a;                 // fragment plane (f32 weights: the hi plane, then the lo plane)
+    const void *a_lo;              // f32 weights: the lo plane (a + one plane)
     const unsigned short *scale;   // q8_0 block scales, f16 bits
     int type;                      // PK_TYPE_Q8_0, PK_TYPE_F16, PK_TYPE_F32
     int rows, tiles, KB;           // KB: stored K blocks of 32 per tile row (q8_0: padded to whole units)
@@ -662,6 +662,7 @@ struct MatSrc {
     __amdgpu_buffer_rsrc_t r0, r1;
     const unsigned char *lds;
     int KB;
+    unsigned plane;   // f32: bytes of the hi plane (the lo plane's offset)
 };
 template <bool Q8, bool CACHED>
 __device__ __forceinline__ MatSrc mat_src(const TMat &m, bool two, const unsigned char *wc) {
@@ -669,13 +670,14 @@ __device__ __forceinline__ MatSrc mat_src(const TMat &m, bool two, const unsigne
     if (Q8) {
         s.r0 = rsrc(m.a, (unsigned)m.tiles * m.KB * kWave * 8u);
         s.r1 = rsrc(m.scale, (unsigned)m.tiles * m.KB * kTile * 2u);
-    } else {
+    } else {   // f32: both planes under one descriptor (the lo plane follows the hi plane)
         const unsigned bytes = (unsigned)m.tiles * m.KB * kWave * 16u;
-        s.r0 = rsrc(m.a, bytes);
-        s.r1 = rsrc(two ? m.a_lo : m.a, bytes);
+        s.r0 = rsrc(m.a, two ? 2 * bytes : bytes);
+        s.r1 = s.r0;
     }
     s.lds = CACHED ? wc + m.lds_off : nullptr;
     s.KB = m.KB;
+    s.plane = (unsigned)m.tiles * m.KB * kWave * 16u;
     return s;
 }
 
@@ -732,9 +734,11 @@ __device__ __forceinline__ void unit_load_src(const MatSrc &m, bool two, int til
             const int sb = sb0 + j;
             const int kb = two ? sb >> 1 : sb;
             const bool ok = FULL || j < nb;
-            const unsigned o = ok ? (unsigned)(((tile * m.KB + kb) * kWave + lane) * 16) : kBad;
-            f[j] = __builtin_bit_cast(uint4, (two && (sb & 1)) ? __builtin_amdgcn_raw_buffer_load_b128(m.r1, o, 0, 0)
-                                                               : __builtin_amdgcn_raw_buffer_load_b128(m.r0, o, 0, 0));
+            // f32: odd sub-blocks read the lo plane, m.plane bytes past the hi plane
+            const unsigned o = ok ? (unsigned)(((tile * m.KB + kb) * kWave + lane) * 16) +
+                                        ((two && (sb & 1)) ? m.plane : 0u)
+                                  : kBad;
+            f[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(m.r0, o, 0, 0));
         }
     }
 }
@@ -820,6 +824,10 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
     half8 ah[U], al[U];
     uint4 fa[U], fb[U];
     int u = c0, c = u / nj, i = u - c * nj, cur = -1;
+    // f16 / f32 from L2: the prefetch past the range reloads the wave's last unit,
+    // an address the compiler cannot equate with the set in flight (reloading the
+    // current unit, it copies that set instead, waiting for its loads)
+    const int cl = (c1 - 1) / nj, il = (c1 - 1) - cl * nj;
     load(j0 + i, c, fa);
     // one unit: issue the next unit's loads into fn, then multiply fc
     auto step = [&](uint4 (&fc)[U], uint4 (&fn)[U]) {
@@ -835,6 +843,7 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
         // and LDS-cached paths are faster with the conditional form.)
         if (u + 1 < c1) load(j0 + ni, nc, fn);
         else if (Q8 && !CACHED) load(j0 + i, c, fn);
+        else if (!CACHED) load(j0 + il, cl, fn);   // f16 / f32: the wave's last unit (see below)
         const int sb0 = c * U;
         if (c != cur) {
             unit_act(x, xo, two, sb0, min(U, KBa - sb0), ah, al);
@@ -891,15 +900,15 @@ __device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm
     for (int j0 = 0; j0 < n_items; j0 += batch) {
         const int j1 = min(n_items, j0 + batch);
         if (j0 > 0) lds_sync();   // the previous pass's reduce has read its slots
-        // q8_0 matrices are stored with whole units of K blocks (zero blocks past
-        // K / 32), so their unit loads are never masked
+        // matrices are stored with whole units of K blocks (zero blocks past
+        // K / 32), so unit loads are never masked
         auto q8 = [&]() {
             if (cached) phase_partials<true, true, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
             else phase_partials<true, false, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
         };
         auto half = [&]() {
-            if (cached) phase_partials<false, true, false>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
-            else phase_partials<false, false, false>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
+            if (cached) phase_partials<false, true, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
+            else phase_partials<false, false, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
         };
         if constexpr (WC == kWcQ8) q8();
         else if constexpr (WC == kWcHalf) half();
