@@ -362,7 +362,8 @@ struct pk_decoder {
     unsigned char *scratch = nullptr;   // this device's fixed scratch array (pk_decode_noalloc)
     int last_iters = 0;
     int lock_fd = -1;          // this GPU's cross-process loop lock (see DeviceLoopLock), -1: none
-    const void *loop_fn = nullptr;   // the decode-loop instantiation for this decoder's weight storage
+    const void *loop_fn[2] = {};   // the decode-loop instantiations for this decoder's weight storage:
+                                   // several domains, one domain (argmax key slots)
 };
 
 namespace {
@@ -674,24 +675,32 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
         for (int l = 1; l < kp.L; ++l) see(kp.w_ih[l]);
         see(kp.w_pred);
         see(kp.w_out);
-        dec->loop_fn = all_q8 ? reinterpret_cast<const void *>(pkdev::decode_loop_kernel<pkdev::kWcQ8>)
-                     : all_half ? reinterpret_cast<const void *>(pkdev::decode_loop_kernel<pkdev::kWcHalf>)
-                                : reinterpret_cast<const void *>(pkdev::decode_loop_kernel<pkdev::kWcAny>);
+        using namespace pkdev;
+        dec->loop_fn[0] = all_q8 ? reinterpret_cast<const void *>(decode_loop_kernel<kWcQ8, false>)
+                        : all_half ? reinterpret_cast<const void *>(decode_loop_kernel<kWcHalf, false>)
+                                   : reinterpret_cast<const void *>(decode_loop_kernel<kWcAny, false>);
+        dec->loop_fn[1] = all_q8 ? reinterpret_cast<const void *>(decode_loop_kernel<kWcQ8, true>)
+                        : all_half ? reinterpret_cast<const void *>(decode_loop_kernel<kWcHalf, true>)
+                                   : reinterpret_cast<const void *>(decode_loop_kernel<kWcAny, true>);
     }
-    hipFuncAttributes fa{};
-    if (hipFuncGetAttributes(&fa, dec->loop_fn) != hipSuccess)
-        return cleanup(fail(PK_ERR_DEVICE, "hipFuncGetAttributes"));
-    const size_t stat = fa.sharedSizeBytes;
+    size_t stat = 0;   // the larger static LDS of the two instantiations
+    for (const void *fn : dec->loop_fn) {
+        hipFuncAttributes fa{};
+        if (hipFuncGetAttributes(&fa, fn) != hipSuccess) return cleanup(fail(PK_ERR_DEVICE, "hipFuncGetAttributes"));
+        stat = std::max(stat, fa.sharedSizeBytes);
+    }
     const size_t need = (size_t)dec->lds_block > stat ? (size_t)dec->lds_block - stat : 0;
     if (dec->lds_fixed + (size_t)2 * kWaves * kWave * 16 > need)
         return cleanup(fail(PK_ERR_UNSUPPORTED, "LDS %zu B needed, %d available", dec->lds_fixed + stat,
                             dec->lds_block));
     dec->lds_bytes = need;
-    if (hipFuncSetAttribute(dec->loop_fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)need) != hipSuccess)
-        return cleanup(fail(PK_ERR_DEVICE, "hipFuncSetAttribute"));
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, dec->loop_fn, kBlock, need) != hipSuccess || per_cu < 1)
-        return cleanup(fail(PK_ERR_DEVICE, "decode kernel does not fit on a CU"));
+    for (const void *fn : dec->loop_fn) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)need) != hipSuccess)
+            return cleanup(fail(PK_ERR_DEVICE, "hipFuncSetAttribute"));
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kBlock, need) != hipSuccess || per_cu < 1)
+            return cleanup(fail(PK_ERR_DEVICE, "decode kernel does not fit on a CU"));
+    }
     dec->nwg = std::min(dec->n_cu, kBlock);
     if ((rc = scratch_address(dec->device, &dec->scratch))) return cleanup(rc);
     dec->lock_fd = open_loop_lock(dec->device);
@@ -868,7 +877,7 @@ int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds) {
     if (!last) HIP_TRY(hipEventCreateWithFlags(&last, hipEventDisableTiming));
     HIP_TRY(hipStreamWaitEvent(dec->stream, last, 0));
     void *args[] = {&p};
-    const void *fn = dec->loop_fn;
+    const void *fn = dec->loop_fn[p.slots ? 1 : 0];   // one domain: the argmax-slot instantiation
     bool &refused = g_loops.coop_refused[dec->device];
     // PK_LOOP_DISPATCH=1: ordinary dispatch from the first launch on.  For
     // profiler runs: rocprofv3 (ROCm 7.2) ends with SIGSEGV in the HIP
@@ -1092,9 +1101,13 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     p.shards = 1;
     while (p.shards < pkdev::kShards && p.shards * 8 < pl.P) p.shards *= 2;
     const size_t keys_bytes = (size_t)2 * pl.n_dom * pkdev::kColCap * p.shards * 2 * 8;
+    // one-domain launches: per-workgroup argmax key slots (used while at most
+    // kSlotCols joint columns are live)
+    const size_t slots_bytes = pl.n_dom == 1 ? (size_t)2 * pl.P * pkdev::kSlotCols * 2 * 8 : 0;
     // the words every launch starts from zero, in one allocation cleared by
-    // one fill: 64 B of status, the barrier flags, the argmax keys
-    const size_t flags_bytes = (size_t)nwg * kFlagStride * 4, clear_bytes = 256 + flags_bytes + keys_bytes;
+    // one fill: 64 B of status, the barrier flags, the argmax keys and slots
+    const size_t flags_bytes = (size_t)nwg * kFlagStride * 4,
+                 clear_bytes = 256 + flags_bytes + keys_bytes + slots_bytes;
     void *d_clear = nullptr, *d_xchg = nullptr;
     if ((rc = cs.get(dec->d_clear, clear_bytes, &d_clear))) return rc;
     const size_t xh = 2 * (size_t)L * m * H, xp = (size_t)m * J, xr = 2 * (size_t)L * m * 4 * H;
@@ -1110,6 +1123,9 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     p.status = static_cast<int *>(d_clear) + 4;
     p.flags = reinterpret_cast<unsigned *>(static_cast<uint8_t *>(d_clear) + 256);
     p.keys = reinterpret_cast<unsigned long long *>(static_cast<uint8_t *>(d_clear) + 256 + flags_bytes);
+    p.slots = slots_bytes ? reinterpret_cast<unsigned long long *>(static_cast<uint8_t *>(d_clear) + 256 +
+                                                                 flags_bytes + keys_bytes)
+                          : nullptr;
     if (cs.fixed) {   // the fixed scratch keeps the last call's contents: cleared by a fill kernel
         const size_t words = clear_bytes / 4;   // clear_bytes is a multiple of 32
         pkdev::fill_zero_kernel<<<(unsigned)std::min<size_t>((words + 255) / 256, 1024), 256, 0, dec->stream>>>(

@@ -26,6 +26,8 @@ constexpr int kStampShift = 46;             // argmax key: 14 index + 32 value b
 constexpr unsigned kMaxStamp = (1u << 18) - 1;
 constexpr int kFlagStride = 64;             // words between barrier flags (256 B)
 constexpr int kShards = 32;                 // argmax keys: most max targets per utterance and head
+constexpr int kSlotCols = 2;                // one-domain launches with at most this many joint columns
+                                            // exchange argmax keys through per-workgroup slots
 constexpr int kKPad = 8;                    // halves of padding per staged row (bank spread)
 
 // Flags in the per-utterance control word.
@@ -124,6 +126,8 @@ struct KParams {
     int bias_floats;             // LDS bias table size (floats)
     int wcache_bytes;            // LDS weight cache per workgroup (0: weights are read from L2)
     unsigned long long *prof;    // nullable: per-phase wall-clock totals of workgroup 0 (100 MHz ticks)
+    unsigned long long *slots;   // nullable (one-domain launches): [2][P][kSlotCols][2] stamped best keys
+                                 // of each workgroup, by iteration parity
 };
 
 // Phase timers (workgroup 0 only, when p.prof is set): totals kept in LDS,
@@ -1003,9 +1007,21 @@ __device__ __forceinline__ void cache_matrix(const TMat &m, int rank, int P, uns
     }
 }
 
+// A one-domain launch with at most kSlotCols joint columns exchanges the argmax
+// keys through per-workgroup slots instead of atomics, a barrier and a gather:
+// each workgroup stores its stamped best key per column and head in its own
+// slot, and every workgroup polls all slots until each carries this
+// iteration's stamp (the stamp is the arrival signal).  One round trip instead
+// of two.  The condition is the same in every workgroup of the domain; ONE
+// launches (one domain, p.slots set) run their own instantiation of the loop.
+template <bool ONE>
+__device__ __forceinline__ bool slot_mode(const Ctl &s) {
+    return ONE && s.ncol <= kSlotCols;
+}
+
 // Joint + argmax for this workgroup's output tiles.  Utterances are processed
 // 16 at a time (one MFMA column tile).
-template <int WC>
+template <int WC, bool ONE>
 __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned stamp,
                             unsigned long long &tlast) {
     const int J = p.J, lane = threadIdx.x & (kWave - 1);
@@ -1106,6 +1122,16 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         lds_sync();
         TLA(27);
         pmark(p, s, tlast, kPrJCompute);
+    }
+    if (slot_mode<ONE>(s)) {   // this workgroup's stamped best keys into its own slot
+        if (threadIdx.x < 2 * s.ncol) {
+            const int u = threadIdx.x / 2, head = threadIdx.x % 2;
+            __hip_atomic_store(p.slots + (((size_t)(stamp & 1) * s.P + s.rank) * kSlotCols + u) * 2 + head,
+                               ((unsigned long long)stamp << kStampShift) | s.wgkey[u][head], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        TLA(28);
+        return;
     }
     // one device-scope max per utterance and head into shard rank % kShards
     // (spreads the atomics of many workgroups over several words); the stamp
@@ -1324,6 +1350,53 @@ __device__ __forceinline__ void gather_shards(const KParams &p, Ctl &s, unsigned
     lds_sync();
 }
 
+// The domain's best key per joint column and head from the workgroups' slots
+// (slot mode): thread e polls slot (pair e / P, rank e % P) until it carries
+// stamp, each wave takes the maximum per pair, and one LDS atomic max per wave
+// and pair lands in s.wgkey (stamped keys are above the unstamped local ones it
+// holds).  Bounded like dom_sync: false on an error or a ~2 s wait.
+__device__ __forceinline__ bool gather_slots(const KParams &p, Ctl &s, unsigned stamp) {
+    __shared__ int s_ok;
+    if (threadIdx.x == 0) s_ok = 1;
+    lds_sync();   // this workgroup's slot stores have read s.wgkey
+    const int P = s.P, npair = 2 * s.ncol, n = npair * P;
+    const unsigned long long *sl = p.slots + (size_t)(stamp & 1) * P * kSlotCols * 2;
+    const int lane = threadIdx.x & (kWave - 1);
+    for (int e0 = 0; e0 < n; e0 += kBlock) {   // whole waves stay together
+        const int e = e0 + threadIdx.x;
+        unsigned long long k = 0ull;
+        int pair = -1;
+        if (e < n) {
+            pair = e / P;
+            const int r = e - pair * P;
+            const unsigned long long *w = sl + ((size_t)r * kSlotCols + (pair >> 1)) * 2 + (pair & 1);
+            const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+            unsigned m = 0;
+            while (key_stamp(k = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) != stamp) {
+                if ((++m & 63) != 0) continue;
+                if (__hip_atomic_load(p.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) { s_ok = 0; break; }
+                if (__builtin_amdgcn_s_memrealtime() - t0 > 200000000ull) {   // 100 MHz clock: 2 s
+                    __hip_atomic_store(p.status, PK_ERR_TIMEOUT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    s_ok = 0;
+                    break;
+                }
+            }
+        }
+        for (int q = 0; q < npair; ++q) {
+            unsigned long long v = pair == q ? k : 0ull;
+#pragma unroll
+            for (int m = 1; m < kWave; m <<= 1) {
+                const unsigned long long o = __shfl_xor(v, m, kWave);
+                v = o > v ? o : v;
+            }
+            if (lane == 0 && v != 0ull) atomicMax(&s.wgkey[q >> 1][q & 1], v);
+        }
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    lds_sync();
+    return s_ok != 0;
+}
+
 // One utterance per thread.  Its first decision is column i (frame t); while
 // the decision keeps the prediction output (a TDT blank; an EOU blank, <EOB>
 // or special piece) and the next frame's column was evaluated, the walk goes
@@ -1425,14 +1498,14 @@ __device__ __forceinline__ void decide_steps(const KParams &p, Ctl &s, unsigned 
     }
 }
 
-__device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp) {
-    gather_shards(p, s, stamp);
+__device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp, bool gathered) {
+    if (!gathered) gather_shards(p, s, stamp);
     TLA(30);
     if (s.ncol > s.nj) decide_steps<true>(p, s, stamp);
     else decide_steps<false>(p, s, stamp);
 }
 
-template <int WC>
+template <int WC, bool ONE>
 __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
     __shared__ Ctl s;
@@ -1582,12 +1655,13 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
             if (!ok) break;
         }
         if (s.nj > 0) {
-            joint_phase<WC>(p, s, B, S, iter, tlast);
-            ok = dom_sync(p, s, epoch);
+            joint_phase<WC, ONE>(p, s, B, S, iter, tlast);
+            const bool slots = slot_mode<ONE>(s);
+            ok = slots ? gather_slots(p, s, iter) : dom_sync(p, s, epoch);
             TLA(29);
             pmark(p, s, tlast, kPrJSync);
             if (!ok) break;
-            decide(p, s, iter);
+            decide(p, s, iter, slots);
         }
         lds_sync();
         build_lists(s, p.spec != 0);
