@@ -1102,8 +1102,11 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     while (p.shards < pkdev::kShards && p.shards * 8 < pl.P) p.shards *= 2;
     const size_t keys_bytes = (size_t)2 * pl.n_dom * pkdev::kColCap * p.shards * 2 * 8;
     // one-domain launches: per-workgroup argmax key slots (used while at most
-    // kSlotCols joint columns are live)
-    const size_t slots_bytes = pl.n_dom == 1 ? (size_t)2 * pl.P * pkdev::kSlotCols * 2 * 8 : 0;
+    // kSlotCols joint columns are live); PK_ARGMAX_SLOTS=0 keeps the sharded
+    // atomics and barrier instead (for comparisons)
+    const char *slots_env = std::getenv("PK_ARGMAX_SLOTS");
+    const bool use_slots = pl.n_dom == 1 && !(slots_env && slots_env[0] == '0');
+    const size_t slots_bytes = use_slots ? (size_t)2 * pl.P * pkdev::kSlotCols * 2 * 8 : 0;
     // the words every launch starts from zero, in one allocation cleared by
     // one fill: 64 B of status, the barrier flags, the argmax keys and slots
     const size_t flags_bytes = (size_t)nwg * kFlagStride * 4,

@@ -35,8 +35,11 @@ def _both(dev, encs, n, **kw):
     return on, off, it_on, it_off
 
 
-@pytest.mark.parametrize("B", [1, 4, 40])
+@pytest.mark.parametrize("B", [1, 2, 4, 40])
 def test_tdt_blank_runs_replay_and_equal(tmp_path, B):
+    """B=1 and B=2 run the one-domain loop, whose argmax exchange switches between
+    the per-workgroup key slots (at most 2 joint columns) and the sharded atomics
+    (spare columns in use) from one iteration to the next."""
     from parakeet_amd import gguf, pk, synth
     import oracle
     path = str(tmp_path / "m.gguf")
@@ -95,4 +98,34 @@ def test_tdt_blank_runs_across_windows(tmp_path):
     for t0 in range(0, 70, 7):
         toks += dev.decode([enc[t0:t0 + 7]], slots=[1], blank_bias=bb)[0]["tokens"].tolist()
     assert toks == whole["tokens"].tolist()
+    dev.close()
+
+
+@pytest.mark.parametrize("B", [1, 2])
+def test_argmax_slots_equal_sharded_atomics(tmp_path, B):
+    """One-domain launches exchange the argmax keys through per-workgroup slots
+    while at most 2 joint columns are live; PK_ARGMAX_SLOTS=0 runs the same decode
+    with the sharded atomics and barrier.  Tokens, steps, traces and final state
+    are bit-identical, with and without runs of blanks (which switch the exchange
+    between the two forms from one iteration to the next)."""
+    from parakeet_amd import pk, synth
+    path = str(tmp_path / "m.gguf")
+    small_tdt(path)
+    dev = pk.Decoder.from_gguf(path, n_slots=8 * B)
+    encs = [synth.encoder_frames(1500 + u, 45 + 9 * u, 128) for u in range(B)]
+    for k, bias in enumerate((0.0, 3.0)):
+        bb = np.full(B, bias, np.float32)
+        base = 4 * B * k
+        os.environ["PK_ARGMAX_SLOTS"] = "0"
+        try:
+            ref = dev.decode(encs, slots=list(range(base + B, base + 2 * B)), trace=True, blank_bias=bb, max_symbols=5)
+        finally:
+            os.environ.pop("PK_ARGMAX_SLOTS", None)
+        got = dev.decode(encs, slots=list(range(base, base + B)), trace=True, blank_bias=bb, max_symbols=5)
+        for u in range(B):
+            assert np.array_equal(got[u]["tokens"], ref[u]["tokens"]), (bias, u)
+            assert np.array_equal(got[u]["trace"], ref[u]["trace"]), (bias, u)
+            assert got[u]["steps"] == ref[u]["steps"], (bias, u)
+            a, b = dev.read_state(base + u), dev.read_state(base + B + u)
+            assert np.array_equal(a["h"], b["h"]) and np.array_equal(a["c"], b["c"]), (bias, u)
     dev.close()
