@@ -358,6 +358,9 @@ struct pk_decoder {
     // per-call scratch
     DevBuf d_desc, d_encp, d_clear, d_enc, d_out, d_xchg, d_prof;   // d_clear: status, barrier flags, argmax keys
     std::vector<uint8_t> h_desc;
+    HostBuf h_pin;             // pinned: 16 B of status read back, then the descriptor block
+                               // (sized at creation for n_slots utterances, so the uploads and the
+                               // status read are asynchronous copies and no call allocates it)
     HostBuf h_out;             // staging of host-memory outputs
     unsigned char *scratch = nullptr;   // this device's fixed scratch array (pk_decode_noalloc)
     int last_iters = 0;
@@ -704,6 +707,11 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     dec->nwg = std::min(dec->n_cu, kBlock);
     if ((rc = scratch_address(dec->device, &dec->scratch))) return cleanup(rc);
     dec->lock_fd = open_loop_lock(dec->device);
+    {   // the largest descriptor block of a call (n_slots utterances; at most nwg domains of kDomCap)
+        const size_t nwg = (size_t)dec->nwg;
+        const size_t most = (size_t)n_slots * (2 * 8 + 5 * 4) + 4 * (nwg + nwg * kDomCap + 3 * nwg);
+        if ((rc = dec->h_pin.ensure(16 + most))) return cleanup(rc);
+    }
     if (hipStreamCreateWithFlags(&dec->stream, hipStreamNonBlocking) != hipSuccess)
         return cleanup(fail(PK_ERR_DEVICE, "stream"));
     for (auto &e : dec->ev)
@@ -1006,8 +1014,13 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     const size_t desc_bytes = n64 * 8 + n32 * 4;
     void *d_desc = nullptr;
     if ((rc = cs.get(dec->d_desc, desc_bytes, &d_desc))) return rc;
-    dec->h_desc.resize(desc_bytes);
-    uint8_t *hd = dec->h_desc.data();
+    uint8_t *hd;
+    if (16 + desc_bytes <= dec->h_pin.n) {
+        hd = dec->h_pin.as<uint8_t>() + 16;
+    } else {
+        dec->h_desc.resize(desc_bytes);
+        hd = dec->h_desc.data();
+    }
     size_t off = 0;
     auto put = [&](const void *src, size_t bytes) {
         memcpy(hd + off, src, bytes);
@@ -1208,8 +1221,8 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     const DeviceLoopLock cross_process(dec->lock_fd);
     if ((rc = launch_loop(dec, nwg, p, lds))) return rc;
     HIP_TRY(hipEventRecord(dec->ev[2], dec->stream));
-    int status[4] = {0, 0, 0, 0};
-    HIP_TRY(hipMemcpyAsync(status, p.status, sizeof status, hipMemcpyDeviceToHost, dec->stream));
+    int *status = dec->h_pin.as<int>();   // read after the stream synchronisation below
+    HIP_TRY(hipMemcpyAsync(status, p.status, 4 * sizeof(int), hipMemcpyDeviceToHost, dec->stream));
     if (host) {
         // the counters of every utterance in one copy (n_tokens, steps,
         // n_segments are consecutive), then the filled prefix of each output
