@@ -799,18 +799,21 @@ __device__ __forceinline__ f32x4 unit_mma(const uint4 (&f)[kUnitOf<Q8>], const h
     return acc + lo;
 }
 
-// Wave w's unit range [c0, c1) of N units.
-// Waves w and w + 4 share a SIMD, and the older one (w < 4) wins the issue
-// arbitration: for equal ranges the younger one finishes 15-30 % later, and the
-// reduce waits for it.  With at least 6 units per wave, waves 0-3 take 19 %
-// more than an even share and waves 4-7 19 % less (shares of 76 and 52 in
-// 64ths; 4 x 76 + 4 x 52 = 512).  Partials are reduced in chunk order, so the
-// split does not change results.  Measured: B=256 -1.5 %, ragged B=512 -1.8 %,
-// TDT-1.1b f16 -1.9 %; a 28 % skew gained no more, 38 % less.
-__device__ __forceinline__ int wave_cut(int N, int w) {
+// Wave w's unit range [c0, c1) of N units.  Waves w and w + 4 share SIMD w & 3,
+// and the older one (w < 4) wins the issue arbitration: for equal ranges the
+// younger one finishes 15-30 % later, and the reduce waits for it.  So each SIMD
+// gets an even quarter of the units, and its older wave takes the odd unit and,
+// with at least 12 units per SIMD, 19 % more than half (76 / 128).  Partials are
+// reduced in chunk order, so the split does not change results.  Measured
+// against an even split over the 8 waves (two A/Bs chained): B=256, ragged
+// B=512 and TDT-1.1b f16 about -3 %, B=64 -0.5 %, B=1 +1.5 %; a 28 % skew
+// gained no more.
+__device__ __forceinline__ void wave_range(int N, int w, int &c0, int &c1) {
+    const int j = w & 3, a = (N * j) >> 2, b = (N * (j + 1)) >> 2, len = b - a;
     const int d = N >= 48 ? 12 : 0;
-    const int k = w * (64 + d) - 2 * d * max(w - 4, 0);
-    return (int)(((long long)N * k) / (kWaves * 64));
+    const int o = (len * (64 + d) + 64) >> 7;   // the older wave's share of its SIMD's range
+    c0 = w < 4 ? a : a + o;
+    c1 = w < 4 ? a + o : b;
 }
 
 // Partials of items j0 .. j1-1 (one pass), K-major, next unit's weights prefetched.
@@ -825,7 +828,8 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
     constexpr int U = kUnitOf<Q8>;
     const int S = (KBe + U - 1) / U;                  // units per item
     const int nj = j1 - j0, N = nj * S;
-    const int c0 = wave_cut(N, wave), c1 = wave_cut(N, wave + 1);
+    int c0, c1;
+    wave_range(N, wave, c0, c1);
     if (c0 >= c1) return;
     // Column c of the product depends only on row c of the activations; rows
     // past x.n are not staged (they hold older values) and the columns they
