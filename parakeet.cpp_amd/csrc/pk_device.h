@@ -431,6 +431,9 @@ struct Ctl {                      // per-workgroup copy of its domain's control 
     int dur[PK_MAX_DURATIONS];    // duration values (the decision step reads them from LDS)
     int n, nl, nj;
     int dom, rank, P;
+    // this workgroup's tiles of an LSTM matrix, of W_p and of W_o (fixed for the
+    // launch; computed once, since each is an integer division)
+    int own_lstm, own_pred, own_out;
     unsigned long long wgkey[kColCap][2];   // this workgroup's best key per joint column and head
     unsigned long long prof[kPrN];
 };
@@ -961,12 +964,10 @@ struct Lds {
 // Epilogue bias rows of this workgroup's tiles, in LDS for the whole launch:
 // the 16 rows of each owned tile of W_ih_l (b_ih_l + b_hh_l, l = 1 .. L-1;
 // 4H/16 tiles each), then of W_p (b_p; J/16 tiles), then of W_o (b_o).
-// bias_base gives the table offset (floats) of matrix index m (0 .. L-2
-// LSTM, L-1 pred, L joint).
-__device__ __forceinline__ int bias_base(const KParams &p, int rank, int P, int m) {
-    const int n_lstm = owned(p.H / 4, rank, P), n_pred = owned(p.J / kTile, rank, P);   // 4H/16 and J/16 tiles
-    return kTile * (m < p.L ? m * n_lstm : (p.L - 1) * n_lstm + n_pred);
-}
+// The rows of matrix m start at float kTile * m * own_lstm (m = 0 .. L-2 the
+// LSTM layers 1 .. L-1, m = L-1 W_p) and W_o's at kTile * ((L-1) * own_lstm +
+// own_pred): H and J are multiples of 32, so own_lstm and own_pred count the
+// 4H/16 and J/16 tiles used here.
 __device__ __forceinline__ void bias_table(const KParams &p, int rank, int P, float *tab) {
     const int n_lstm = owned(p.H / 4, rank, P), n_pred = owned(p.J / kTile, rank, P);
     const int n_out = owned(p.w_out.tiles, rank, P);
@@ -1041,7 +1042,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
                             unsigned long long &tlast) {
     const int J = p.J, lane = threadIdx.x & (kWave - 1);
     if (threadIdx.x < 2 * kColCap) s.wgkey[threadIdx.x / 2][threadIdx.x % 2] = 0ull;
-    const int n_out = owned(p.w_out.tiles, s.rank, s.P);
+    const int n_out = s.own_out;
     for (int c0 = 0; c0 < s.ncol; c0 += kTile) {
         const int nc = min(kTile, s.ncol - c0);
         Act x = S.act[0];
@@ -1089,7 +1090,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         const int u = 4 * (lane >> 4) + (lane & 3), g = (lane >> 2) & 3;
         const float bb = u < nc ? s.bbias[s.cu[c0 + u]] : 0.0f;
         // (b_out is zero-padded to whole tiles)
-        const float *btab = S.bias + bias_base(p, s.rank, s.P, p.L);
+        const float *btab = S.bias + kTile * ((p.L - 1) * s.own_lstm + s.own_pred);
         TL(1);
         // debug logit tap: this lane's utterance row of the current step
         float *ltap = nullptr;
@@ -1173,7 +1174,7 @@ constexpr int kL0 = 3;
 __device__ __forceinline__ void lstm_layer0(const KParams &p, Ctl &s, const Lds &S, const Bufs &B, bool redundant) {
     const int H = p.H;
     const int groups = p.w_hh[0].tiles;                 // unit groups of 4
-    const int n_own = owned(groups, s.rank, s.P);
+    const int n_own = s.own_lstm;
     const int nunits = redundant ? H : 4 * n_own;
     const int n_work = s.nl * nunits;
     for (int base = 0; base < n_work; base += kL0 * kBlock) {
@@ -1233,7 +1234,7 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
     const bool last = lc == p.L - 1;
     const TMat &wc = last ? p.w_pred : p.w_ih[lc + 1];
     const TMat &wr = p.w_hh[lc];
-    const int n_c = owned(wc.tiles, s.rank, s.P), n_r = owned(wr.tiles, s.rank, s.P);
+    const int n_c = last ? s.own_pred : s.own_lstm, n_r = s.own_lstm;
     // the epilogue quad-transposes the (transposed) D fragment, after which a
     // lane holds rows 4g .. 4g+3 of a tile (the four gates of one unit, or four
     // pred rows) for one utterance u of the column tile
@@ -1243,7 +1244,7 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
     const bool zero = s.flags[ul] & kFlagZeroHC;
     // bias rows of the consumer tiles (LDS table): lane rows row0 .. row0+3 are
     // the pred rows, or the four gates of unit j = row0 / 4
-    const float *btab = S.bias + bias_base(p, s.rank, s.P, layer - 1);
+    const float *btab = S.bias + kTile * lc * s.own_lstm;
     TL(1);
     run_phase<WC>(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache, p.red_slots,
               [&](int it, f32x4 acc) {
@@ -1571,6 +1572,9 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         s.rank = p.wg_rank[wg];
         s.P = p.dom_size;
         s.n = p.dom_n[s.dom];
+        s.own_lstm = owned(p.w_hh[0].tiles, s.rank, s.P);
+        s.own_pred = owned(p.w_pred.tiles, s.rank, s.P);
+        s.own_out = owned(p.w_out.tiles, s.rank, s.P);
     }
     if (threadIdx.x < PK_MAX_DURATIONS) s.dur[threadIdx.x] = threadIdx.x < p.n_dur ? p.durations[threadIdx.x] : 0;
     __syncthreads();
