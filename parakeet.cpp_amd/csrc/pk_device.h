@@ -434,6 +434,9 @@ struct Ctl {                      // per-workgroup copy of its domain's control 
     // this workgroup's tiles of an LSTM matrix, of W_p and of W_o (fixed for the
     // launch; computed once, since each is an integer division)
     int own_lstm, own_pred, own_out;
+    int pass[PK_MAX_LAYERS + 1];  // items per pass of the phase consuming layer l's output (l < L), of W_o (L)
+    unsigned mag_p, mag_h, mag_units;   // udiv multipliers for P, H and 4 * own_lstm
+    unsigned wmask;               // bit ul: this workgroup writes utterance ul's outputs (ul % P == rank)
     unsigned long long wgkey[kColCap][2];   // this workgroup's best key per joint column and head
     unsigned long long prof[kPrN];
 };
@@ -847,11 +850,20 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
     };
     half8 ah[U], al[U];
     uint4 fa[U], fb[U];
-    int u = c0, c = u / nj, i = u - c * nj, cur = -1;
+    // u = c * nj + i: c < S, so short wave-uniform loops instead of divisions
+    int u = c0, c = 0, i = c0, cur = -1;
+    while (i >= nj) {
+        i -= nj;
+        ++c;
+    }
     // f16 / f32 from L2: the prefetch past the range reloads the wave's last unit,
     // an address the compiler cannot equate with the set in flight (reloading the
     // current unit, it copies that set instead, waiting for its loads)
-    const int cl = (c1 - 1) / nj, il = (c1 - 1) - cl * nj;
+    int cl = 0, il = c1 - 1;
+    while (il >= nj) {
+        il -= nj;
+        ++cl;
+    }
     load(j0 + i, c, fa);
     // one unit: issue the next unit's loads into fn, then multiply fc
     auto step = [&](uint4 (&fc)[U], uint4 (&fn)[U]) {
@@ -910,17 +922,16 @@ __device__ __forceinline__ void phase_reduce(int j0, int j1, int S, const f32x4 
 enum { kWcQ8 = 0, kWcHalf = 1, kWcAny = 2 };
 
 // Products of one phase for this workgroup, then the epilogue per item, in
-// passes of at most red_slots / S items.
+// passes of at most `batch` items (red_slots / S, computed once per launch).
 template <int WC, class EpiFn>
 __device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm, int n_items, int rank, int P,
-                                          const Act &x, f32x4 *red, const unsigned char *wc, int red_slots, EpiFn epi) {
+                                          const Act &x, f32x4 *red, const unsigned char *wc, int batch, EpiFn epi) {
     if (n_items <= 0) return;
     // both matrices of a phase are in the LDS weight cache or neither
     const bool cached = wc != nullptr && A.lds_off >= 0;
     const int KBe = A.type == PK_TYPE_F32 ? 2 * A.KB : A.KB;
-    const int U = unit_blocks(A.type);
+    const int U = WC == kWcQ8 ? kUnitOf<true> : WC == kWcHalf ? kUnitOf<false> : unit_blocks(A.type);
     const int S = (KBe + U - 1) / U;
-    const int batch = red_slots / S;
     for (int j0 = 0; j0 < n_items; j0 += batch) {
         const int j1 = min(n_items, j0 + batch);
         if (j0 > 0) lds_sync();   // the previous pass's reduce has read its slots
@@ -944,6 +955,18 @@ __device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm
 
 // Tiles of a matrix with `tiles` row tiles owned by rank r of P: t = r, r+P, ...
 __device__ __forceinline__ int owned(int tiles, int r, int P) { return tiles > r ? (tiles - r + P - 1) / P : 0; }
+
+// n / d without a division, for n * d < 2^32: with m = floor(2^32 / d) + 1,
+// floor(n * m / 2^32) = floor(n / d + n * e / 2^32) (0 < e <= 1), and the added
+// term stays below 1 / d, the distance from n / d up to the next integer.
+__host__ __device__ inline unsigned udiv_magic(unsigned d) { return d <= 1 ? 0u : (unsigned)(0x100000000ull / d + 1); }
+__device__ __forceinline__ int udiv(int n, unsigned m, int d) { return d <= 1 ? n : (int)__umulhi((unsigned)n, m); }
+
+// Units (kUnitOf K blocks) per tile row of a matrix.
+__device__ __forceinline__ int units_per_item(const TMat &m) {
+    const int KBe = m.type == PK_TYPE_F32 ? 2 * m.KB : m.KB, U = unit_blocks(m.type);
+    return (KBe + U - 1) / U;
+}
 
 // LSTM state of layers >= 1 kept in LDS by the workgroup that owns the units:
 // for layer l, utterance ul (domain index) and owned tile k (tile rank + kP,
@@ -1102,7 +1125,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         // lanes of one utterance then combine, and one LDS atomic per utterance
         // and head follows
         unsigned long long best0 = 0ull, best1 = 0ull;
-        run_phase<WC>(p.w_out, n_out, p.w_out, n_out, s.rank, s.P, x, S.red, S.wcache, p.red_slots,
+        run_phase<WC>(p.w_out, n_out, p.w_out, n_out, s.rank, s.P, x, S.red, S.wcache, s.pass[p.L],
                   [&](int k, f32x4 acc) {
                       acc = quad_transpose(acc);   // every lane of the wave takes part
                       if (u >= nc) return;
@@ -1157,7 +1180,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         const int u = threadIdx.x / 2, head = threadIdx.x % 2;
         const unsigned long long k = s.wgkey[u][head];
         if (k != 0ull)
-            __hip_atomic_fetch_max(&keys[((size_t)(s.dom * kColCap + u) * p.shards + s.rank % p.shards) * 2 + head],
+            __hip_atomic_fetch_max(&keys[((size_t)(s.dom * kColCap + u) * p.shards + (s.rank & (p.shards - 1))) * 2 + head],
                                    ((unsigned long long)stamp << kStampShift) | k, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -1173,18 +1196,22 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
 constexpr int kL0 = 3;
 __device__ __forceinline__ void lstm_layer0(const KParams &p, Ctl &s, const Lds &S, const Bufs &B, bool redundant) {
     const int H = p.H;
-    const int groups = p.w_hh[0].tiles;                 // unit groups of 4
     const int n_own = s.own_lstm;
     const int nunits = redundant ? H : 4 * n_own;
+    const unsigned mag = redundant ? s.mag_h : s.mag_units;
     const int n_work = s.nl * nunits;
     for (int base = 0; base < n_work; base += kL0 * kBlock) {
         float4 e[kL0], r[kL0];
         float c_prev[kL0];
+        int uq[kL0], jq[kL0];
 #pragma unroll
         for (int q = 0; q < kL0; ++q) {   // no branches: unused loads take kBad and return 0
             const int i = base + threadIdx.x + q * kBlock;
-            const int u = min(i, n_work - 1) / nunits, jj = min(i, n_work - 1) - u * nunits;
+            const int ic = min(i, n_work - 1);
+            const int u = udiv(ic, mag, nunits), jj = ic - u * nunits;   // ic * nunits < 2^32 (H <= 4096)
             const int j = redundant ? jj : 4 * (s.rank + (jj / 4) * s.P) + (jj & 3);
+            uq[q] = u;
+            jq[q] = j;
             const bool ok = i < n_work && j < H;
             const int ul = s.lst[u], b = s.b[ul], cur = s.cur[ul];
             const bool st = ok && !(s.flags[ul] & kFlagZeroHC);
@@ -1195,10 +1222,8 @@ __device__ __forceinline__ void lstm_layer0(const KParams &p, Ctl &s, const Lds 
 #pragma unroll
         for (int q = 0; q < kL0; ++q) {
             const int i = base + threadIdx.x + q * kBlock;
-            if (i >= n_work) continue;
-            const int u = i / nunits, jj = i - u * nunits;
-            const int j = redundant ? jj : 4 * (s.rank + (jj / 4) * s.P) + (jj & 3);
-            if (j >= H) continue;
+            const int u = uq[q], j = jq[q];
+            if (i >= n_work || j >= H) continue;
             const int ul = s.lst[u], b = s.b[ul], cur = s.cur[ul];
             float c_new, h_new;
             cell(e[q].x + r[q].x, e[q].y + r[q].y, e[q].z + r[q].z, e[q].w + r[q].w, c_prev[q], c_new, h_new);
@@ -1206,7 +1231,8 @@ __device__ __forceinline__ void lstm_layer0(const KParams &p, Ctl &s, const Lds 
                 const Act &x = S.act[1];
                 split_f16(h_new, x.hi[u * x.kp + j], x.lo[u * x.kp + j]);
             }
-            if (((j >> 2) % s.P) == s.rank) {
+            // owner of unit group j / 4 (always, when only this workgroup's units are listed)
+            if (!redundant || (j >> 2) - udiv(j >> 2, s.mag_p, s.P) * s.P == s.rank) {
                 st_coh(p.cx + hx_off(p, cur ^ 1, 0, b) + j, c_new);
                 st_coh(p.hx + hx_off(p, cur ^ 1, 0, b) + j, h_new);
             }
@@ -1246,7 +1272,7 @@ __device__ __forceinline__ void consume_layer(const KParams &p, Ctl &s, const Ld
     // the pred rows, or the four gates of unit j = row0 / 4
     const float *btab = S.bias + kTile * lc * s.own_lstm;
     TL(1);
-    run_phase<WC>(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache, p.red_slots,
+    run_phase<WC>(wc, n_c, wr, n_c + n_r, s.rank, s.P, x, S.red, S.wcache, s.pass[lc],
               [&](int it, f32x4 acc) {
                   acc = quad_transpose(acc);   // every lane of the wave takes part
                   if (u >= nc) return;
@@ -1341,7 +1367,7 @@ __device__ __forceinline__ bool lstm_and_pred(const KParams &p, Ctl &s, const Bu
 // iteration hold older stamps and are skipped).  Lane groups of p.shards
 // reduce one (column, head) with shuffles; results go to s.wgkey.
 __device__ __forceinline__ void gather_shards(const KParams &p, Ctl &s, unsigned stamp) {
-    const int G = p.shards;
+    const int G = p.shards, lg = __builtin_ctz((unsigned)G);   // a power of two
     const unsigned long long *keys = p.keys + (size_t)(stamp & 1) * p.n_dom * kColCap * G * 2;
     const int lane = threadIdx.x & (kWave - 1);
     const int n = s.ncol * 2 * G;
@@ -1349,7 +1375,7 @@ __device__ __forceinline__ void gather_shards(const KParams &p, Ctl &s, unsigned
         const int e = e0 + threadIdx.x;
         unsigned long long k = 0ull;
         if (e < n) {
-            const int pair = e / G, sh = e - pair * G;
+            const int pair = e >> lg, sh = e & (G - 1);
             const size_t col = (size_t)s.dom * kColCap + (pair >> 1);
             k = __hip_atomic_load(&keys[(col * G + sh) * 2 + (pair & 1)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (key_stamp(k) != stamp) k = 0ull;
@@ -1359,7 +1385,7 @@ __device__ __forceinline__ void gather_shards(const KParams &p, Ctl &s, unsigned
             k = o > k ? o : k;
         }
         if (e < n && (lane & (G - 1)) == 0) {
-            const int pair = e / G;
+            const int pair = e >> lg;
             s.wgkey[pair >> 1][pair & 1] = k;
         }
     }
@@ -1383,7 +1409,7 @@ __device__ __forceinline__ bool gather_slots(const KParams &p, Ctl &s, unsigned 
         unsigned long long k = 0ull;
         int pair = -1;
         if (e < n) {
-            pair = e / P;
+            pair = udiv(e, s.mag_p, P);
             const int r = e - pair * P;
             const unsigned long long *w = sl + ((size_t)r * kSlotCols + (pair >> 1)) * 2 + (pair & 1);
             const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
@@ -1423,7 +1449,7 @@ template <bool CHAIN>
 __device__ __forceinline__ void decide_steps(const KParams &p, Ctl &s, unsigned stamp) {
     for (int i = threadIdx.x; i < s.nj; i += kBlock) {
         const int ul = s.jst[i], b = s.b[ul];
-        const bool writer = (ul % s.P) == s.rank;
+        const bool writer = ((s.wmask >> ul) & 1u) != 0u;
         const int t0 = s.t[ul];
         int col = i;
         while (true) {
@@ -1575,6 +1601,15 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
         s.own_lstm = owned(p.w_hh[0].tiles, s.rank, s.P);
         s.own_pred = owned(p.w_pred.tiles, s.rank, s.P);
         s.own_out = owned(p.w_out.tiles, s.rank, s.P);
+        for (int lc = 0; lc < p.L; ++lc)
+            s.pass[lc] = p.red_slots / units_per_item(lc == p.L - 1 ? p.w_pred : p.w_ih[lc + 1]);
+        s.pass[p.L] = p.red_slots / units_per_item(p.w_out);
+        s.mag_p = udiv_magic(s.P);
+        s.mag_h = udiv_magic(p.H);
+        s.mag_units = udiv_magic(4 * s.own_lstm);
+        unsigned wm = 0;
+        for (int ul = 0; ul < kDomCap; ++ul) wm |= (ul % s.P == s.rank ? 1u : 0u) << ul;
+        s.wmask = wm;
     }
     if (threadIdx.x < PK_MAX_DURATIONS) s.dur[threadIdx.x] = threadIdx.x < p.n_dur ? p.durations[threadIdx.x] : 0;
     __syncthreads();
