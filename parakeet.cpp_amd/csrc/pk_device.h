@@ -1060,9 +1060,25 @@ __device__ __forceinline__ bool slot_mode(const Ctl &s) {
 
 // Joint + argmax for this workgroup's output tiles.  Utterances are processed
 // 16 at a time (one MFMA column tile).
+// The encp rows of the joint's first staging round (column tile 0, chunks
+// sub, sub + 32, ...), loaded at the start of the iteration: the list rebuild
+// has fixed every column's frame, and the loads complete during layer 0, whose
+// own loads take as long, instead of at the joint's staging.
+__device__ __forceinline__ void encp_prefetch(const KParams &p, const Ctl &s, const Bufs &B, float4 (&e)[kStageMax]) {
+    const int J = p.J, per = J / 4, sub = threadIdx.x % kStageTpr, u = threadIdx.x / kStageTpr;
+    const int nc = min(kTile, s.ncol);
+    const bool live = u < nc;
+    const unsigned erow = (unsigned)((size_t)s.crow[live ? u : 0] * J * 4);
+#pragma unroll
+    for (int j = 0; j < kStageMax; ++j) {
+        const int k4 = sub + kStageTpr * j;
+        e[j] = ld4(B.encp, live && k4 < per ? erow + (unsigned)k4 * 16 : kBad);
+    }
+}
+
 template <int WC, bool ONE>
 __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs &B, const Lds &S, unsigned stamp,
-                            unsigned long long &tlast) {
+                            const float4 (&epre)[kStageMax], unsigned long long &tlast) {
     const int J = p.J, lane = threadIdx.x & (kWave - 1);
     if (threadIdx.x < 2 * kColCap) s.wgkey[threadIdx.x / 2][threadIdx.x % 2] = 0ull;
     const int n_out = s.own_out;
@@ -1085,7 +1101,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
                     for (int j = 0; j < kStageMax; ++j) {
                         const int k4 = k0 + sub + kStageTpr * j;
                         const bool ok = live && k4 < per;
-                        e[j] = ld4(B.encp, ok ? erow + (unsigned)k4 * 16 : kBad);
+                        e[j] = (c0 == 0 && k0 == 0) ? epre[j] : ld4(B.encp, ok ? erow + (unsigned)k4 * 16 : kBad);
                         q[j] = ld4_coh(B.ppx, ok ? prow + (unsigned)k4 * 16 : kBad);
                     }
 #pragma unroll
@@ -1704,12 +1720,14 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
             lds_sync();
         }
 #endif
+        float4 epre[kStageMax];
+        if (s.nj > 0) encp_prefetch(p, s, B, epre);
         if (s.nl > 0) {
             ok = lstm_and_pred<WC>(p, s, B, S, epoch, tlast);
             if (!ok) break;
         }
         if (s.nj > 0) {
-            joint_phase<WC, ONE>(p, s, B, S, iter, tlast);
+            joint_phase<WC, ONE>(p, s, B, S, iter, epre, tlast);
             const bool slots = slot_mode<ONE>(s);
             ok = slots ? gather_slots(p, s, iter) : dom_sync(p, s, epoch);
             TLA(29);
