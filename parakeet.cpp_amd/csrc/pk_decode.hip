@@ -358,9 +358,10 @@ struct pk_decoder {
     // per-call scratch
     DevBuf d_desc, d_encp, d_clear, d_enc, d_out, d_xchg, d_prof;   // d_clear: status, barrier flags, argmax keys
     std::vector<uint8_t> h_desc;
-    HostBuf h_pin;             // pinned: 16 B of status read back, then the descriptor block
-                               // (sized at creation for n_slots utterances, so the uploads and the
-                               // status read are asynchronous copies and no call allocates it)
+    HostBuf h_pin;             // pinned: 16 B of status read back, the descriptor block, then the
+                               // per-utterance counters read back (sized at creation for n_slots
+                               // utterances, so these copies are asynchronous and no call allocates)
+    size_t pin_cnt = 0;        // offset of the counters in h_pin (the descriptor block ends there)
     HostBuf h_out;             // staging of host-memory outputs
     unsigned char *scratch = nullptr;   // this device's fixed scratch array (pk_decode_noalloc)
     int last_iters = 0;
@@ -710,7 +711,8 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     {   // the largest descriptor block of a call (n_slots utterances; at most nwg domains of kDomCap)
         const size_t nwg = (size_t)dec->nwg;
         const size_t most = (size_t)n_slots * (2 * 8 + 5 * 4) + 4 * (nwg + nwg * kDomCap + 3 * nwg);
-        if ((rc = dec->h_pin.ensure(16 + most))) return cleanup(rc);
+        dec->pin_cnt = (16 + most + 15) & ~(size_t)15;
+        if ((rc = dec->h_pin.ensure(dec->pin_cnt + 12 * (size_t)n_slots))) return cleanup(rc);
     }
     if (hipStreamCreateWithFlags(&dec->stream, hipStreamNonBlocking) != hipSuccess)
         return cleanup(fail(PK_ERR_DEVICE, "stream"));
@@ -1015,7 +1017,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     void *d_desc = nullptr;
     if ((rc = cs.get(dec->d_desc, desc_bytes, &d_desc))) return rc;
     uint8_t *hd;
-    if (16 + desc_bytes <= dec->h_pin.n) {
+    if (16 + desc_bytes <= dec->pin_cnt) {
         hd = dec->h_pin.as<uint8_t>() + 16;
     } else {
         dec->h_desc.resize(desc_bytes);
@@ -1227,10 +1229,17 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
         // the counters of every utterance in one copy (n_tokens, steps,
         // n_segments are consecutive), then the filled prefix of each output
         // row in one strided copy per array, staged in pinned memory
-        std::vector<int> cnt(3 * (size_t)m);
-        HIP_TRY(hipMemcpyAsync(cnt.data(), o_ntok, 12 * (size_t)m, hipMemcpyDeviceToHost, dec->stream));
+        std::vector<int> cnt_v;
+        int *cnt;
+        if (dec->pin_cnt + 12 * (size_t)m <= dec->h_pin.n) {   // (m <= n_slots: slots are distinct)
+            cnt = reinterpret_cast<int *>(dec->h_pin.as<uint8_t>() + dec->pin_cnt);
+        } else {
+            cnt_v.resize(3 * (size_t)m);
+            cnt = cnt_v.data();
+        }
+        HIP_TRY(hipMemcpyAsync(cnt, o_ntok, 12 * (size_t)m, hipMemcpyDeviceToHost, dec->stream));
         HIP_TRY(hipStreamSynchronize(dec->stream));
-        const int *c_tok = cnt.data(), *c_steps = c_tok + m, *c_seg = c_steps + m;
+        const int *c_tok = cnt, *c_steps = c_tok + m, *c_seg = c_steps + m;
         int wt = 0, ws = 0, wr = 0;
         for (int i = 0; i < m; ++i) {
             wt = std::max(wt, std::min(c_tok[i], tcap));
