@@ -814,6 +814,7 @@ __device__ __forceinline__ f32x4 unit_mma(const uint4 (&f)[kUnitOf<Q8>], const h
 // against an even split over the 8 waves (two A/Bs chained): B=256, ragged
 // B=512 and TDT-1.1b f16 about -3 %, B=64 -0.5 %, B=1 +1.5 %; a 28 % skew
 // gained no more.
+static_assert(kWaves == 8, "wave_range pairs waves w and w + 4 on SIMD w & 3");
 __device__ __forceinline__ void wave_range(int N, int w, int &c0, int &c1) {
     const int j = w & 3, a = (N * j) >> 2, b = (N * (j + 1)) >> 2, len = b - a;
     const int d = N >= 48 ? 12 : 0;
