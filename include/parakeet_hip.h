@@ -167,8 +167,27 @@ PK_API int pk_slot_read(pk_decoder *dec, int32_t slot, float *h, float *c, float
  * TdtDecodeState / EouDecodeState value (src/parakeet_tdt.h:175-183) that then
  * decodes independently of the original. */
 PK_API int pk_slot_copy(pk_decoder *dec, int32_t src, int32_t dst);
-/* Decode one window for every utterance of the batch. */
+/* Decode one window for every utterance of the batch.  Windows of any length: a
+ * window one launch of the decode loop cannot take (see pk_window_split) is decoded
+ * in several launches, its state carried from piece to piece, with the same results
+ * as one launch (the reference's loop, src/parakeet_tdt.cpp:917-967, has no length
+ * limit).  The logit tap takes windows of one launch only. */
 PK_API int pk_decode(pk_decoder *dec, const pk_batch *batch);
+/* How pk_decode splits windows.  One launch takes at most 2^18 - 1 lockstep
+ * iterations (the 18-bit stamp of its argmax keys; a window of T frames may take
+ * T * (max_symbols + 1) + 4) and at most (2^31 - 1) / (4 * joint_hidden) frames in
+ * all (32-bit offsets of its enc_proj rows).  When a batch exceeds either, utterance
+ * u is decoded as launches[u] consecutive pieces of nearly equal length (the first
+ * n_frames[u] % launches[u] pieces one frame longer than n_frames[u] / launches[u]),
+ * at most *piece_frames frames each, and launch j takes piece j of every utterance
+ * that has one.  Every piece is longer than the largest carry a TDT duration can
+ * leave (max_duration - 1, where max_duration is the largest value of the duration
+ * table), which makes the split decode equal to one launch over each window.
+ * launches[u] is 1 for every non-empty window when no split is needed (0 for an
+ * empty one).  Returns PK_ERR_UNSUPPORTED when no piece length satisfies the bounds.
+ * Host arithmetic only: needs no device. */
+PK_API int pk_window_split(int32_t n_utts, const int32_t *n_frames, int32_t max_symbols, int32_t joint_hidden,
+                           int32_t max_duration, int32_t *piece_frames, int32_t *launches);
 /* pk_decode without any device allocation.  No counterpart in the reference:
  * it is for callers that cannot allocate (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  batch->mem must be

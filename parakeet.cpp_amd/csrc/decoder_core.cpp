@@ -2,6 +2,7 @@
 #include "decoder_core.h"
 
 #include <algorithm>
+#include <climits>
 #include <cstdio>
 #include <cstring>
 #include <stdexcept>
@@ -128,6 +129,9 @@ int device_frames(const float *data, int64_t n_rows, int d_model, const std::vec
 
 namespace {
 
+// Host output staging of one batched call: at most 2^28 token slots (1 GiB).
+constexpr long long kMaxOutputInts = 1ll << 28;
+
 // One launch over utterances [i, j) of the batch.
 int decode_launch(SlotPool &pool, int D_enc, int max_symbols, const Frames &fr, const std::vector<int> &n_frames,
                   const std::vector<SlotHandle *> &slots, const std::vector<int> &tokens_base, bool tdt, size_t i,
@@ -154,8 +158,17 @@ int decode_launch(SlotPool &pool, int D_enc, int max_symbols, const Frames &fr, 
             if (T[u] > 0)
                 memcpy(packed.data() + (size_t)row[u] * D_enc, fr.host[i + u], sizeof(float) * (size_t)T[u] * D_enc);
     }
-    const int cap = max_T * std::max(1, max_symbols) + 1;
-    std::vector<int32_t> tok((size_t)n * cap), ntok(n), st(n), seg((size_t)n * (cap + 1)), nseg(n);
+    // every emission of a window fits (at most max_symbols per frame); an EOU boundary ends
+    // its frame, so a window records at most max_T + 1 of them.  Sized in 64 bits and
+    // bounded before anything is allocated.
+    const long long cap64 = (long long)max_T * std::max(1, max_symbols) + 1;
+    if (cap64 > INT32_MAX || (long long)n * cap64 > kMaxOutputInts) {
+        std::fprintf(stderr, "decode: %d windows of up to %d frames at max_symbols %d need %lld output tokens "
+                     "(at most %lld)\n", n, max_T, max_symbols, (long long)n * cap64, (long long)kMaxOutputInts);
+        return PK_ERR_UNSUPPORTED;
+    }
+    const int cap = (int)cap64, scap = tdt ? 0 : max_T + 1;
+    std::vector<int32_t> tok((size_t)n * cap), ntok(n), st(n), seg((size_t)n * std::max(scap, 1)), nseg(n);
     std::vector<int32_t> ctrl((size_t)n * PK_CTRL_N);
     pk_batch b{};
     b.n_utts = n;
@@ -171,8 +184,8 @@ int decode_launch(SlotPool &pool, int D_enc, int max_symbols, const Frames &fr, 
     b.token_cap = cap;
     b.n_tokens = ntok.data();
     b.steps = st.data();
-    b.segments = seg.data();
-    b.seg_cap = cap + 1;
+    b.segments = scap ? seg.data() : nullptr;
+    b.seg_cap = scap;
     b.n_segments = nseg.data();
     b.reset = reset.data();
     b.ctrl_out = ctrl.data();
@@ -183,7 +196,7 @@ int decode_launch(SlotPool &pool, int D_enc, int max_symbols, const Frames &fr, 
     for (int u = 0; u < n; ++u) {
         const size_t k = i + u;
         out.tokens[k].assign(tok.begin() + (size_t)u * cap, tok.begin() + (size_t)u * cap + ntok[u]);
-        out.segments[k].assign(seg.begin() + (size_t)u * (cap + 1), seg.begin() + (size_t)u * (cap + 1) + nseg[u]);
+        if (scap) out.segments[k].assign(seg.begin() + (size_t)u * scap, seg.begin() + (size_t)u * scap + nseg[u]);
         out.steps[k] = st[u];
         std::copy(ctrl.begin() + (size_t)u * PK_CTRL_N, ctrl.begin() + (size_t)(u + 1) * PK_CTRL_N,
                   out.ctrl[k].begin());

@@ -5,6 +5,8 @@
 #pragma once
 
 #include <array>
+#include <cstdio>
+#include <exception>
 #include <cstdint>
 #include <memory>
 #include <mutex>
@@ -72,6 +74,20 @@ std::string detokenize(const std::vector<std::string> &pieces, int32_t blank_id,
 // non-empty ones joined with '\n'.
 std::string eou_text(const std::vector<std::string> &pieces, int32_t blank_id, int32_t bos_id, int32_t eos_id,
                      int32_t pad_id, const std::vector<int32_t> &ids, const std::vector<int32_t> &boundaries);
+
+// Runs f() and returns its status; an exception (a state slot that cannot be
+// leased, or a failed device copy of a state) becomes PK_ERR_NOMEM with the
+// message on stderr, so the decoder entry points return status codes and never
+// throw, as the reference's do.
+template <class F>
+int no_throw(const char *who, F &&f) {
+    try {
+        return f();
+    } catch (const std::exception &e) {
+        std::fprintf(stderr, "%s: %s\n", who, e.what());
+        return PK_ERR_NOMEM;
+    }
+}
 
 // 1 where the vocabulary piece is "<...>" (the EOU loop's special pieces).
 std::vector<uint8_t> special_pieces(const std::vector<std::string> &pieces);

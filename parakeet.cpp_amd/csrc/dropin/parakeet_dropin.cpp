@@ -91,7 +91,10 @@ int tdt_prepare_runtime(const ParakeetCtcModel &model, TdtRuntimeWeights &W) {
     return 0;
 }
 
-void tdt_init_state(TdtRuntimeWeights &W, int, TdtDecodeState &state) { core::tdt_fresh(W.pool, state); }
+void tdt_init_state(TdtRuntimeWeights &W, int, TdtDecodeState &state) {
+    // a state that gets no slot stays uninitialised; its next window tries again and returns a status
+    if (core::no_throw("tdt_init_state", [&] { core::tdt_fresh(W.pool, state); return 0; })) state.initialized = false;
+}
 
 int tdt_decode_batch(const ParakeetCtcModel &, TdtRuntimeWeights &W, const std::vector<const float *> &enc,
                      const std::vector<int> &n_frames, int D_enc, const TdtDecodeOptions &opts,
@@ -107,7 +110,9 @@ int tdt_decode_batch(const ParakeetCtcModel &, TdtRuntimeWeights &W, const std::
     if ((int)n_frames.size() != n || (int)states.size() != n || !W.pool) return 3;
     core::Frames fr;
     fr.host = enc;
-    return core::tdt_run(W.pool, D_enc, opts.max_symbols_per_step, fr, n_frames, states, out_tokens, out_steps);
+    return core::no_throw("tdt_decode_window", [&] {
+        return core::tdt_run(W.pool, D_enc, opts.max_symbols_per_step, fr, n_frames, states, out_tokens, out_steps);
+    });
 }
 
 int tdt_decode_window(const ParakeetCtcModel &model, TdtRuntimeWeights &W, const float *encoder_out_window,
@@ -153,7 +158,9 @@ int eou_prepare_runtime(const ParakeetCtcModel &model, EouRuntimeWeights &W) {
     return make_pool(model, model.eou, true, W.pool);
 }
 
-void eou_init_state(const EouRuntimeWeights &W, EouDecodeState &state) { core::eou_fresh(W.pool, state); }
+void eou_init_state(const EouRuntimeWeights &W, EouDecodeState &state) {
+    if (core::no_throw("eou_init_state", [&] { core::eou_fresh(W.pool, state); return 0; })) state.initialized = false;
+}
 
 namespace {
 
@@ -164,8 +171,10 @@ int eou_batch(const EouRuntimeWeights &W, const std::vector<const float *> &enc,
     core::Frames fr;
     fr.host = enc;
     std::vector<std::vector<int32_t>> bounds(n_frames.size());
-    if (int rc = core::eou_run(W.pool, D_enc, opts.max_symbols_per_step, fr, n_frames, states, tokens_base, out_tokens,
-                               bounds, out_steps))
+    if (int rc = core::no_throw("eou_decode_window", [&] {
+            return core::eou_run(W.pool, D_enc, opts.max_symbols_per_step, fr, n_frames, states, tokens_base,
+                                 out_tokens, bounds, out_steps);
+        }))
         return rc;
     for (size_t u = 0; u < n_frames.size(); ++u)
         for (int32_t b : bounds[u]) out_segments[u].push_back(EouSegmentBoundary{b, true});

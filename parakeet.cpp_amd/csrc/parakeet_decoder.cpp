@@ -197,14 +197,19 @@ int tdt_prepare_runtime(const DecoderModel &model, TdtRuntimeWeights &W, int n_s
 
 // src/parakeet_tdt.cpp:813-863 (see core::tdt_fresh: the device work runs in
 // the state's next decode launch).
-void tdt_init_state(TdtRuntimeWeights &W, int, TdtDecodeState &state) { core::tdt_fresh(W.pool, state); }
+void tdt_init_state(TdtRuntimeWeights &W, int, TdtDecodeState &state) {
+    // a state that gets no slot stays uninitialised; its next window tries again and returns a status
+    if (core::no_throw("tdt_init_state", [&] { core::tdt_fresh(W.pool, state); return 0; })) state.initialized = false;
+}
 
 namespace {
 
 int tdt_batch(TdtRuntimeWeights &W, const Frames &fr, const std::vector<int> &n_frames, int D_enc,
               const TdtDecodeOptions &opts, const std::vector<TdtDecodeState *> &states,
               std::vector<std::vector<int32_t>> &out_tokens, std::vector<int> &out_steps) {
-    return core::tdt_run(W.pool, D_enc, opts.max_symbols_per_step, fr, n_frames, states, out_tokens, out_steps);
+    return core::no_throw("tdt_decode_window", [&] {
+        return core::tdt_run(W.pool, D_enc, opts.max_symbols_per_step, fr, n_frames, states, out_tokens, out_steps);
+    });
 }
 
 }  // namespace
@@ -282,7 +287,9 @@ int eou_prepare_runtime(const DecoderModel &model, EouRuntimeWeights &W, int n_s
 }
 
 // src/parakeet_eou.cpp:206-230 (see core::eou_fresh).
-void eou_init_state(const EouRuntimeWeights &W, EouDecodeState &state) { core::eou_fresh(W.pool, state); }
+void eou_init_state(const EouRuntimeWeights &W, EouDecodeState &state) {
+    if (core::no_throw("eou_init_state", [&] { core::eou_fresh(W.pool, state); return 0; })) state.initialized = false;
+}
 
 namespace {
 
@@ -291,8 +298,10 @@ int eou_batch(const EouRuntimeWeights &W, const Frames &fr, const std::vector<in
               const std::vector<int> &tokens_base, std::vector<std::vector<int32_t>> &out_tokens,
               std::vector<std::vector<EouSegmentBoundary>> &out_segments, std::vector<int> &out_steps) {
     std::vector<std::vector<int32_t>> bounds(n_frames.size());
-    if (int rc = core::eou_run(W.pool, D_enc, opts.max_symbols_per_step, fr, n_frames, states, tokens_base, out_tokens,
-                               bounds, out_steps))
+    if (int rc = core::no_throw("eou_decode_window", [&] {
+            return core::eou_run(W.pool, D_enc, opts.max_symbols_per_step, fr, n_frames, states, tokens_base,
+                                 out_tokens, bounds, out_steps);
+        }))
         return rc;
     for (size_t u = 0; u < n_frames.size(); ++u)
         for (int32_t b : bounds[u]) out_segments[u].push_back(EouSegmentBoundary{b, true});

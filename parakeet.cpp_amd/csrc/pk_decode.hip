@@ -33,6 +33,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cerrno>
 #include <cmath>
 #include <cstdarg>
@@ -49,6 +50,8 @@
 #include <sys/file.h>
 #include <sys/stat.h>
 #include <unistd.h>
+
+extern char **environ;
 
 #include "parakeet_hip.h"
 #include "pk_device.h"
@@ -71,6 +74,8 @@ using pkdev::kWaves;
 constexpr int kMaxBatch = PK_MAX_BATCH;
 
 thread_local std::string g_err;
+// set by an atexit handler: process teardown has begun
+std::atomic<bool> g_exiting{false};
 
 int fail(int rc, const char *fmt, ...) {
     char buf[512];
@@ -368,6 +373,18 @@ struct pk_decoder {
     int lock_fd = -1;          // this GPU's cross-process loop lock (see DeviceLoopLock), -1: none
     const void *loop_fn[2] = {};   // the decode-loop instantiations for this decoder's weight storage:
                                    // several domains, one domain (argmax key slots)
+    // Drop every device and pinned allocation without freeing it (process exit).
+    void forget_device() {
+        for (DevBuf *b : {&arena, &eproj, &slots_h, &slots_c, &slots_pp, &slots_r, &slots_ctrl, &special, &d_desc,
+                          &d_encp, &d_clear, &d_enc, &d_out, &d_xchg, &d_prof}) {
+            b->p = nullptr;
+            b->n = 0;
+        }
+        for (HostBuf *b : {&h_pin, &h_out}) {
+            b->p = nullptr;
+            b->n = 0;
+        }
+    }
 };
 
 namespace {
@@ -482,6 +499,9 @@ struct CallScratch {
 };
 
 int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratch cs = CallScratch{});
+int decode_chained(pk_decoder *dec, const pk_batch *bt, int W, const std::vector<int32_t> &launches);
+// Longest piece of a window split over several launches (bounds the per-launch host staging).
+constexpr int kChainFrames = 8192;
 int open_loop_lock(int device);
 
 }  // namespace
@@ -503,6 +523,10 @@ PK_API int pk_device_info(int32_t *n_cu, int32_t *lds_per_block, int32_t *wave_s
 
 PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decoder **out) {
     g_err.clear();
+    // registered after any static that holds this decoder has been constructed, so at exit
+    // it runs before that static's destructor (which then makes no HIP call)
+    static std::once_flag exit_hook;
+    std::call_once(exit_hook, [] { std::atexit([] { g_exiting.store(true); }); });
     if (!d || !out || n_slots <= 0) return fail(PK_ERR_ARG, "pk_decoder_create: bad arguments");
     *out = nullptr;
     const int H = d->pred_hidden, L = d->pred_rnn_layers, J = d->joint_hidden, D = d->d_enc;
@@ -724,6 +748,15 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
 
 PK_API int pk_decoder_destroy(pk_decoder *dec) {
     if (!dec) return 0;
+    if (g_exiting.load()) {
+        // process exit (a static runtime's destructor, as the reference CLI keeps at
+        // src/main.cpp:746, :761): no HIP call here, the driver reclaims the device memory
+        // with the process.  Every call has completed (pk_decode returns after its stream).
+        dec->forget_device();
+        if (dec->lock_fd >= 0) close(dec->lock_fd);
+        delete dec;
+        return 0;
+    }
     (void)hipSetDevice(dec->device);
     if (dec->stream) (void)hipStreamSynchronize(dec->stream);
     for (auto &e : dec->ev) if (e) (void)hipEventDestroy(e);
@@ -812,8 +845,55 @@ PK_API int pk_last_timing(pk_decoder *dec, float *enc_proj_ms, float *loop_ms, i
     return 0;
 }
 
+PK_API int pk_window_split(int32_t n_utts, const int32_t *n_frames, int32_t max_symbols, int32_t joint_hidden,
+                           int32_t max_duration, int32_t *piece_frames, int32_t *launches) {
+    if (n_utts < 0 || (n_utts > 0 && !n_frames) || joint_hidden <= 0 || !piece_frames)
+        return fail(PK_ERR_ARG, "pk_window_split: bad arguments");
+    const long long S = std::max(max_symbols, 1);
+    // one launch: max_T * (S + 1) + 4 < 2^18 - 1 iterations, rows * J * 4 < 2^31 bytes of enc_proj rows
+    const long long w_stamp = ((long long)kMaxStamp - 1 - 4) / (S + 1);
+    const long long rows_limit = ((1ll << 31) - 1) / (4ll * joint_hidden);
+    long long max_T = 0, rows = 0;
+    for (int u = 0; u < n_utts; ++u) {
+        if (n_frames[u] < 0) return fail(PK_ERR_ARG, "negative n_frames");
+        max_T = std::max<long long>(max_T, n_frames[u]);
+        rows += n_frames[u];
+    }
+    long long W = max_T;
+    if (max_T > w_stamp || rows > rows_limit)
+        W = std::min({w_stamp, rows_limit / std::max(n_utts, 1), (long long)kChainFrames});
+    if (W < 1 && max_T > 0) return fail(PK_ERR_UNSUPPORTED, "no launch takes one frame of %d utterances", n_utts);
+    const long long carry = std::max(max_duration, 1) - 1;   // largest TDT carry_frames a step can leave
+    for (int u = 0; u < n_utts; ++u) {
+        const long long T = n_frames[u], k = T > 0 ? (T + W - 1) / W : 0;
+        if (k > 1 && T / k <= carry)
+            return fail(PK_ERR_UNSUPPORTED, "window of %lld frames: pieces of %lld frames are not longer than the "
+                        "largest duration carry (%lld)", T, T / k, carry);
+        if (launches) launches[u] = (int32_t)k;
+    }
+    *piece_frames = (int32_t)W;
+    return 0;
+}
+
 PK_API int pk_decode(pk_decoder *dec, const pk_batch *bt) {
     g_err.clear();
+    if (!dec || !bt) return fail(PK_ERR_ARG, "pk_decode: null argument");
+    if (bt->n_utts > 0 && bt->n_utts <= kMaxBatch && bt->n_frames) {
+        // a window one launch cannot take is decoded in several launches (state carried)
+        int32_t W = 0;
+        std::vector<int32_t> k(bt->n_utts);
+        int max_dur = 1;
+        if (dec->kp.kind == PK_KIND_TDT)
+            for (int i = 0; i < dec->kp.Dn; ++i)
+                max_dur = std::max(max_dur, dec->kp.n_dur > 0 ? dec->kp.durations[i] : i);
+        bool ok = true;
+        for (int u = 0; u < bt->n_utts; ++u) ok = ok && bt->n_frames[u] >= 0;
+        if (ok) {
+            if (int rc = pk_window_split(bt->n_utts, bt->n_frames, bt->max_symbols, dec->kp.J, max_dur, &W, k.data()))
+                return rc;
+            if (*std::max_element(k.begin(), k.end()) > 1) return decode_chained(dec, bt, W, k);
+        }
+    }
     return decode_impl(dec, bt, false);
 }
 
@@ -837,17 +917,30 @@ namespace {
 // run it on one GPU together: an exclusive flock on a per-GPU file
 // (/tmp/parakeet_hip-<PCI bus id>.lock, opened once per decoder) is held from a
 // call's loop launch to its last stream synchronisation.  Advisory and
-// best-effort: without the file (no /tmp, no permission) calls are not
-// serialised across processes, and overlapping loops end with PK_ERR_TIMEOUT.
+// best-effort: without the file (no /tmp, no permission, something other than
+// a regular file at the path) calls are not serialised across processes, and
+// overlapping loops end with PK_ERR_TIMEOUT.  The wait for the lock is bounded
+// (kLockWaitMs): a process that holds it longer makes the call return
+// PK_ERR_TIMEOUT instead of blocking forever.
+constexpr int kLockWaitMs = 30000;
 struct DeviceLoopLock {
     int fd;
-    explicit DeviceLoopLock(int f) : fd(f) {
-        if (fd >= 0)
-            while (flock(fd, LOCK_EX) != 0 && errno == EINTR) {
+    bool held = false;
+    explicit DeviceLoopLock(int f) : fd(f) {}
+    int acquire() {
+        if (fd < 0) return 0;
+        for (int waited = 0;; ++waited) {
+            if (flock(fd, LOCK_EX | LOCK_NB) == 0) {
+                held = true;
+                return 0;
             }
+            if (errno != EWOULDBLOCK && errno != EINTR) return 0;   // no usable lock: not serialised
+            if (waited >= kLockWaitMs) return fail(PK_ERR_TIMEOUT, "another process held this GPU's decode lock for %d ms", kLockWaitMs);
+            usleep(1000);
+        }
     }
     ~DeviceLoopLock() {
-        if (fd >= 0) (void)flock(fd, LOCK_UN);
+        if (held) (void)flock(fd, LOCK_UN);
     }
     DeviceLoopLock(const DeviceLoopLock &) = delete;
     DeviceLoopLock &operator=(const DeviceLoopLock &) = delete;
@@ -858,9 +951,21 @@ int open_loop_lock(int device) {
     if (hipDeviceGetPCIBusId(bus, sizeof bus, device) != hipSuccess) return -1;
     char path[128];
     snprintf(path, sizeof path, "/tmp/parakeet_hip-%s.lock", bus);
-    int fd = open(path, O_RDWR | O_CREAT | O_CLOEXEC, 0666);
-    if (fd < 0) fd = open(path, O_RDONLY | O_CLOEXEC);   // created by another user: a shared lock file
-    if (fd >= 0) (void)fchmod(fd, 0666);
+    // never follow a link planted at the path; make the file shared only when this process created it
+    bool created = true;
+    int fd = open(path, O_RDWR | O_CREAT | O_EXCL | O_NOFOLLOW | O_CLOEXEC, 0666);
+    if (fd < 0 && errno == EEXIST) {
+        created = false;
+        fd = open(path, O_RDWR | O_NOFOLLOW | O_CLOEXEC);
+        if (fd < 0) fd = open(path, O_RDONLY | O_NOFOLLOW | O_CLOEXEC);   // created by another user
+    }
+    if (fd < 0) return -1;
+    struct stat st;
+    if (fstat(fd, &st) != 0 || !S_ISREG(st.st_mode)) {
+        close(fd);
+        return -1;
+    }
+    if (created) (void)fchmod(fd, 0666);   // (the umask may have narrowed the mode)
     return fd;
 }
 
@@ -893,9 +998,17 @@ int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds) {
     // profiler runs: rocprofv3 (ROCm 7.2) ends with SIGSEGV in the HIP
     // runtime's exit-time teardown of any process that made a cooperative
     // launch, a one-kernel program included; the kernel is the same either way.
+    // Without PK_LOOP_DISPATCH the ordinary dispatch is also chosen when the process runs
+    // under rocprofv3 (its ROCPROF* environment, or its tool library preloaded), so the
+    // default path profiles and exits cleanly; PK_LOOP_DISPATCH=0 keeps the cooperative launch.
     static const bool force_dispatch = [] {
         const char *v = std::getenv("PK_LOOP_DISPATCH");
-        return v && v[0] == '1';
+        if (v && v[0]) return v[0] == '1';
+        const char *pre = std::getenv("LD_PRELOAD");
+        if (pre && strstr(pre, "rocprof")) return true;
+        for (char **e = environ; e && *e; ++e)
+            if (strncmp(*e, "ROCPROF", 7) == 0) return true;
+        return false;
     }();
     if (!refused && !force_dispatch) {
         const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(nwg), dim3(kBlock), args, lds, dec->stream);
@@ -971,11 +1084,13 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
         base[i] = bt->tokens_base ? bt->tokens_base[u] : 0;
         reset[i] = bt->reset ? (bt->reset[u] ? 1 : 0) : 0;
     }
-    const int max_iter = max_T * (std::max(bt->max_symbols, 1) + 1) + 4;
-    // the loop addresses encp with 32-bit buffer offsets below 2^31
+    const long long max_iter = (long long)max_T * ((long long)std::max(bt->max_symbols, 1) + 1) + 4;
+    // the loop addresses encp with 32-bit buffer offsets below 2^31 (pk_decode splits longer
+    // windows into several launches before it gets here; see pk_window_split)
     if (rows * (long long)p.J * 4 >= (1ll << 31))
-        return fail(PK_ERR_UNSUPPORTED, "%lld frames in one call; at most %lld", rows, ((1ll << 31) - 1) / (p.J * 4ll));
-    if ((unsigned)max_iter >= kMaxStamp) return fail(PK_ERR_UNSUPPORTED, "window too long for the iteration stamp");
+        return fail(PK_ERR_UNSUPPORTED, "%lld frames in one launch; at most %lld", rows, ((1ll << 31) - 1) / (p.J * 4ll));
+    if (max_iter >= (long long)kMaxStamp)
+        return fail(PK_ERR_UNSUPPORTED, "window too long for the iteration stamp of one launch");
     const int D = dec->desc.d_enc, J = p.J, L = p.L, H = p.H;
     int rc;
     // encoder frames: device pointer as given, or packed host rows uploaded
@@ -1097,7 +1212,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     p.reset = bt->reset ? d_reset : nullptr;
     p.ctrl_out = o_ctrl;
     p.max_sym = bt->max_symbols;
-    p.max_iter = max_iter;
+    p.max_iter = (int)max_iter;
     p.n_dom = pl.n_dom;
     p.dom_size = pl.P;
     // blank runs over the joint tile's spare columns (not while the logit tap records
@@ -1220,7 +1335,8 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     }
     // held until this call's last stream synchronisation (scope end): another
     // process's decode loop on this GPU waits here instead of sharing the CUs
-    const DeviceLoopLock cross_process(dec->lock_fd);
+    DeviceLoopLock cross_process(dec->lock_fd);
+    if ((rc = cross_process.acquire())) return rc;
     if ((rc = launch_loop(dec, nwg, p, lds))) return rc;
     HIP_TRY(hipEventRecord(dec->ev[2], dec->stream));
     int *status = dec->h_pin.as<int>();   // read after the stream synchronisation below
@@ -1318,6 +1434,137 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     }
     if (status[0]) return fail(status[0], "device decode failed (status %d)", status[0]);
     if (status[2]) return fail(PK_ERR_OVERFLOW, "token or segment capacity exceeded");
+    return 0;
+}
+
+}  // namespace
+
+namespace {
+
+// A batch whose windows one launch cannot take (pk_window_split): utterance u
+// decodes its window as launches[u] consecutive pieces of nearly equal length,
+// one launch per piece index, its slot carrying the state from piece to piece
+// exactly as between two calls (TDT symbols and carry_frames, EOU last token and
+// segment start).  Every piece is longer than the largest duration carry, so
+// the result equals one launch over the whole window.  Each launch's outputs
+// come back to host memory and are appended to the caller's arrays (uploaded at
+// the end for device outputs); EOU pieces count segment boundaries from the
+// tokens of the earlier pieces (tokens_base).
+int decode_chained(pk_decoder *dec, const pk_batch *bt, int W, const std::vector<int32_t> &launches) {
+    const int n = bt->n_utts;
+    if (bt->logits && bt->logit_steps > 0)
+        return fail(PK_ERR_UNSUPPORTED, "the logit tap takes windows of at most %d frames (one launch)", W);
+    if (!bt->enc_row || !bt->slot || !bt->n_tokens || !bt->steps || !bt->tokens)
+        return fail(PK_ERR_ARG, "pk_decode: missing batch array");
+    const bool dev_out = bt->mem == PK_MEM_DEVICE;
+    const int S = std::max(bt->max_symbols, 1);
+    const int tcap = std::max(bt->token_cap, 0), scap = bt->segments ? std::max(bt->seg_cap, 0) : 0;
+    const int rcap = bt->trace ? std::max(bt->trace_cap, 0) : 0;
+    // caller's outputs, assembled on the host
+    std::vector<int32_t> h_tok, h_seg, h_tr, h_ctrl;
+    int32_t *o_tok = bt->tokens, *o_seg = bt->segments, *o_tr = bt->trace, *o_ctrl = bt->ctrl_out;
+    if (dev_out) {
+        h_tok.assign((size_t)n * tcap, 0);
+        o_tok = h_tok.data();
+        if (scap) { h_seg.assign((size_t)n * scap, 0); o_seg = h_seg.data(); }
+        if (rcap) { h_tr.assign((size_t)n * rcap * 2, 0); o_tr = h_tr.data(); }
+        if (bt->ctrl_out) { h_ctrl.assign((size_t)n * PK_CTRL_N, 0); o_ctrl = h_ctrl.data(); }
+    }
+    std::vector<long long> done(n, 0);                 // frames decoded so far
+    std::vector<int32_t> ntok(n, 0), nseg(n, 0), nst(n, 0);
+    const int n_launch = *std::max_element(launches.begin(), launches.end());
+    for (int j = 0; j < n_launch; ++j) {
+        // the utterances with a piece j (launch 0: all, so windows with no frames are handled as usual)
+        std::vector<int> idx;
+        for (int u = 0; u < n; ++u)
+            if (j == 0 || launches[u] > j) idx.push_back(u);
+        const int m = (int)idx.size();
+        std::vector<int64_t> row(m);
+        std::vector<int32_t> T(m), sl(m), base(m);
+        std::vector<float> bias(m);
+        std::vector<uint8_t> rst(m, 0);
+        int cap = 1, sc = scap ? 1 : 0, rc_cap = rcap ? 1 : 0;
+        for (int i = 0; i < m; ++i) {
+            const int u = idx[i];
+            const long long Tu = bt->n_frames[u], k = launches[u];
+            const long long piece = k > 0 ? Tu / k + (j < Tu % k ? 1 : 0) : 0;
+            row[i] = bt->enc_row[u] + done[u];
+            T[i] = (int32_t)piece;
+            sl[i] = bt->slot[u];
+            base[i] = (bt->tokens_base ? bt->tokens_base[u] : 0) + ntok[u];
+            bias[i] = bt->blank_bias ? bt->blank_bias[u] : 0.0f;
+            if (j == 0 && bt->reset) rst[i] = bt->reset[u];
+            // staging just large enough for what this piece can add below the caller's capacity
+            cap = std::max<long long>(cap, std::min<long long>(std::max(tcap - ntok[u], 0), piece * S + 1));
+            if (scap) sc = std::max<long long>(sc, std::min<long long>(std::max(scap - nseg[u], 0), piece + 1));
+            if (rcap) rc_cap = std::max<long long>(rc_cap, std::min<long long>(std::max(rcap - nst[u], 0),
+                                                                               piece * (S + 1) + 1));
+        }
+        std::vector<int32_t> tok((size_t)m * cap), cnt(m), st(m), seg((size_t)m * std::max(sc, 1)), cs(m),
+            tr((size_t)m * std::max(rc_cap, 1) * 2), ctrl((size_t)m * PK_CTRL_N);
+        pk_batch b{};
+        b.n_utts = m;
+        b.mem = dev_out ? PK_MEM_DEVICE_FRAMES : bt->mem;
+        b.d_enc = bt->d_enc;
+        b.max_symbols = bt->max_symbols;
+        b.enc = bt->enc;
+        b.enc_row = row.data();
+        b.n_frames = T.data();
+        b.slot = sl.data();
+        b.blank_bias = bt->blank_bias ? bias.data() : nullptr;
+        b.tokens_base = base.data();
+        b.tokens = tok.data();
+        b.token_cap = cap;
+        b.n_tokens = cnt.data();
+        b.steps = st.data();
+        b.segments = scap ? seg.data() : nullptr;
+        b.seg_cap = sc;
+        b.n_segments = cs.data();
+        b.trace = rcap ? tr.data() : nullptr;
+        b.trace_cap = rc_cap;
+        b.reset = bt->reset ? rst.data() : nullptr;
+        b.ctrl_out = ctrl.data();
+        const int rc = decode_impl(dec, &b, false);
+        if (rc != 0 && rc != PK_ERR_OVERFLOW) return rc;   // capacity is judged on the totals below
+        for (int i = 0; i < m; ++i) {
+            const int u = idx[i];
+            const int nt = std::min(cnt[i], cap), keep_t = std::max(0, std::min(nt, tcap - ntok[u]));
+            if (keep_t > 0)
+                memcpy(o_tok + (size_t)u * tcap + ntok[u], tok.data() + (size_t)i * cap, 4 * (size_t)keep_t);
+            if (scap) {
+                const int ns = std::min(cs[i], sc), keep_s = std::max(0, std::min(ns, scap - nseg[u]));
+                if (keep_s > 0)
+                    memcpy(o_seg + (size_t)u * scap + nseg[u], seg.data() + (size_t)i * sc, 4 * (size_t)keep_s);
+            }
+            if (rcap) {
+                const int nr = std::min(st[i], rc_cap), keep_r = std::max(0, std::min(nr, rcap - nst[u]));
+                if (keep_r > 0)
+                    memcpy(o_tr + ((size_t)u * rcap + nst[u]) * 2, tr.data() + (size_t)i * rc_cap * 2,
+                           8 * (size_t)keep_r);
+            }
+            if (o_ctrl) memcpy(o_ctrl + (size_t)u * PK_CTRL_N, ctrl.data() + (size_t)i * PK_CTRL_N, 4 * PK_CTRL_N);
+            ntok[u] += cnt[i];
+            nseg[u] += cs[i];
+            nst[u] += st[i];
+            done[u] += T[i];
+        }
+    }
+    bool over = false;
+    for (int u = 0; u < n; ++u) over = over || ntok[u] > tcap || (bt->segments && nseg[u] > scap);
+    if (dev_out) {
+        HIP_TRY(hipMemcpy(bt->tokens, h_tok.data(), h_tok.size() * 4, hipMemcpyHostToDevice));
+        HIP_TRY(hipMemcpy(bt->n_tokens, ntok.data(), 4 * (size_t)n, hipMemcpyHostToDevice));
+        HIP_TRY(hipMemcpy(bt->steps, nst.data(), 4 * (size_t)n, hipMemcpyHostToDevice));
+        if (bt->n_segments) HIP_TRY(hipMemcpy(bt->n_segments, nseg.data(), 4 * (size_t)n, hipMemcpyHostToDevice));
+        if (scap) HIP_TRY(hipMemcpy(bt->segments, h_seg.data(), h_seg.size() * 4, hipMemcpyHostToDevice));
+        if (rcap) HIP_TRY(hipMemcpy(bt->trace, h_tr.data(), h_tr.size() * 4, hipMemcpyHostToDevice));
+        if (bt->ctrl_out) HIP_TRY(hipMemcpy(bt->ctrl_out, h_ctrl.data(), h_ctrl.size() * 4, hipMemcpyHostToDevice));
+    } else {
+        memcpy(bt->n_tokens, ntok.data(), 4 * (size_t)n);
+        memcpy(bt->steps, nst.data(), 4 * (size_t)n);
+        if (bt->n_segments) memcpy(bt->n_segments, nseg.data(), 4 * (size_t)n);
+    }
+    if (over) return fail(PK_ERR_OVERFLOW, "token or segment capacity exceeded");
     return 0;
 }
 

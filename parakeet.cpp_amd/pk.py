@@ -70,7 +70,7 @@ class PkBatch(C.Structure):
 
 EXPORTED = ["pk_decoder_create", "pk_decoder_destroy", "pk_slot_init", "pk_slot_reset",
             "pk_slot_read", "pk_slot_copy", "pk_decode", "pk_decode_noalloc", "pk_last_timing", "pk_last_error",
-            "pk_device_info"]
+            "pk_device_info", "pk_window_split"]
 
 _lib = None
 
@@ -93,6 +93,8 @@ def lib():
                                      C.POINTER(C.c_int32)]
         L.pk_last_error.restype = C.c_char_p
         L.pk_device_info.argtypes = [C.POINTER(C.c_int32)] * 3
+        L.pk_window_split.argtypes = [C.c_int32, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
+                                      C.POINTER(C.c_int32), C.c_void_p]
         _lib = L
     return _lib
 
@@ -343,6 +345,16 @@ class Decoder:
         a, b, it = C.c_float(), C.c_float(), C.c_int32()
         check(lib().pk_last_timing(self.h, C.byref(a), C.byref(b), C.byref(it)))
         return dict(enc_proj_ms=a.value, loop_ms=b.value, iterations=it.value)
+
+
+def window_split(n_frames, max_symbols: int, joint_hidden: int, max_duration: int):
+    """pk_window_split: (piece_frames, launches[u]) -- how pk_decode splits windows that
+    one launch cannot take (host arithmetic, no device needed)."""
+    T = np.ascontiguousarray(n_frames, np.int32)
+    k = np.zeros(len(T), np.int32)
+    w = C.c_int32()
+    check(lib().pk_window_split(len(T), _ptr(T), max_symbols, joint_hidden, max_duration, C.byref(w), _ptr(k)))
+    return w.value, k
 
 
 def device_info():

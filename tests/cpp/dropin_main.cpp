@@ -23,6 +23,7 @@
 // Frame files: int32 n, T, D, then n*T*D float32 (utterance-major).
 #include <chrono>
 #include <cstdio>
+#include <cstring>
 #include <cstdlib>
 #include <deque>
 #include <string>
@@ -194,9 +195,61 @@ int fail(const char *what, int rc) {
 
 }  // namespace
 
+// The reference CLI's pattern (src/main.cpp:745-777): each model type keeps its
+// runtime in a function-local static, prepared on first use and destroyed at
+// process exit, after main returns.
+int run_once(const char *path, const Frames &f, std::vector<int32_t> &ids) {
+    Loaded ld;
+    if (int rc = load(path, ld)) return rc;
+    const ParakeetCtcModel &model = ld.model;
+    if (model.model_type == ParakeetModelType::TDT) {
+        static TdtRuntimeWeights rt;
+        static bool rt_ready = false;
+        if (!rt_ready) {
+            if (tdt_prepare_runtime(model, rt) != 0) return 20;
+            rt_ready = true;
+        }
+        TdtDecodeOptions dopts;
+        TdtDecodeResult dres;
+        if (int rc = tdt_greedy_decode(model, rt, f.utt(0), f.T, f.D, dopts, dres)) return rc;
+        ids = std::move(dres.token_ids);
+    } else {
+        static EouRuntimeWeights rt;
+        static bool rt_ready = false;
+        if (!rt_ready) {
+            if (eou_prepare_runtime(model, rt) != 0) return 20;
+            rt_ready = true;
+        }
+        EouDecodeOptions dopts;
+        dopts.max_symbols_per_step = model.encoder_cfg.eou_max_symbols_per_step;
+        EouDecodeResult dres;
+        if (int rc = eou_greedy_decode(model, rt, f.utt(0), f.T, f.D, dopts, dres)) return rc;
+        ids = std::move(dres.token_ids);
+    }
+    return 0;
+}
+
+// --static-exit: decode utterance 0 of each model through run_once, print the
+// token ids and return from main with both static runtimes alive.
+int static_exit(int argc, char **argv) {
+    if (argc < 6) return 2;
+    Frames ft, fe;
+    if (!read_frames(argv[3], ft) || !read_frames(argv[5], fe)) return fail("reading the frames", -1);
+    std::vector<std::vector<int32_t>> ids(2);
+    if (int rc = run_once(argv[2], ft, ids[0])) return fail("run_once(tdt)", rc);
+    if (int rc = run_once(argv[4], fe, ids[1])) return fail("run_once(eou)", rc);
+    std::printf("{\"static_exit\":");
+    lists(ids);
+    std::printf("}\n");
+    std::fflush(stdout);
+    return 0;
+}
+
 int main(int argc, char **argv) {
+    if (argc > 1 && std::strcmp(argv[1], "--static-exit") == 0) return static_exit(argc, argv);
     if (argc < 6) {
-        std::fprintf(stderr, "usage: dropin_main TDT.gguf TDT_FRAMES EOU.gguf EOU_FRAMES WINDOW [reps]\n");
+        std::fprintf(stderr, "usage: dropin_main TDT.gguf TDT_FRAMES EOU.gguf EOU_FRAMES WINDOW [reps]\n"
+                             "       dropin_main --static-exit TDT.gguf TDT_FRAMES EOU.gguf EOU_FRAMES\n");
         return 2;
     }
     const int W = std::atoi(argv[5]);

@@ -184,3 +184,31 @@ def test_dropin_matches_c_abi(tmp_path):
     assert sum(len(s) for s in e["segments"]) > 0   # the raised <EOU> bias does end segments
     print(f"dropin: tdt_greedy_decode B=1 T={T}: {t['call_us']:.1f} us per call, {t['call_steps']} steps "
           f"({t['call_us'] / max(1, t['call_steps']):.2f} us/step)", flush=True)
+
+
+@pytest.mark.gpu
+def test_dropin_static_runtime_exits_cleanly(tmp_path):
+    """The reference CLI keeps each runtime in a function-local static
+    (src/main.cpp:746, :761) that is destroyed after main returns: the process
+    must exit 0 with both runtimes alive at exit, and decode as the C ABI does."""
+    if not os.path.exists(DRIVER):
+        pytest.skip("the drop-in driver is built only where parakeet.cpp's sources are present")
+    from parakeet_amd import pk, synth
+    tdt_path, eou_path = str(tmp_path / "t.gguf"), str(tmp_path / "e.gguf")
+    small_tdt(tdt_path)
+    small_eou(eou_path)
+    encs_t = [synth.encoder_frames(970, 30, 128)]
+    encs_e = [synth.encoder_frames(971, 30, 64)]
+    _frames_file(tmp_path / "t.bin", encs_t)
+    _frames_file(tmp_path / "e.bin", encs_e)
+    print("dropin: --static-exit driver", flush=True)
+    r = subprocess.run([DRIVER, "--static-exit", tdt_path, str(tmp_path / "t.bin"), eou_path,
+                        str(tmp_path / "e.bin")], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, (r.returncode, r.stderr)
+    out = json.loads(r.stdout)["static_exit"]
+    dt = pk.Decoder.from_gguf(tdt_path, n_slots=1)
+    assert out[0] == dt.decode(encs_t)[0]["tokens"].tolist()
+    dt.close()
+    de = pk.Decoder.from_gguf(eou_path, n_slots=1)
+    assert out[1] == de.decode(encs_e, max_symbols=de.info.max_symbols)[0]["tokens"].tolist()
+    de.close()
