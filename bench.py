@@ -13,6 +13,8 @@ decode loop), the CPU baseline (the oracle, a C restatement of the
 reference's scalar decoder, timed on this host on a bounded sample), and the
 other workload shapes (--no-extras skips them):
   b1                 B=1, T=125 on the same decoder: latency per step
+  b1_cpp             the same utterance through the drop-in tdt_greedy_decode (the reference
+                     CLI's call), wall time per call and per step, host overhead included
   b1_blank4          the same with the blank logit raised by 4 (blank-dominated decoding, as a
                      trained model's is): latency per step with runs of blanks walked over
                      the joint tile's spare columns, and without them (PK_SPEC=0)
@@ -102,6 +104,42 @@ def traffic_passes(args) -> tuple[list[str] | None, str | None]:
             return None, f"{ctr} pass failed (status {r.returncode}): {r.stderr[-300:]}"
         csvs.append(found[0])
     return csvs, None
+
+
+def cpp_b1(frames=125, reps=30):
+    """B=1 latency through the reference's own decoder interface: the drop-in
+    tdt_greedy_decode (include/dropin/parakeet_tdt.h, the call the reference CLI
+    makes, src/main.cpp:745-761) on the TDT-0.6b-v3 q8_0 decoder, one 125-frame
+    utterance, timed by tests/cpp/dropin_main --bench in a child process started
+    before this process touches the GPU.  Wall time per call includes the frame
+    upload, enc_proj, the decode loop and the output copies."""
+    import subprocess
+    exe = os.path.join(ROOT, "tests", "cpp", "dropin_main")
+    if not os.path.exists(exe):
+        return {"missing": "tests/cpp/dropin_main is built only where parakeet.cpp's sources are present"}
+    import __graft_entry__ as graft
+    graft.load_package()
+    from parakeet_amd import synth
+    tmp = tempfile.mkdtemp(prefix="pk_cpp_")
+    path = os.path.join(tmp, "tdt-0.6b-v3-q8_0.gguf")
+    synth.make_shape(path, "tdt-0.6b-v3")
+    fpath = os.path.join(tmp, "frames.bin")
+    enc = synth.encoder_frames(0, frames, 1024)
+    with open(fpath, "wb") as f:
+        np.array([1, frames, 1024], np.int32).tofile(f)
+        enc.astype(np.float32).tofile(f)
+    print("[bench] b1_cpp: drop-in tdt_greedy_decode", file=sys.stderr, flush=True)
+    r = subprocess.run(["timeout", "-k", "10", "120", exe, "--bench", path, fpath, str(reps)], capture_output=True,
+                       text=True, errors="replace")
+    if r.returncode != 0:
+        return {"missing": f"dropin_main --bench failed (status {r.returncode}): {r.stderr[-300:]}"}
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    steps = max(1, d["steps"])
+    return {"api": "drop-in tdt_greedy_decode (host frames, host outputs)", "frames": frames, "steps": d["steps"],
+            "us_per_call": d["call_us"], "us_per_call_min": d["call_us_min"],
+            "us_per_step_wall": round(d["call_us"] / steps, 3),
+            "kernel_us_per_call": d["kernel_us"], "host_us_per_call": round(d["call_us"] - d["kernel_us"], 3),
+            "reps": d["reps"]}
 
 
 class Workload:
@@ -378,6 +416,9 @@ def main():
         traffic_csvs = list(args.traffic)
     elif not (args.no_traffic or args.no_extras or args.only):
         traffic_csvs, traffic_note = traffic_passes(args)
+    b1_cpp = None
+    if not (args.no_extras or args.only):
+        b1_cpp = cpp_b1()
     import __graft_entry__ as graft
     graft.load_package()
     from parakeet_amd import gguf, hipmem, pk, roofline, synth
@@ -521,6 +562,7 @@ def main():
             out[name] = run_extra(name, pk, hipmem, roofline, gguf, synth, dec, cost, tmp, D, MS, base, n_b1)
             if name == "b1":
                 wl.free()   # the B=64 frames are not needed past here
+        out["b1_cpp"] = b1_cpp
     print(json.dumps(out), flush=True)
     # every device buffer is released before the interpreter exits (no HIP call
     # runs from a finaliser after the runtime has been torn down)

@@ -151,12 +151,28 @@ int decode_launch(SlotPool &pool, int D_enc, int max_symbols, const Frames &fr, 
         reset[u] = slots[i + u]->pending_init() ? 1 : 0;
         if (!tokens_base.empty()) base[u] = tokens_base[i + u];
     }
+    // host windows: read in place when they follow one another in memory (always at
+    // B=1: the caller's pointer is the batch's frames); otherwise packed in order
     std::vector<float> packed;
+    const float *host_base = nullptr;
     if (!fr.device) {
-        packed.resize((size_t)std::max<int64_t>(rows, 1) * D_enc);
-        for (int u = 0; u < n; ++u)
-            if (T[u] > 0)
-                memcpy(packed.data() + (size_t)row[u] * D_enc, fr.host[i + u], sizeof(float) * (size_t)T[u] * D_enc);
+        bool contiguous = true;
+        const float *at = nullptr;
+        for (int u = 0; u < n && contiguous; ++u) {
+            if (T[u] <= 0) continue;
+            if (!at) host_base = fr.host[i + u];
+            else contiguous = fr.host[i + u] == at;
+            at = fr.host[i + u] + (size_t)T[u] * D_enc;
+        }
+        if (!contiguous) {
+            host_base = nullptr;
+            packed.resize((size_t)std::max<int64_t>(rows, 1) * D_enc);
+            for (int u = 0; u < n; ++u)
+                if (T[u] > 0)
+                    memcpy(packed.data() + (size_t)row[u] * D_enc, fr.host[i + u],
+                           sizeof(float) * (size_t)T[u] * D_enc);
+            host_base = packed.data();
+        }
     }
     // every emission of a window fits (at most max_symbols per frame); an EOU boundary ends
     // its frame, so a window records at most max_T + 1 of them.  Sized in 64 bits and
@@ -175,7 +191,7 @@ int decode_launch(SlotPool &pool, int D_enc, int max_symbols, const Frames &fr, 
     b.mem = fr.device ? PK_MEM_DEVICE_FRAMES : PK_MEM_HOST;
     b.d_enc = D_enc;
     b.max_symbols = max_symbols;
-    b.enc = fr.device ? fr.dev : packed.data();
+    b.enc = fr.device ? fr.dev : host_base;
     b.enc_row = row.data();
     b.n_frames = T.data();
     b.slot = sl.data();

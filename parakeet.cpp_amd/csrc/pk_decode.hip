@@ -72,6 +72,10 @@ using pkdev::kWave;
 using pkdev::kWaves;
 
 constexpr int kMaxBatch = PK_MAX_BATCH;
+// host outputs up to this size come back whole with the counters (one stream wait per call)
+constexpr size_t kEagerCopyBytes = 256 << 10;
+// host frames up to this size go up through a pinned staging block of the decoder
+constexpr size_t kPinnedFrames = 64ull << 20;
 
 thread_local std::string g_err;
 // set by an atexit handler: process teardown has begun
@@ -368,6 +372,7 @@ struct pk_decoder {
                                // utterances, so these copies are asynchronous and no call allocates)
     size_t pin_cnt = 0;        // offset of the counters in h_pin (the descriptor block ends there)
     HostBuf h_out;             // staging of host-memory outputs
+    HostBuf h_frames;          // staging of host-memory frames (up to kPinnedFrames bytes)
     unsigned char *scratch = nullptr;   // this device's fixed scratch array (pk_decode_noalloc)
     int last_iters = 0;
     int lock_fd = -1;          // this GPU's cross-process loop lock (see DeviceLoopLock), -1: none
@@ -380,7 +385,7 @@ struct pk_decoder {
             b->p = nullptr;
             b->n = 0;
         }
-        for (HostBuf *b : {&h_pin, &h_out}) {
+        for (HostBuf *b : {&h_pin, &h_out, &h_frames}) {
             b->p = nullptr;
             b->n = 0;
         }
@@ -1097,9 +1102,13 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     const float *enc = bt->enc;
     if (enc_host && rows > 0) {
         if ((rc = dec->d_enc.ensure((size_t)rows * D * 4))) return rc;
-        // one copy per run of utterances whose source rows follow each other
-        // (one copy in all when the caller packs them in order); the device
-        // rows are packed in utterance order
+        // up to kPinnedFrames bytes the rows are gathered into pinned memory and go up in one
+        // asynchronous copy; beyond, one copy from the caller's (pageable) memory per run of
+        // utterances whose source rows follow each other.  The device rows are packed in
+        // utterance order.
+        const size_t fbytes = (size_t)rows * D * 4;
+        float *pin = nullptr;
+        if (fbytes <= kPinnedFrames && dec->h_frames.ensure(fbytes) == 0) pin = dec->h_frames.as<float>();
         for (int i = 0; i < m;) {
             int j = i + 1;
             long long end = src_row[i] + T[i];
@@ -1108,12 +1117,15 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
                 ++j;
             }
             const long long n_rows = end - src_row[i];
-            if (n_rows > 0)
+            if (n_rows > 0 && pin)
+                memcpy(pin + (size_t)dst_row[i] * D, bt->enc + (size_t)src_row[i] * D, (size_t)n_rows * D * 4);
+            else if (n_rows > 0)
                 HIP_TRY(hipMemcpyAsync(dec->d_enc.as<float>() + (size_t)dst_row[i] * D,
                                        bt->enc + (size_t)src_row[i] * D, (size_t)n_rows * D * 4,
                                        hipMemcpyHostToDevice, dec->stream));
             i = j;
         }
+        if (pin) HIP_TRY(hipMemcpyAsync(dec->d_enc.p, pin, fbytes, hipMemcpyHostToDevice, dec->stream));
         enc = dec->d_enc.as<float>();
         src_row = dst_row;
     }
@@ -1342,9 +1354,10 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     int *status = dec->h_pin.as<int>();   // read after the stream synchronisation below
     HIP_TRY(hipMemcpyAsync(status, p.status, 4 * sizeof(int), hipMemcpyDeviceToHost, dec->stream));
     if (host) {
-        // the counters of every utterance in one copy (n_tokens, steps,
-        // n_segments are consecutive), then the filled prefix of each output
-        // row in one strided copy per array, staged in pinned memory
+        // the counters of every utterance in one copy (n_tokens, steps, n_segments are
+        // consecutive), into pinned memory.  Small outputs (every row whole, up to
+        // kEagerCopyBytes) and the control words follow at once, so the call waits for the
+        // stream once; larger ones copy only each row's filled prefix after the counters.
         std::vector<int> cnt_v;
         int *cnt;
         if (dec->pin_cnt + 12 * (size_t)m <= dec->h_pin.n) {   // (m <= n_slots: slots are distinct)
@@ -1354,42 +1367,59 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
             cnt = cnt_v.data();
         }
         HIP_TRY(hipMemcpyAsync(cnt, o_ntok, 12 * (size_t)m, hipMemcpyDeviceToHost, dec->stream));
+        const size_t tb = (size_t)m * tcap * 4, sb = bt->segments ? (size_t)m * scap * 4 : 0,
+                     rb = o_trace ? (size_t)m * trcap * 8 : 0, cb = o_ctrl ? (size_t)m * PK_CTRL_N * 4 : 0;
+        const bool eager = tb + sb + rb <= kEagerCopyBytes;
+        if ((rc = dec->h_out.ensure(std::max<size_t>(cb + (eager ? tb + sb + rb : 0), 64)))) return rc;
+        int32_t *s_ctrl = dec->h_out.as<int32_t>();
+        int *e_tok = s_ctrl + cb / 4, *e_seg = e_tok + tb / 4, *e_tr = e_seg + sb / 4;
+        if (cb) HIP_TRY(hipMemcpyAsync(s_ctrl, o_ctrl, cb, hipMemcpyDeviceToHost, dec->stream));
+        if (eager) {
+            if (tb) HIP_TRY(hipMemcpyAsync(e_tok, o_tok, tb, hipMemcpyDeviceToHost, dec->stream));
+            if (sb) HIP_TRY(hipMemcpyAsync(e_seg, o_seg, sb, hipMemcpyDeviceToHost, dec->stream));
+            if (rb) HIP_TRY(hipMemcpyAsync(e_tr, o_trace, rb, hipMemcpyDeviceToHost, dec->stream));
+        }
         HIP_TRY(hipStreamSynchronize(dec->stream));
         const int *c_tok = cnt, *c_steps = c_tok + m, *c_seg = c_steps + m;
-        int wt = 0, ws = 0, wr = 0;
-        for (int i = 0; i < m; ++i) {
-            wt = std::max(wt, std::min(c_tok[i], tcap));
-            ws = std::max(ws, std::min(c_seg[i], scap));
-            wr = std::max(wr, std::min(c_steps[i], trcap));
+        // rows of width wt / ws / wr (prefix copies) or of the full capacities (eager)
+        int wt = tcap, ws = bt->segments ? scap : 0, wr = o_trace ? trcap : 0;
+        const int *s_tok = e_tok, *s_seg = e_seg, *s_tr = e_tr;
+        std::vector<int> prefix;
+        if (!eager) {
+            wt = ws = wr = 0;
+            for (int i = 0; i < m; ++i) {
+                wt = std::max(wt, std::min(c_tok[i], tcap));
+                ws = std::max(ws, std::min(c_seg[i], scap));
+                wr = std::max(wr, std::min(c_steps[i], trcap));
+            }
+            if (!bt->segments) ws = 0;
+            if (!o_trace) wr = 0;
+            const size_t stage = (size_t)m * (wt + ws + 2 * (size_t)wr) * 4;
+            if (stage > 0) {
+                prefix.resize(stage / 4);
+                int *p_tok = prefix.data(), *p_seg = p_tok + (size_t)m * wt, *p_tr = p_seg + (size_t)m * ws;
+                if (wt)
+                    HIP_TRY(hipMemcpy2DAsync(p_tok, 4 * (size_t)wt, o_tok, 4 * (size_t)tcap, 4 * (size_t)wt, m,
+                                             hipMemcpyDeviceToHost, dec->stream));
+                if (ws)
+                    HIP_TRY(hipMemcpy2DAsync(p_seg, 4 * (size_t)ws, o_seg, 4 * (size_t)scap, 4 * (size_t)ws, m,
+                                             hipMemcpyDeviceToHost, dec->stream));
+                if (wr)
+                    HIP_TRY(hipMemcpy2DAsync(p_tr, 8 * (size_t)wr, o_trace, 8 * (size_t)trcap, 8 * (size_t)wr, m,
+                                             hipMemcpyDeviceToHost, dec->stream));
+                HIP_TRY(hipStreamSynchronize(dec->stream));
+                s_tok = p_tok;
+                s_seg = p_seg;
+                s_tr = p_tr;
+            }
         }
-        if (!bt->segments) ws = 0;
-        if (!o_trace) wr = 0;
-        const size_t stage = (size_t)m * (wt + ws + 2 * (size_t)wr) * 4;
-        if (stage > 0) {
-            if ((rc = dec->h_out.ensure(stage))) return rc;
-            int *s_tok = dec->h_out.as<int>(), *s_seg = s_tok + (size_t)m * wt, *s_tr = s_seg + (size_t)m * ws;
-            if (wt)
-                HIP_TRY(hipMemcpy2DAsync(s_tok, 4 * (size_t)wt, o_tok, 4 * (size_t)tcap, 4 * (size_t)wt, m,
-                                         hipMemcpyDeviceToHost, dec->stream));
-            if (ws)
-                HIP_TRY(hipMemcpy2DAsync(s_seg, 4 * (size_t)ws, o_seg, 4 * (size_t)scap, 4 * (size_t)ws, m,
-                                         hipMemcpyDeviceToHost, dec->stream));
-            if (wr)
-                HIP_TRY(hipMemcpy2DAsync(s_tr, 8 * (size_t)wr, o_trace, 8 * (size_t)trcap, 8 * (size_t)wr, m,
-                                         hipMemcpyDeviceToHost, dec->stream));
-            HIP_TRY(hipStreamSynchronize(dec->stream));
-        }
-        if (o_ctrl) {   // control words of every utterance in one copy
-            std::vector<int32_t> c((size_t)m * PK_CTRL_N);
-            HIP_TRY(hipMemcpy(c.data(), o_ctrl, c.size() * 4, hipMemcpyDeviceToHost));
+        if (o_ctrl)
             for (int i = 0; i < m; ++i)
-                memcpy(bt->ctrl_out + (size_t)map[i] * PK_CTRL_N, c.data() + (size_t)i * PK_CTRL_N, PK_CTRL_N * 4);
-        }
+                memcpy(bt->ctrl_out + (size_t)map[i] * PK_CTRL_N, s_ctrl + (size_t)i * PK_CTRL_N, PK_CTRL_N * 4);
         if (o_logits)   // debug tap: straight into the caller's rows (utterance order may differ)
             for (int i = 0; i < m; ++i)
                 HIP_TRY(hipMemcpy(bt->logits + (size_t)map[i] * lrow, o_logits + (size_t)i * lrow, lrow * 4,
                                   hipMemcpyDeviceToHost));
-        const int *s_tok = dec->h_out.as<int>(), *s_seg = s_tok + (size_t)m * wt, *s_tr = s_seg + (size_t)m * ws;
         for (int i = 0; i < m; ++i) {
             const int u = map[i];
             bt->n_tokens[u] = c_tok[i];

@@ -21,6 +21,7 @@
 //
 // Usage: dropin_main TDT.gguf TDT_FRAMES EOU.gguf EOU_FRAMES WINDOW [reps]
 // Frame files: int32 n, T, D, then n*T*D float32 (utterance-major).
+#include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cstring>
@@ -29,6 +30,7 @@
 #include <string>
 #include <vector>
 
+#include "decoder_core.h"
 #include "dropin_tensor.h"
 #include "gguf_reader.h"
 #include "parakeet_ctc.h"
@@ -245,11 +247,49 @@ int static_exit(int argc, char **argv) {
     return 0;
 }
 
+// --bench TDT.gguf FRAMES REPS: the reference CLI's decode of one utterance
+// (tdt_greedy_decode, src/main.cpp:745-761) timed REPS times after a warm-up:
+// wall time per call and the kernels' share of it (pk_last_timing).
+int bench(int argc, char **argv) {
+    if (argc < 5) return 2;
+    Frames f;
+    if (!read_frames(argv[3], f)) return fail("reading the frames", -1);
+    const int reps = std::max(1, std::atoi(argv[4]));
+    Loaded ld;
+    if (int rc = load(argv[2], ld)) return fail("loading the model", rc);
+    const ParakeetCtcModel &model = ld.model;
+    TdtRuntimeWeights rt;
+    if (int rc = tdt_prepare_runtime(model, rt)) return fail("tdt_prepare_runtime", rc);
+    TdtDecodeOptions dopts;
+    double wall = 0.0, wmin = 1e30, kern = 0.0;
+    int steps = 0;
+    for (int r = 0; r <= reps; ++r) {
+        TdtDecodeResult res;
+        const auto t0 = std::chrono::steady_clock::now();
+        if (int rc = tdt_greedy_decode(model, rt, f.utt(0), f.T, f.D, dopts, res)) return fail("tdt_greedy_decode", rc);
+        const double dt = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+        float ep = 0.f, lp = 0.f;
+        int32_t it = 0;
+        pk_last_timing(rt.pool->dec, &ep, &lp, &it);
+        if (r > 0) {   // the first call is a warm-up
+            wall += dt;
+            wmin = std::min(wmin, dt);
+            kern += 1000.0 * (ep + lp);
+        }
+        steps = res.steps;
+    }
+    std::printf("{\"call_us\":%.3f,\"call_us_min\":%.3f,\"kernel_us\":%.3f,\"steps\":%d,\"frames\":%d,\"reps\":%d}\n",
+                wall / reps, wmin, kern / reps, steps, f.T, reps);
+    return 0;
+}
+
 int main(int argc, char **argv) {
     if (argc > 1 && std::strcmp(argv[1], "--static-exit") == 0) return static_exit(argc, argv);
+    if (argc > 1 && std::strcmp(argv[1], "--bench") == 0) return bench(argc, argv);
     if (argc < 6) {
         std::fprintf(stderr, "usage: dropin_main TDT.gguf TDT_FRAMES EOU.gguf EOU_FRAMES WINDOW [reps]\n"
-                             "       dropin_main --static-exit TDT.gguf TDT_FRAMES EOU.gguf EOU_FRAMES\n");
+                             "       dropin_main --static-exit TDT.gguf TDT_FRAMES EOU.gguf EOU_FRAMES\n"
+                             "       dropin_main --bench TDT.gguf TDT_FRAMES REPS\n");
         return 2;
     }
     const int W = std::atoi(argv[5]);
