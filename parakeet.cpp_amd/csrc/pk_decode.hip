@@ -365,7 +365,7 @@ struct pk_decoder {
     DevBuf slots_h, slots_c, slots_pp, slots_r, slots_ctrl;
     DevBuf special;
     // per-call scratch
-    DevBuf d_desc, d_encp, d_clear, d_enc, d_out, d_xchg, d_prof;   // d_clear: status, barrier flags, argmax keys
+    DevBuf d_desc, d_encp, d_clear, d_enc, d_out, d_xchg, d_prof, d_lcol;   // d_clear: status, barrier flags, argmax keys
     std::vector<uint8_t> h_desc;
     HostBuf h_pin;             // pinned: 16 B of status read back, the descriptor block, then the
                                // per-utterance counters read back (sized at creation for n_slots
@@ -381,7 +381,7 @@ struct pk_decoder {
     // Drop every device and pinned allocation without freeing it (process exit).
     void forget_device() {
         for (DevBuf *b : {&arena, &eproj, &slots_h, &slots_c, &slots_pp, &slots_r, &slots_ctrl, &special, &d_desc,
-                          &d_encp, &d_clear, &d_enc, &d_out, &d_xchg, &d_prof}) {
+                          &d_encp, &d_clear, &d_enc, &d_out, &d_xchg, &d_prof, &d_lcol}) {
             b->p = nullptr;
             b->n = 0;
         }
@@ -1227,12 +1227,16 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     p.max_iter = (int)max_iter;
     p.n_dom = pl.n_dom;
     p.dom_size = pl.P;
-    // blank runs over the joint tile's spare columns (not while the logit tap records
-    // per-step rows; PK_SPEC=0 turns them off for comparisons)
+    // blank runs over the joint tile's spare columns (PK_SPEC=0 turns them off for comparisons)
     {
         const char *v = std::getenv("PK_SPEC");
-        p.spec = (lsteps == 0 && !(v && v[0] == '0')) ? 1 : 0;
+        p.spec = !(v && v[0] == '0') ? 1 : 0;
     }
+    // logit tap staging: one row of Vo logits per joint column of each domain
+    p.lcol = nullptr;
+    if (lsteps > 0 &&
+        (rc = cs.get(dec->d_lcol, (size_t)pl.n_dom * pkdev::kColCap * p.Vo * 4, reinterpret_cast<void **>(&p.lcol))))
+        return rc;
     p.nt = pl.nt;
     p.dom_n = d_dom_n;
     p.dom_list = d_dom_list;

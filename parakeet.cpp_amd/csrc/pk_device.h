@@ -99,6 +99,8 @@ struct KParams {
     int *segs; int seg_cap; int *n_segs;
     int *trace; int trace_cap;
     float *logits; int logit_steps;   // nullable debug tap [n_utts][logit_steps][Vo]
+    float *lcol;                 // tap staging [n_dom][kColCap][Vo]: each joint column's logits of one
+                                 // iteration, copied to the row of the step that takes the column
     const int *reset;            // nullable [n_utts]: 1 = fresh state whatever the slot holds
     int *ctrl_out;               // nullable [n_utts][PK_CTRL_N]: control words after the call
     // exchange buffers of one launch (batch-indexed, written/read coherently)
@@ -437,6 +439,8 @@ struct Ctl {                      // per-workgroup copy of its domain's control 
     int pass[PK_MAX_LAYERS + 1];  // items per pass of the phase consuming layer l's output (l < L), of W_o (L)
     unsigned mag_p, mag_h, mag_units;   // udiv multipliers for P, H and 4 * own_lstm
     unsigned wmask;               // bit ul: this workgroup writes utterance ul's outputs (ul % P == rank)
+    int tq_n, tq_col[kColCap], tq_b[kColCap], tq_step[kColCap];   // logit tap: (column, utterance, step)
+                                                                  // of this iteration's decisions
     unsigned long long wgkey[kColCap][2];   // this workgroup's best key per joint column and head
     unsigned long long prof[kPrN];
 };
@@ -1132,12 +1136,10 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
         // (b_out is zero-padded to whole tiles)
         const float *btab = S.bias + kTile * ((p.L - 1) * s.own_lstm + s.own_pred);
         TL(1);
-        // debug logit tap: this lane's utterance row of the current step
+        // debug logit tap: this lane's column (spare columns included) into the staging rows;
+        // the decision step copies a column to the row of the step that takes it
         float *ltap = nullptr;
-        if (p.logits && u < nc) {   // (no spare columns while the tap is on: column = joint-list index)
-            const int ul = s.cu[c0 + u], step = s.steps[ul];
-            if (step < p.logit_steps) ltap = p.logits + ((size_t)s.b[ul] * p.logit_steps + step) * p.Vo;
-        }
+        if (p.logits && u < nc) ltap = p.lcol + ((size_t)s.dom * kColCap + c0 + u) * p.Vo;
         // each lane keeps its best key per head over all its rows; the four
         // lanes of one utterance then combine, and one LDS atomic per utterance
         // and head follows
@@ -1155,7 +1157,7 @@ __device__ __forceinline__ void joint_phase(const KParams &p, Ctl &s, const Bufs
                           const float bias = i == 0 ? bias4.x : i == 1 ? bias4.y : i == 2 ? bias4.z : bias4.w;
                           float v = acc[i] + bias;
                           if (row == p.blank) v += bb;
-                          if (ltap) ltap[row] = v;
+                          if (ltap) st_coh(ltap + row, v);
                           if (row < p.V1) {
                               const unsigned long long key = make_key(v, row);
                               best0 = key > best0 ? key : best0;
@@ -1479,6 +1481,12 @@ __device__ __forceinline__ void decide_steps(const KParams &p, Ctl &s, unsigned 
             const int tok = key_index(kt);
             const int di = p.Dn > 0 ? key_index(kd) : -1;
             const int step = s.steps[ul]++;
+            if (p.logits && step < p.logit_steps) {
+                const int q = atomicAdd(&s.tq_n, 1);
+                s.tq_col[q] = col;
+                s.tq_b[q] = b;
+                s.tq_step[q] = step;
+            }
             if (writer && p.trace) {
                 if (step < p.trace_cap) {
                     p.trace[((size_t)b * p.trace_cap + step) * 2] = tok;
@@ -1557,11 +1565,30 @@ __device__ __forceinline__ void decide_steps(const KParams &p, Ctl &s, unsigned 
     }
 }
 
+// Logit tap: the staged logits of each column a decision took go to the row of
+// that decision's step.  Every workgroup copies the rows of its own W_o tiles,
+// the ones it staged (so no other workgroup's stores are read).
+__device__ __forceinline__ void tap_copy(const KParams &p, Ctl &s) {
+    __builtin_amdgcn_s_waitcnt(0);   // this workgroup's staging stores are complete
+    lds_sync();
+    const int rows = s.own_out * kTile;
+    for (int e = threadIdx.x; e < s.tq_n * rows; e += kBlock) {
+        const int q = e / rows, r = e - q * rows;
+        const int row = (s.rank + (r / kTile) * s.P) * kTile + r % kTile;
+        if (row >= p.Vo) continue;
+        const float v = ld_coh(p.lcol + ((size_t)s.dom * kColCap + s.tq_col[q]) * p.Vo + row);
+        p.logits[((size_t)s.tq_b[q] * p.logit_steps + s.tq_step[q]) * p.Vo + row] = v;
+    }
+    lds_sync();
+    if (threadIdx.x == 0) s.tq_n = 0;
+}
+
 __device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp, bool gathered) {
     if (!gathered) gather_shards(p, s, stamp);
     TLA(30);
     if (s.ncol > s.nj) decide_steps<true>(p, s, stamp);
     else decide_steps<false>(p, s, stamp);
+    if (p.logits) tap_copy(p, s);
 }
 
 template <int WC, bool ONE>
@@ -1606,6 +1633,7 @@ __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
     }
 
     if (threadIdx.x < kPrN) s.prof[threadIdx.x] = 0ull;
+    if (threadIdx.x == 0) s.tq_n = 0;
 #ifdef PK_TIMELINE
     if (threadIdx.x < kWaves * kTl) tl_sum()[threadIdx.x] = 0ull;
     if (threadIdx.x < 2 + kTl) tl_ctl()[threadIdx.x] = 0;

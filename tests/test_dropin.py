@@ -22,6 +22,7 @@ import numpy as np
 import pytest
 
 from conftest import ROOT, small_eou, small_tdt
+from parity import check_window
 
 REF = os.environ.get("PK_REFERENCE", "/root/reference")
 REF_SRC = os.path.join(REF, "src")
@@ -139,8 +140,13 @@ def test_dropin_matches_c_abi(tmp_path):
     out = json.loads(r.stdout)
 
     dt = pk.Decoder.from_gguf(tdt_path, n_slots=3)
-    ref_t = dt.decode(encs_t)
+    ref_t = dt.decode(encs_t, trace=True)
     pieces_t, blank_t = dt.info.pieces, dt.info.blank
+    # the drop-in's tokens against the oracle: the same window replayed through it
+    # (teacher-forced on the decisions, zero unexplained mismatches, final state within 1e-3)
+    omt = oracle.OracleModel.from_gguf(tdt_path, G)
+    for u in range(3):
+        check_window(omt, dt, u, encs_t[u], ref_t[u], omt.new_state(), 10)
     dt.close()
     t = out["tdt"]
     for u in range(3):

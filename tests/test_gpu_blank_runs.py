@@ -129,3 +129,36 @@ def test_argmax_slots_equal_sharded_atomics(tmp_path, B):
             a, b = dev.read_state(base + u), dev.read_state(base + B + u)
             assert np.array_equal(a["h"], b["h"]) and np.array_equal(a["c"], b["c"]), (bias, u)
     dev.close()
+
+
+@pytest.mark.parametrize("B", [2, 4, 40])
+def test_logit_tap_with_blank_runs(tmp_path, B):
+    """The logit tap with the runs on: the joint logits of every step, including
+    the steps a run takes from a spare column (possibly several frames ahead,
+    after a duration skip), equal the oracle's logits of the same step within
+    1e-3 (src/parakeet_tdt.cpp:154-177), and the bits equal the tap with the
+    runs off."""
+    from parakeet_amd import gguf, pk, synth
+    import oracle
+    from parity import rel
+    path = str(tmp_path / "tdt06.gguf")
+    synth.make_shape(path, "tdt-0.6b-v3")
+    dev = pk.Decoder.from_gguf(path, n_slots=2 * B)
+    om = oracle.OracleModel.from_gguf(path, gguf)
+    encs = [synth.encoder_frames(1300 + u, 40 + 3 * (u % 4), 1024) for u in range(B)]
+    bb = np.full(B, 4.0, np.float32)
+    TAP = 64
+    print(f"logit tap with blank runs: TDT-0.6b B={B}, blank +4, {TAP} steps", flush=True)
+    on, off, it_on, it_off = _both(dev, encs, B, blank_bias=bb, max_symbols=10, logit_steps=TAP)
+    assert it_on < it_off, (it_on, it_off)           # the runs were taken
+    worst = 0.0
+    for u in range(B):
+        assert np.array_equal(on[u]["trace"], off[u]["trace"]), u
+        n = min(TAP, on[u]["steps"])
+        assert np.array_equal(on[u]["logits"][:n], off[u]["logits"][:n]), u
+        rep = om.replay_window(encs[u], om.new_state(), 10, on[u]["trace"], blank_bias=4.0, n_tap=TAP)
+        assert rep["stats"]["unexplained"] == 0, rep["stats"]
+        for j in range(n):
+            worst = max(worst, rel(on[u]["logits"][j], rep["logits"][j]))
+    assert worst < 1e-3, worst
+    print(f"  iterations {it_on} (runs on) vs {it_off}; worst logit rel {worst:.2e}", flush=True)

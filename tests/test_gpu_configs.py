@@ -146,7 +146,8 @@ def test_cfg4_eou_streaming_sessions(tmp_path):
 
 def test_cfg5_ragged_blank_bias(tdt06):
     """B=512, T ~ U{50..1500}, blank offsets {0,+2,+4}: batch invariance for a
-    sample (bitwise), oracle replay for a sample of short utterances."""
+    sample (bitwise), oracle replay of the six shortest utterances and of one
+    utterance of at least 1,000 frames per blank offset."""
     from parakeet_amd import pk, synth
     path, om = tdt06
     B = 512
@@ -160,11 +161,16 @@ def test_cfg5_ragged_blank_bias(tdt06):
     for k, u in enumerate(sample):
         alone = dev.decode([encs[u]], slots=[B + k], trace=True, blank_bias=bb[u:u + 1])[0]
         assert np.array_equal(alone["trace"], res[u]["trace"]), u
+    # replayed: the 6 shortest utterances, and one utterance of at least 1,000 frames per
+    # blank offset (long blank-biased utterances chain runs of blanks over spare columns)
     short = [int(u) for u in order[:6]]
-    reps = _replay_all(om, [encs[u] for u in short], [res[u] for u in short], 10,
-                       blank_bias=[bb[u] for u in short])
-    reps = [(short[i], rep, st) for i, rep, st in reps]
+    longs = [int(next(u for u in order[::-1] if Ts[u] >= 1000 and bb[u] == b)) for b in (0.0, 2.0, 4.0)]
+    picked = short + longs
+    reps = _replay_all(om, [encs[u] for u in picked], [res[u] for u in picked], 10,
+                       blank_bias=[bb[u] for u in picked])
+    reps = [(picked[i], rep, st) for i, rep, st in reps]
     _assert_replays(dev, reps, res)
+    print(f"cfg5: replayed long utterances {[(u, int(Ts[u]), float(bb[u])) for u in longs]}", flush=True)
     dens = [np.mean(res[u]["trace"][:, 0] == 8192) for u in range(B)]
     by_bias = {b: float(np.mean([d for d, x in zip(dens, bb) if x == b])) for b in (0.0, 2.0, 4.0)}
     assert by_bias[0.0] <= by_bias[2.0] <= by_bias[4.0], by_bias

@@ -341,3 +341,31 @@ def test_carry_larger_than_window_is_dropped(tmp_path):
     assert r["steps"] == 0 and st.st.carry_frames == 0   # 2 frames of carry dropped
     r = om.decode_window(np.zeros((1, 128), np.float32), st, 10)
     assert r["steps"] == 1
+
+
+def test_replay_counts_planted_near_tie(tmp_path):
+    """The replay's classifier: a decision that differs from the oracle argmax by
+    less than the tie bound (top-2 margin < 1e-4) is a near-tie, not an
+    unexplained mismatch; the same decision at a margin above the bound is
+    unexplained.  Scripted logits (zero joint weights, biases only): token 5 at
+    1.0 and token 9 just below it, duration index 1 (duration 1) on top, so the
+    margin is exactly what the bias sets, whatever the state."""
+    V1 = 62
+    for gap, tie in ((5e-5, True), (3e-4, False)):
+        bias = np.zeros(V1 + 5, np.float32)
+        bias[5], bias[9], bias[V1 + 1], bias[V1 + 2] = 1.0, 1.0 - gap, 1.0, 1.0 - gap
+        om = _scripted(tmp_path, small_tdt, bias, name=f"tie{int(tie)}.gguf")
+        enc = np.zeros((8, 128), np.float32)
+        r = om.decode_window(enc, om.new_state(), 10, trace=True)
+        assert r["tokens"].tolist() == [5] * 8
+        planted = r["trace"].copy()
+        planted[3, 0] = 9                                  # the runner-up token at step 3
+        planted[7, 1] = 2                                  # the runner-up duration index at the last step
+        rep = om.replay_window(enc, om.new_state(), 10, planted)
+        s = rep["stats"]
+        assert s["structure_error"] == 0
+        assert rep["tokens"].tolist() == [5, 5, 5, 9, 5] + [5] * (len(rep["tokens"]) - 5)
+        if tie:
+            assert s["near_ties"] == 2 and s["unexplained"] == 0, s
+        else:
+            assert s["near_ties"] == 0 and s["unexplained"] == 2 and s["first_unexplained"] == 3, s
