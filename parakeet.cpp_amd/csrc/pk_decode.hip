@@ -76,6 +76,8 @@ constexpr int kMaxBatch = PK_MAX_BATCH;
 constexpr size_t kEagerCopyBytes = 256 << 10;
 // host frames up to this size go up through a pinned staging block of the decoder
 constexpr size_t kPinnedFrames = 64ull << 20;
+// windows shorter than this many frames do not fill the LDS weight cache
+constexpr int kCacheMinFrames = 16;
 
 thread_local std::string g_err;
 // set by an atexit handler: process teardown has begun
@@ -1171,14 +1173,38 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     const int *d_dom_wg = reinterpret_cast<const int *>(put(pl.dom_wg.data(), 4 * pl.dom_wg.size()));
     HIP_TRY(hipMemcpyAsync(d_desc, hd, desc_bytes, hipMemcpyHostToDevice, dec->stream));
 
+    // argmax shards: about 8 ranks per shard
+    p.shards = 1;
+    while (p.shards < pkdev::kShards && p.shards * 8 < pl.P) p.shards *= 2;
+    const size_t keys_bytes = (size_t)2 * pl.n_dom * pkdev::kColCap * p.shards * 2 * 8;
+    // one-domain launches: per-workgroup argmax key slots (used while at most
+    // kSlotCols joint columns are live); PK_ARGMAX_SLOTS=0 keeps the sharded
+    // atomics and barrier instead (for comparisons)
+    const char *slots_env = std::getenv("PK_ARGMAX_SLOTS");
+    const bool use_slots = pl.n_dom == 1 && !(slots_env && slots_env[0] == '0');
+    const size_t slots_bytes = use_slots ? (size_t)2 * pl.P * pkdev::kSlotCols * 2 * 8 : 0;
+    // the words every launch starts from zero, in one allocation cleared by
+    // one fill: 64 B of status, the barrier flags, the argmax keys and slots
+    const size_t flags_bytes = (size_t)nwg * kFlagStride * 4,
+                 clear_bytes = 256 + flags_bytes + keys_bytes + slots_bytes;
+    void *d_clear = nullptr;
+    if ((rc = cs.get(dec->d_clear, clear_bytes, &d_clear))) return rc;
+    // (one fill kernel, never a memset, so that the call may run under graph capture)
+    const size_t clear_words = clear_bytes / 4;   // clear_bytes is a multiple of 32
+
     HIP_TRY(hipEventRecord(dec->ev[0], dec->stream));
     float *d_encp = nullptr;
     if (rows > 0) {
         if ((rc = cs.get(dec->d_encp, (size_t)rows * J * 4, reinterpret_cast<void **>(&d_encp)))) return rc;
-        // tiles over the packed rows of all utterances
+        // tiles over the packed rows of all utterances; the kernel also clears the loop's words
         dim3 grid((unsigned)((rows + pkdev::kEpTile - 1) / pkdev::kEpTile), 1, (J + pkdev::kEpTile - 1) / pkdev::kEpTile);
         pkdev::enc_proj_kernel<<<grid, 256, 0, dec->stream>>>(dec->w_enc_hi, dec->w_enc_lo, J, dec->b_enc, enc, D,
-                                                              d_src, d_dst, m, rows, d_encp);
+                                                              d_src, d_dst, m, rows, d_encp,
+                                                              static_cast<unsigned *>(d_clear), clear_words);
+        HIP_TRY(hipGetLastError());
+    } else {
+        pkdev::fill_zero_kernel<<<(unsigned)std::min<size_t>((clear_words + 255) / 256, 1024), 256, 0, dec->stream>>>(
+            static_cast<unsigned *>(d_clear), clear_words);
         HIP_TRY(hipGetLastError());
     }
     HIP_TRY(hipEventRecord(dec->ev[1], dec->stream));
@@ -1243,22 +1269,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     p.wg_dom = d_wg_dom;
     p.wg_rank = d_wg_rank;
     p.dom_wg = d_dom_wg;
-    // argmax shards: about 8 ranks per shard
-    p.shards = 1;
-    while (p.shards < pkdev::kShards && p.shards * 8 < pl.P) p.shards *= 2;
-    const size_t keys_bytes = (size_t)2 * pl.n_dom * pkdev::kColCap * p.shards * 2 * 8;
-    // one-domain launches: per-workgroup argmax key slots (used while at most
-    // kSlotCols joint columns are live); PK_ARGMAX_SLOTS=0 keeps the sharded
-    // atomics and barrier instead (for comparisons)
-    const char *slots_env = std::getenv("PK_ARGMAX_SLOTS");
-    const bool use_slots = pl.n_dom == 1 && !(slots_env && slots_env[0] == '0');
-    const size_t slots_bytes = use_slots ? (size_t)2 * pl.P * pkdev::kSlotCols * 2 * 8 : 0;
-    // the words every launch starts from zero, in one allocation cleared by
-    // one fill: 64 B of status, the barrier flags, the argmax keys and slots
-    const size_t flags_bytes = (size_t)nwg * kFlagStride * 4,
-                 clear_bytes = 256 + flags_bytes + keys_bytes + slots_bytes;
-    void *d_clear = nullptr, *d_xchg = nullptr;
-    if ((rc = cs.get(dec->d_clear, clear_bytes, &d_clear))) return rc;
+    void *d_xchg = nullptr;
     const size_t xh = 2 * (size_t)L * m * H, xp = (size_t)m * J, xr = 2 * (size_t)L * m * 4 * H;
     // the loop addresses the exchange buffers with 32-bit buffer offsets
     if ((2 * xh + xp + xr) * 4 >= (1ull << 31))
@@ -1275,14 +1286,6 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     p.slots = slots_bytes ? reinterpret_cast<unsigned long long *>(static_cast<uint8_t *>(d_clear) + 256 +
                                                                  flags_bytes + keys_bytes)
                           : nullptr;
-    if (cs.fixed) {   // the fixed scratch keeps the last call's contents: cleared by a fill kernel
-        const size_t words = clear_bytes / 4;   // clear_bytes is a multiple of 32
-        pkdev::fill_zero_kernel<<<(unsigned)std::min<size_t>((words + 255) / 256, 1024), 256, 0, dec->stream>>>(
-            static_cast<unsigned *>(d_clear), words);
-        HIP_TRY(hipGetLastError());
-    } else {
-        HIP_TRY(hipMemsetAsync(d_clear, 0, clear_bytes, dec->stream));
-    }
     // PK_PROFILE_PHASES=1: workgroup 0 accumulates per-phase wall-clock time (stderr summary)
     const bool prof = !cs.fixed && getenv("PK_PROFILE_PHASES") != nullptr;
     p.prof = nullptr;
@@ -1329,6 +1332,10 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     // consume one layer's output, or W_o) are copied into LDS once per launch
     // when the workgroup's tiles of both fit; the LSTM phases are tried first
     // (smaller), then the joint.  A phase whose tiles do not fit reads them from L2.
+    // Windows of fewer than kCacheMinFrames frames (streaming chunks: a few lockstep
+    // iterations per launch) read every phase from L2: the fill would cost more than the
+    // iterations it serves.
+    const bool cache_ok = max_T >= kCacheMinFrames;
     {
         std::vector<std::vector<pkdev::TMat *>> phases;
         for (int lc = 0; lc < p.L; ++lc) phases.push_back({lc + 1 < p.L ? &p.w_ih[lc + 1] : &p.w_pred, &p.w_hh[lc]});
@@ -1340,7 +1347,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
         for (auto &ph : phases) {
             size_t need = 0;
             for (auto *m : ph) need += bytes(m);
-            const bool fits = lds + off + need <= dec->lds_bytes;
+            const bool fits = cache_ok && lds + off + need <= dec->lds_bytes;
             for (auto *m : ph) {
                 m->lds_off = fits ? (int)off : -1;
                 if (fits) off += bytes(m);

@@ -331,14 +331,25 @@ __global__ void __launch_bounds__(256) fill_zero_kernel(unsigned *__restrict p, 
 // dst_row[u] + T[u]), so short windows of many utterances share tiles; a
 // row's utterance is the last u with dst_row[u] <= row.
 constexpr int kEpTile = 64, kEpK = 32, kEpStride = kEpK + 8;   // LDS row stride in halves
+// The global loads of K step k+1 are issued before the products of step k (one
+// register set ahead), so each step waits for LDS and the matrix cores rather
+// than for memory.  Threads of the whole grid also zero `clear_words` 32-bit
+// words at `clear` (the decode loop's status, barrier flags and argmax keys),
+// which saves the loop a separate fill.
 __global__ void __launch_bounds__(256) enc_proj_kernel(const _Float16 *__restrict whi, const _Float16 *__restrict wlo,
                                                        int J, const float *__restrict bias,
                                                        const float *__restrict enc, int d_enc,
                                                        const long long *__restrict src_row,
                                                        const long long *__restrict dst_row, int n_utts,
-                                                       long long rows, float *__restrict out) {
+                                                       long long rows, float *__restrict out,
+                                                       unsigned *__restrict clear, size_t clear_words) {
     __shared__ __attribute__((aligned(16))) _Float16 ah[kEpTile * kEpStride], al[kEpTile * kEpStride];
     __shared__ __attribute__((aligned(16))) _Float16 bh[kEpTile * kEpStride], bl[kEpTile * kEpStride];
+    {
+        const size_t nthreads = (size_t)gridDim.x * gridDim.z * 256;
+        const size_t gtid = ((size_t)blockIdx.z * gridDim.x + blockIdx.x) * 256 + threadIdx.x;
+        for (size_t i = gtid; i < clear_words; i += nthreads) clear[i] = 0u;
+    }
     const long long m0 = (long long)blockIdx.x * kEpTile;
     const int n0 = blockIdx.z * kEpTile;
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -356,16 +367,26 @@ __global__ void __launch_bounds__(256) enc_proj_kernel(const _Float16 *__restric
         }
         src = enc + (size_t)(src_row[lo] + (r - dst_row[lo])) * d_enc;
     }
+    const int j = n0 + sr;
+    // one K step's global operands of this thread: 8 frame values, 8 W_e values (hi, lo)
+    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+    half8 wh = half8{}, wl = half8{};
+    auto fetch = [&](int k0) {
+        if (live) {
+            v0 = *reinterpret_cast<const float4 *>(src + k0 + sc);
+            v1 = *reinterpret_cast<const float4 *>(src + k0 + sc + 4);
+        }
+        if (j < J) {
+            wh = *reinterpret_cast<const half8 *>(whi + (size_t)j * d_enc + k0 + sc);
+            wl = *reinterpret_cast<const half8 *>(wlo + (size_t)j * d_enc + k0 + sc);
+        }
+    };
     f32x4 acc[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    fetch(0);
     for (int k0 = 0; k0 < d_enc; k0 += kEpK) {
         {
-            float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
-            if (live) {
-                v0 = *reinterpret_cast<const float4 *>(src + k0 + sc);
-                v1 = *reinterpret_cast<const float4 *>(src + k0 + sc + 4);
-            }
             const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
             half8 h, l;
 #pragma unroll
@@ -375,16 +396,11 @@ __global__ void __launch_bounds__(256) enc_proj_kernel(const _Float16 *__restric
             }
             *reinterpret_cast<half8 *>(ah + sr * kEpStride + sc) = h;
             *reinterpret_cast<half8 *>(al + sr * kEpStride + sc) = l;
-            const int j = n0 + sr;
-            half8 wh = half8{}, wl = half8{};
-            if (j < J) {
-                wh = *reinterpret_cast<const half8 *>(whi + (size_t)j * d_enc + k0 + sc);
-                wl = *reinterpret_cast<const half8 *>(wlo + (size_t)j * d_enc + k0 + sc);
-            }
             *reinterpret_cast<half8 *>(bh + sr * kEpStride + sc) = wh;
             *reinterpret_cast<half8 *>(bl + sr * kEpStride + sc) = wl;
         }
         __syncthreads();
+        if (k0 + kEpK < d_enc) fetch(k0 + kEpK);   // in flight during this step's products
         const int ao = (wave * 16 + (lane & 15)) * kEpStride + (lane >> 4) * 8;
         const half8 a_h = *reinterpret_cast<const half8 *>(ah + ao);
         const half8 a_l = *reinterpret_cast<const half8 *>(al + ao);
