@@ -711,12 +711,20 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
         see(kp.w_pred);
         see(kp.w_out);
         using namespace pkdev;
-        dec->loop_fn[0] = all_q8 ? reinterpret_cast<const void *>(decode_loop_kernel<kWcQ8, false>)
-                        : all_half ? reinterpret_cast<const void *>(decode_loop_kernel<kWcHalf, false>)
-                                   : reinterpret_cast<const void *>(decode_loop_kernel<kWcAny, false>);
-        dec->loop_fn[1] = all_q8 ? reinterpret_cast<const void *>(decode_loop_kernel<kWcQ8, true>)
-                        : all_half ? reinterpret_cast<const void *>(decode_loop_kernel<kWcHalf, true>)
-                                   : reinterpret_cast<const void *>(decode_loop_kernel<kWcAny, true>);
+        // PK_GEMV=1 (comparisons only): all-q8_0 decoders run the instantiation with the
+        // wavefront-reduction GEMV form for column tiles of at most 4 live utterances
+        const char *gv = std::getenv("PK_GEMV");
+        if (all_q8 && gv && gv[0] == '1') {
+            dec->loop_fn[0] = reinterpret_cast<const void *>(decode_loop_kernel<pkdev::kWcQ8Gemv, false>);
+            dec->loop_fn[1] = reinterpret_cast<const void *>(decode_loop_kernel<pkdev::kWcQ8Gemv, true>);
+        } else {
+            dec->loop_fn[0] = all_q8 ? reinterpret_cast<const void *>(decode_loop_kernel<kWcQ8, false>)
+                            : all_half ? reinterpret_cast<const void *>(decode_loop_kernel<kWcHalf, false>)
+                                       : reinterpret_cast<const void *>(decode_loop_kernel<kWcAny, false>);
+            dec->loop_fn[1] = all_q8 ? reinterpret_cast<const void *>(decode_loop_kernel<kWcQ8, true>)
+                            : all_half ? reinterpret_cast<const void *>(decode_loop_kernel<kWcHalf, true>)
+                                       : reinterpret_cast<const void *>(decode_loop_kernel<kWcAny, true>);
+        }
     }
     size_t stat = 0;   // the larger static LDS of the two instantiations
     for (const void *fn : dec->loop_fn) {

@@ -825,6 +825,51 @@ __device__ __forceinline__ f32x4 unit_mma(const uint4 (&f)[kUnitOf<Q8>], const h
     return acc + lo;
 }
 
+// Wavefront-reduction GEMV form of unit_mma for column tiles with at most
+// kGemvCols live utterances (q8_0 weights): VALU dot products instead of a
+// 16-column MFMA tile of which at most kGemvCols columns are live.  Lane l
+// takes weight row l % 16 and the K slice 8 (l / 16) .. +7 of every block (the
+// fragment it loaded), multiplies it with each live utterance's activations
+// (hi + lo, exact in f32) in f32, scales by the block's d, and the four lanes
+// of a row sum their slices with two shuffles.  The partial lands in the
+// layout unit_mma produces (lane l < 16: row l, utterances 0 .. 3), so the
+// reduce and the epilogues are the same; columns 4 .. 15 read as zero.
+constexpr int kGemvCols = 4;
+template <int U>
+__device__ __forceinline__ f32x4 unit_gemv(const uint4 (&f)[U], const Act &x, int sb0, int nb, int lane) {
+    const int g = lane >> 4;
+    float acc[kGemvCols] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const unsigned q0 = f[j].x, q1 = f[j].y;
+        // the stored bytes are q + 128: exact small integers in f32
+        const float w[8] = {(float)(q0 & 0xffu) - 128.f, (float)((q0 >> 8) & 0xffu) - 128.f,
+                            (float)((q0 >> 16) & 0xffu) - 128.f, (float)(q0 >> 24) - 128.f,
+                            (float)(q1 & 0xffu) - 128.f, (float)((q1 >> 8) & 0xffu) - 128.f,
+                            (float)((q1 >> 16) & 0xffu) - 128.f, (float)(q1 >> 24) - 128.f};
+        const float d = (float)__builtin_bit_cast(_Float16, (unsigned short)f[j].z);
+        // blocks past the weights' K (zero scales, matrices padded to whole units) read the last
+        // real block's activations, which are finite
+        const int ko = (sb0 + min(j, nb - 1)) * 32 + g * 8;
+#pragma unroll
+        for (int u = 0; u < kGemvCols; ++u) {
+            if (u >= x.n) break;   // wave-uniform
+            const half8 h = *reinterpret_cast<const half8 *>(x.hi + u * x.kp + ko);
+            const half8 l = *reinterpret_cast<const half8 *>(x.lo + u * x.kp + ko);
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sum = fmaf(w[i], (float)h[i] + (float)l[i], sum);
+            acc[u] = fmaf(d, sum, acc[u]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kGemvCols; ++u) {
+        acc[u] += __shfl_xor(acc[u], 16, kWave);
+        acc[u] += __shfl_xor(acc[u], 32, kWave);
+    }
+    return lane < kTile ? f32x4{acc[0], acc[1], acc[2], acc[3]} : f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
 // Wave w's unit range [c0, c1) of N units.  Waves w and w + 4 share SIMD w & 3,
 // and the older one (w < 4) wins the issue arbitration: for equal ranges the
 // younger one finishes 15-30 % later, and the reduce waits for it.  So each SIMD
@@ -844,7 +889,7 @@ __device__ __forceinline__ void wave_range(int N, int w, int &c0, int &c1) {
 }
 
 // Partials of items j0 .. j1-1 (one pass), K-major, next unit's weights prefetched.
-template <bool Q8, bool CACHED, bool FULL>
+template <bool Q8, bool CACHED, bool FULL, bool GV = false>
 __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMat &Bm, int j0, int j1, int rank, int P,
                                                const Act &x, f32x4 *red, const unsigned char *wc) {
     // wave-uniform unit bookkeeping: the weight buffer descriptors stay in SGPRs
@@ -902,11 +947,15 @@ __device__ __forceinline__ void phase_partials(const TMat &A, int n_a, const TMa
         else if (Q8 && !CACHED) load(j0 + i, c, fn);
         else if (!CACHED) load(j0 + il, cl, fn);   // f16 / f32: the wave's last unit (see below)
         const int sb0 = c * U;
-        if (c != cur) {
-            unit_act(x, xo, two, sb0, min(U, KBa - sb0), ah, al);
-            cur = c;
+        if constexpr (GV) {
+            red[(i * S + c) * kWave + lane] = unit_gemv<U>(fc, x, sb0, min(U, KBa - sb0), lane);
+        } else {
+            if (c != cur) {
+                unit_act(x, xo, two, sb0, min(U, KBa - sb0), ah, al);
+                cur = c;
+            }
+            red[(i * S + c) * kWave + lane] = unit_mma<Q8>(fc, ah, al, two, sb0, f32x4{0.f, 0.f, 0.f, 0.f});
         }
-        red[(i * S + c) * kWave + lane] = unit_mma<Q8>(fc, ah, al, two, sb0, f32x4{0.f, 0.f, 0.f, 0.f});
         ++u;
         c = nc;
         i = ni;
@@ -940,7 +989,11 @@ __device__ __forceinline__ void phase_reduce(int j0, int j1, int S, const f32x4 
 // Weight classes the decode loop is compiled for: each instantiation carries
 // only the phase engines its matrices need (a smaller kernel with its own
 // register allocation).  kWcAny serves models whose phases mix storage types.
-enum { kWcQ8 = 0, kWcHalf = 1, kWcAny = 2 };
+// kWcQ8Gemv: all-q8_0 decoders with the wavefront-reduction GEMV form for column
+// tiles of at most kGemvCols live utterances (its own instantiation, so the
+// default kernels keep their registers; selected by PK_GEMV=1 for comparisons:
+// the MFMA form measured faster at every batch size).
+enum { kWcQ8 = 0, kWcHalf = 1, kWcAny = 2, kWcQ8Gemv = 3 };
 
 // Products of one phase for this workgroup, then the epilogue per item, in
 // passes of at most `batch` items (red_slots / S, computed once per launch).
@@ -951,7 +1004,7 @@ __device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm
     // both matrices of a phase are in the LDS weight cache or neither
     const bool cached = wc != nullptr && A.lds_off >= 0;
     const int KBe = A.type == PK_TYPE_F32 ? 2 * A.KB : A.KB;
-    const int U = WC == kWcQ8 ? kUnitOf<true> : WC == kWcHalf ? kUnitOf<false> : unit_blocks(A.type);
+    const int U = (WC == kWcQ8 || WC == kWcQ8Gemv) ? kUnitOf<true> : WC == kWcHalf ? kUnitOf<false> : unit_blocks(A.type);
     const int S = (KBe + U - 1) / U;
     for (int j0 = 0; j0 < n_items; j0 += batch) {
         const int j1 = min(n_items, j0 + batch);
@@ -959,14 +1012,20 @@ __device__ __forceinline__ void run_phase(const TMat &A, int n_a, const TMat &Bm
         // matrices are stored with whole units of K blocks (zero blocks past
         // K / 32), so unit loads are never masked
         auto q8 = [&]() {
-            if (cached) phase_partials<true, true, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
-            else phase_partials<true, false, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
+            if (WC == kWcQ8Gemv && x.n <= kGemvCols) {
+                if (cached) phase_partials<true, true, true, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
+                else phase_partials<true, false, true, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
+            } else if (cached) {
+                phase_partials<true, true, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
+            } else {
+                phase_partials<true, false, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
+            }
         };
         auto half = [&]() {
             if (cached) phase_partials<false, true, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
             else phase_partials<false, false, true>(A, n_a, Bm, j0, j1, rank, P, x, red, wc);
         };
-        if constexpr (WC == kWcQ8) q8();
+        if constexpr (WC == kWcQ8 || WC == kWcQ8Gemv) q8();
         else if constexpr (WC == kWcHalf) half();
         else if (A.type == PK_TYPE_Q8_0) q8();
         else half();
