@@ -249,7 +249,7 @@ int vec_f32(const pk_tensor &t, int n, const std::vector<int> *map, std::vector<
 struct HostTiled {
     int type = 0, rows = 0, tiles = 0, KB = 0, KBa = 0;
     std::vector<uint8_t> a;   // f32: the hi plane, then the lo plane
-    std::vector<uint16_t> scale;   // q8_0 block scales as stored (f16 bits)
+    std::vector<uint16_t> scale;   // (unused: q8_0 block scales live in the unit records of `a`)
 };
 
 int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *map, HostTiled &out, const char *name) {
@@ -266,23 +266,28 @@ int tile_matrix(const pk_tensor &t, int rows, int cols, const std::vector<int> *
     const size_t frags = (size_t)out.tiles * out.KB;
     const uint8_t *src = static_cast<const uint8_t *>(t.data);
     if (quantized(t.type)) {
+        // unit records (pkdev::TMat): per tile and unit of 5 blocks, lane l's bytes of blocks
+        // 0-1, of blocks 2-3, of block 4, then 16 bytes of block scales per row
         const int bb = block_bytes(t.type);
-        out.a.assign(frags * kWave * 8, 0);
-        out.scale.assign(frags * kTile, 0);
+        const int units = out.KB / pkdev::kQ8Unit;
+        out.a.assign((size_t)out.tiles * units * pkdev::kQ8UnitBytes, 0);
         for (int tile = 0; tile < out.tiles; ++tile)
             for (int r = 0; r < kTile; ++r) {
                 const int row = tile * kTile + r;
                 if (row >= rows) continue;
                 const uint8_t *srow = src + (size_t)(map ? (*map)[row] : row) * out.KBa * bb;
                 for (int kb = 0; kb < out.KBa; ++kb) {
-                    const size_t f = (size_t)tile * out.KB + kb;
+                    const int uc = kb / pkdev::kQ8Unit, j = kb % pkdev::kQ8Unit;
+                    uint8_t *rec = out.a.data() + ((size_t)tile * units + uc) * pkdev::kQ8UnitBytes;
                     uint16_t dh;
                     int8_t q[32];
                     block_q(srow + (size_t)bb * kb, t.type, dh, q);
-                    out.scale[f * kTile + r] = dh;
-                    for (int g = 0; g < 4; ++g)   // lane r + 16 g holds q[8g .. 8g+8) as q ^ 0x80
-                        for (int i = 0; i < 8; ++i)
-                            out.a[(f * kWave + r + 16 * g) * 8 + i] = (uint8_t)q[8 * g + i] ^ 0x80;
+                    memcpy(rec + pkdev::kQ8Scales + r * 16 + j * 2, &dh, 2);
+                    for (int g = 0; g < 4; ++g) {   // lane r + 16 g holds q[8g .. 8g+8) as q ^ 0x80
+                        const int lane = r + 16 * g;
+                        uint8_t *dst = j < 4 ? rec + (j / 2) * 1024 + lane * 16 + (j % 2) * 8 : rec + 2048 + lane * 8;
+                        for (int i = 0; i < 8; ++i) dst[i] = (uint8_t)q[8 * g + i] ^ 0x80;
+                    }
                 }
             }
     } else {
@@ -1349,7 +1354,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
         for (int lc = 0; lc < p.L; ++lc) phases.push_back({lc + 1 < p.L ? &p.w_ih[lc + 1] : &p.w_pred, &p.w_hh[lc]});
         phases.push_back({&p.w_out});
         auto bytes = [&](const pkdev::TMat *m) {
-            return (size_t)((m->tiles + pl.P - 1) / pl.P) * m->KB * pkdev::cache_block_bytes(m->type);
+            return (size_t)((m->tiles + pl.P - 1) / pl.P) * pkdev::tile_bytes(m->type, m->KB);
         };
         size_t off = 0;
         for (auto &ph : phases) {

@@ -43,11 +43,16 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // A weight matrix [rows][K] laid out as MFMA fragments: for row tile t and
 // K block kb (32 columns), lane l holds the 8 consecutive weights of row
-// 16t + l%16 starting at column 32kb + 8(l/16).  q8_0: 8 bytes q ^ 0x80 per
-// lane (the int8 values offset by 128, so the conversion needs no xor) plus
-// the block scales d[16t + r][kb] (the stored f16 bits) at
-// scale[(t*KB + kb)*16 + r]; f16: 8 halves per lane; f32: two f16 planes
-// holding hi = f16(w), lo = f16(w - hi).
+// 16t + l%16 starting at column 32kb + 8(l/16).  f16: 8 halves per lane,
+// [t][kb][lane]; f32: two f16 planes holding hi = f16(w), lo = f16(w - hi).
+// q8_0: 8 bytes q ^ 0x80 per lane and block (the int8 values offset by 128, so
+// the conversion needs no xor), stored per unit of kQ8Unit = 5 blocks as one
+// kQ8UnitBytes record [t][unit]: lane l's 16 bytes of blocks 0-1 (1 KB for the
+// 64 lanes), of blocks 2-3 (1 KB), its 8 bytes of block 4 (512 B), then the
+// block scales (the stored f16 bits), 16 bytes per row r = d[16t + r] of
+// blocks 0-4 and three zeros.  A unit is then 4 wave loads (16 + 16 + 8 bytes
+// of quants, 16 bytes of scales per lane) instead of 10: the products are paced
+// by the number of vector memory instructions per CU, not by bytes.
 //
 // Products are computed transposed: the staged activations are the MFMA A
 // operand (rows = utterances) and the weight fragment the B operand (columns =
@@ -63,10 +68,13 @@ struct TMat {
     int lds_off;                   // byte offset of this workgroup's tiles in its LDS weight cache, -1: not cached
 };
 
-// Bytes of one cached K block: q8_0 fragment (512) + its 16 scales (32); f16
-// fragment; f32 hi then lo fragment.
-__host__ __device__ constexpr int cache_block_bytes(int type) {
-    return type == PK_TYPE_Q8_0 ? 544 : type == PK_TYPE_F16 ? 1024 : 2048;
+constexpr int kQ8Unit = 5, kQ8UnitBytes = 2 * 1024 + 512 + 16 * 16;   // q8_0 unit record (see TMat)
+constexpr int kQ8Scales = 2560;                                        // offset of its scales
+
+// Bytes of one tile row of a matrix (KB stored blocks), as stored and as cached
+// in LDS: q8_0 unit records; f16 fragments; f32 hi then lo fragments.
+__host__ __device__ constexpr int tile_bytes(int type, int KB) {
+    return type == PK_TYPE_Q8_0 ? KB / kQ8Unit * kQ8UnitBytes : type == PK_TYPE_F16 ? KB * 1024 : KB * 2048;
 }
 
 struct KParams {
@@ -698,8 +706,8 @@ template <bool Q8, bool CACHED>
 __device__ __forceinline__ MatSrc mat_src(const TMat &m, bool two, const unsigned char *wc) {
     MatSrc s;
     if (Q8) {
-        s.r0 = rsrc(m.a, (unsigned)m.tiles * m.KB * kWave * 8u);
-        s.r1 = rsrc(m.scale, (unsigned)m.tiles * m.KB * kTile * 2u);
+        s.r0 = rsrc(m.a, (unsigned)m.tiles * (unsigned)tile_bytes(PK_TYPE_Q8_0, m.KB));
+        s.r1 = s.r0;
     } else {   // f32: both planes under one descriptor (the lo plane follows the hi plane)
         const unsigned bytes = (unsigned)m.tiles * m.KB * kWave * 16u;
         s.r0 = rsrc(m.a, two ? 2 * bytes : bytes);
@@ -712,27 +720,47 @@ __device__ __forceinline__ MatSrc mat_src(const TMat &m, bool two, const unsigne
 }
 
 // Fragments of one unit, blocks sb0 .. sb0+kUnitOf-1 of tile `tile` (local index
-// li in the LDS cache).  FULL: all kUnitOf blocks exist (K is a whole number of
-// units), so every offset is a lane constant plus a wave-uniform base plus an
-// immediate.  Otherwise blocks past nb read as zero (buffer loads past the
-// range return 0; cached blocks are zeroed).  Matrices are stored in whole
-// units, so only FULL is instantiated; the masked form stays because taking it
-// out changes the q8_0 loop's register assignment, which measured 0.5 % slower.
+// li in the LDS cache).  q8_0: the unit's record, four loads.  f16 / f32: FULL,
+// all kUnitOf blocks exist (K is a whole number of units), so every offset is a
+// lane constant plus a wave-uniform base plus an immediate; otherwise blocks
+// past nb read as zero (buffer loads past the range return 0; cached blocks are
+// zeroed).  Matrices are stored in whole units, so only FULL is instantiated.
 template <bool Q8, bool CACHED, bool FULL>
 __device__ __forceinline__ void unit_load_src(const MatSrc &m, bool two, int tile, int li, int sb0, int nb, int lane,
                                               uint4 (&f)[kUnitOf<Q8>]) {
+    if constexpr (Q8) {   // one unit record (matrices are stored in whole units: every block exists)
+        static_assert(kUnitOf<Q8> == kQ8Unit, "q8_0 units are the stored records");
+        const int uc = sb0 / kQ8Unit;
+        uint4 qa, qb, sc;
+        uint2 qc;
+        if (CACHED) {
+            const unsigned char *rec = m.lds + ((size_t)li * (m.KB / kQ8Unit) + uc) * kQ8UnitBytes;
+            qa = *reinterpret_cast<const uint4 *>(rec + lane * 16);
+            qb = *reinterpret_cast<const uint4 *>(rec + 1024 + lane * 16);
+            qc = *reinterpret_cast<const uint2 *>(rec + 2048 + lane * 8);
+            sc = *reinterpret_cast<const uint4 *>(rec + kQ8Scales + (lane & 15) * 16);
+        } else {
+            const int rec = (tile * (m.KB / kQ8Unit) + uc) * kQ8UnitBytes;   // wave-uniform
+            qa = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(m.r0, lane * 16, rec, 0));
+            qb = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(m.r0, lane * 16 + 1024, rec, 0));
+            qc = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(m.r0, lane * 8 + 2048, rec, 0));
+            sc = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(m.r0, (lane & 15) * 16 + kQ8Scales,
+                                                                                 rec, 0));
+        }
+        f[0] = make_uint4(qa.x, qa.y, sc.x & 0xffffu, 0u);
+        f[1] = make_uint4(qa.z, qa.w, sc.x >> 16, 0u);
+        f[2] = make_uint4(qb.x, qb.y, sc.y & 0xffffu, 0u);
+        f[3] = make_uint4(qb.z, qb.w, sc.y >> 16, 0u);
+        f[4] = make_uint4(qc.x, qc.y, sc.z & 0xffffu, 0u);
+        return;
+    }
     if (CACHED) {
 #pragma unroll
         for (int j = 0; j < kUnitOf<Q8>; ++j) {
             const bool ok = FULL || j < nb;
             const int sb = ok ? sb0 + j : sb0;
             uint4 v;
-            if (Q8) {
-                const unsigned char *blk = m.lds + ((size_t)li * m.KB + sb) * 544;
-                const uint2 q = *reinterpret_cast<const uint2 *>(blk + lane * 8);
-                const unsigned d = *reinterpret_cast<const unsigned short *>(blk + 512 + (lane & 15) * 2);
-                v = make_uint4(q.x, q.y, d, 0u);
-            } else {
+            {
                 const int kb = two ? sb >> 1 : sb;
                 const int plane = two ? (sb & 1) : 0;
                 v = *reinterpret_cast<const uint4 *>(m.lds + (((size_t)li * m.KB + kb) * (two ? 2 : 1) + plane) * 1024 +
@@ -742,25 +770,7 @@ __device__ __forceinline__ void unit_load_src(const MatSrc &m, bool two, int til
         }
         return;
     }
-    if (Q8) {
-        const int f0 = tile * m.KB + sb0;   // wave-uniform fragment index of block sb0
-#pragma unroll
-        for (int j = 0; j < kUnitOf<Q8>; ++j) {
-            uint2 q;
-            unsigned d;
-            if (FULL) {
-                q = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(m.r0, lane * 8 + j * 512, f0 * 512, 0));
-                d = __builtin_amdgcn_raw_buffer_load_b16(m.r1, (lane & 15) * 2 + j * 32, f0 * 32, 0);
-            } else {
-                const bool ok = j < nb;
-                const unsigned oq = ok ? (unsigned)((f0 + j) * kWave + lane) * 8u : kBad;
-                const unsigned os = ok ? (unsigned)((f0 + j) * kTile + (lane & 15)) * 2u : kBad;
-                q = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(m.r0, oq, 0, 0));
-                d = __builtin_amdgcn_raw_buffer_load_b16(m.r1, os, 0, 0);
-            }
-            f[j] = make_uint4(q.x, q.y, d, 0u);
-        }
-    } else {
+    {
 #pragma unroll
         for (int j = 0; j < kUnitOf<Q8>; ++j) {
             const int sb = sb0 + j;
@@ -1096,21 +1106,21 @@ __device__ __forceinline__ void bias_table(const KParams &p, int rank, int P, fl
 // per K block the fragment, then (q8_0) the 16 block scales.  kCacheB 16-byte
 // chunks per thread are loaded before any is stored.
 constexpr int kCacheB = 8;
+// 16-byte chunk c of this workgroup's cached image of m: its tiles in order,
+// each as stored (q8_0 unit records, f16 fragments; f32: per K block the hi
+// then the lo fragment).
 __device__ __forceinline__ const unsigned char *cache_src(const TMat &m, int rank, int P, int chunks, int c) {
-    const int ch = c % chunks, blk = c / chunks;      // blk = local tile * KB + kb
-    const int li = blk / m.KB, kb = blk % m.KB;
-    const size_t f = (size_t)(rank + li * P) * m.KB + kb;   // global fragment index
-    if (m.type == PK_TYPE_Q8_0)
-        return ch < 32 ? static_cast<const unsigned char *>(m.a) + f * 512 + ch * 16
-                       : reinterpret_cast<const unsigned char *>(m.scale) + f * 32 + (ch - 32) * 16;
-    if (m.type == PK_TYPE_F16) return static_cast<const unsigned char *>(m.a) + f * 1024 + ch * 16;
-    return static_cast<const unsigned char *>(ch < 64 ? m.a : m.a_lo) + f * 1024 + (ch % 64) * 16;
+    const int ch = c % chunks, li = c / chunks;   // chunks: of one tile
+    const size_t t = (size_t)(rank + li * P);      // global tile
+    if (m.type != PK_TYPE_F32) return static_cast<const unsigned char *>(m.a) + t * (size_t)chunks * 16 + ch * 16;
+    const int kb = ch / 128, part = ch % 128;      // f32: 128 chunks per block (64 hi, 64 lo)
+    return static_cast<const unsigned char *>(part < 64 ? m.a : m.a_lo) + (t * m.KB + kb) * 1024 + (part % 64) * 16;
 }
 __device__ __forceinline__ void cache_matrix(const TMat &m, int rank, int P, unsigned char *wc) {
     if (m.lds_off < 0) return;
     const int n = owned(m.tiles, rank, P);
-    const int bpb = cache_block_bytes(m.type), chunks = bpb / 16;
-    const int nchunk = n * m.KB * chunks;
+    const int chunks = tile_bytes(m.type, m.KB) / 16;
+    const int nchunk = n * chunks;
     if (nchunk == 0) return;
     for (int base = 0; base < nchunk; base += kCacheB * kBlock) {
         uint4 v[kCacheB];
@@ -1120,8 +1130,7 @@ __device__ __forceinline__ void cache_matrix(const TMat &m, int rank, int P, uns
 #pragma unroll
         for (int j = 0; j < kCacheB; ++j) {
             const int c = base + threadIdx.x + j * kBlock;
-            if (c < nchunk)   // local offset: (local tile * KB + kb) * bpb + chunk * 16
-                *reinterpret_cast<uint4 *>(wc + m.lds_off + (size_t)(c / chunks) * bpb + (c % chunks) * 16) = v[j];
+            if (c < nchunk) *reinterpret_cast<uint4 *>(wc + m.lds_off + (size_t)c * 16) = v[j];
         }
     }
 }
