@@ -200,7 +200,8 @@ PK_API int pk_window_split(int32_t n_utts, const int32_t *n_frames, int32_t max_
  * overlap in time on the same device race. */
 PK_API int pk_decode_noalloc(pk_decoder *dec, const pk_batch *batch);
 /* Time, with HIP events on the handle's stream, the last pk_decode's
- * kernels: enc_proj GEMM and the decode loop (milliseconds). */
+ * kernels: enc_proj GEMM and the decode loop (milliseconds), and its lockstep
+ * iterations; summed over the launches of a call decoded in several. */
 PK_API int pk_last_timing(pk_decoder *dec, float *enc_proj_ms, float *loop_ms, int32_t *iterations);
 /* Message of the last failure on this thread ("" if none). */
 PK_API const char *pk_last_error(void);

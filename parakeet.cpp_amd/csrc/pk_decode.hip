@@ -382,6 +382,11 @@ struct pk_decoder {
     HostBuf h_frames;          // staging of host-memory frames (up to kPinnedFrames bytes)
     unsigned char *scratch = nullptr;   // this device's fixed scratch array (pk_decode_noalloc)
     int last_iters = 0;
+    // a call decoded in several launches (decode_chained): the kernels' times and the
+    // lockstep iterations summed over its launches, which pk_last_timing then reports
+    bool chained = false;
+    float chain_ep_ms = 0.f, chain_loop_ms = 0.f;
+    int chain_iters = 0;
     int lock_fd = -1;          // this GPU's cross-process loop lock (see DeviceLoopLock), -1: none
     const void *loop_fn[2] = {};   // the decode-loop instantiations for this decoder's weight storage:
                                    // several domains, one domain (argmax key slots)
@@ -856,6 +861,12 @@ PK_API int pk_slot_copy(pk_decoder *dec, int32_t src, int32_t dst) {
 
 PK_API int pk_last_timing(pk_decoder *dec, float *enc_proj_ms, float *loop_ms, int32_t *iterations) {
     if (!dec) return fail(PK_ERR_ARG, "pk_last_timing: null");
+    if (dec->chained) {
+        if (enc_proj_ms) *enc_proj_ms = dec->chain_ep_ms;
+        if (loop_ms) *loop_ms = dec->chain_loop_ms;
+        if (iterations) *iterations = dec->chain_iters;
+        return 0;
+    }
     float a = 0, b = 0;
     HIP_TRY(hipEventElapsedTime(&a, dec->ev[0], dec->ev[1]));
     HIP_TRY(hipEventElapsedTime(&b, dec->ev[1], dec->ev[2]));
@@ -1047,6 +1058,7 @@ int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds) {
 
 int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratch cs) {
     if (!dec || !bt) return fail(PK_ERR_ARG, "pk_decode: null argument");
+    dec->chained = false;   // (decode_chained sets it again after its last launch)
     KParams &p = dec->kp;
     if (bt->d_enc != dec->desc.d_enc)
         return fail(PK_ERR_D_ENC, "encoder d_model mismatch (%d vs %d)", bt->d_enc, dec->desc.d_enc);
@@ -1526,6 +1538,8 @@ int decode_chained(pk_decoder *dec, const pk_batch *bt, int W, const std::vector
     }
     std::vector<long long> done(n, 0);                 // frames decoded so far
     std::vector<int32_t> ntok(n, 0), nseg(n, 0), nst(n, 0);
+    float ep_ms = 0.f, loop_ms = 0.f;
+    int iters = 0;
     const int n_launch = *std::max_element(launches.begin(), launches.end());
     for (int j = 0; j < n_launch; ++j) {
         // the utterances with a piece j (launch 0: all, so windows with no frames are handled as usual)
@@ -1580,6 +1594,10 @@ int decode_chained(pk_decoder *dec, const pk_batch *bt, int W, const std::vector
         b.ctrl_out = ctrl.data();
         const int rc = decode_impl(dec, &b, false);
         if (rc != 0 && rc != PK_ERR_OVERFLOW) return rc;   // capacity is judged on the totals below
+        float a = 0.f, c = 0.f;
+        if (hipEventElapsedTime(&a, dec->ev[0], dec->ev[1]) == hipSuccess) ep_ms += a;
+        if (hipEventElapsedTime(&c, dec->ev[1], dec->ev[2]) == hipSuccess) loop_ms += c;
+        iters += dec->last_iters;
         for (int i = 0; i < m; ++i) {
             const int u = idx[i];
             const int nt = std::min(cnt[i], cap), keep_t = std::max(0, std::min(nt, tcap - ntok[u]));
@@ -1618,6 +1636,10 @@ int decode_chained(pk_decoder *dec, const pk_batch *bt, int W, const std::vector
         memcpy(bt->steps, nst.data(), 4 * (size_t)n);
         if (bt->n_segments) memcpy(bt->n_segments, nseg.data(), 4 * (size_t)n);
     }
+    dec->chained = true;
+    dec->chain_ep_ms = ep_ms;
+    dec->chain_loop_ms = loop_ms;
+    dec->chain_iters = iters;
     if (over) return fail(PK_ERR_OVERFLOW, "token or segment capacity exceeded");
     return 0;
 }

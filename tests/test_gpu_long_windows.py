@@ -133,3 +133,58 @@ def test_tdt06b_b1_30000_frames(tmp_path):
     ost = om.new_state()
     s = check_window(om, dev, 2, enc[:n0], q, ost, 10)
     print(f"  {r['steps']} steps; replayed the first {q['steps']}, near-ties {s['near_ties']}", flush=True)
+
+
+def _alone_equal(dev, encs, res, base, **kw):
+    for u, e in enumerate(encs):
+        a = dev.decode([e], slots=[base + u], trace=True, **{k: (v[u:u + 1] if hasattr(v, "__len__") else v)
+                                                             for k, v in kw.items()})[0]
+        assert np.array_equal(a["trace"], res[u]["trace"]), u
+        assert a["tokens"].tolist() == res[u]["tokens"].tolist(), u
+        assert a["segments"].tolist() == res[u]["segments"].tolist(), u
+        x, y = dev.read_state(u), dev.read_state(base + u)
+        assert np.array_equal(x["h"], y["h"]) and np.array_equal(x["c"], y["c"]), u
+        assert x["ctrl"].tolist() == y["ctrl"].tolist(), u
+
+
+def test_ragged_batch_equals_alone(tmp_path):
+    """A ragged batch (T ~ U{20..400}, per-utterance blank bias): every utterance
+    equals its decode alone, bit for bit (decisions, tokens, final state and
+    control words), and the longest and shortest replay through the oracle."""
+    from parakeet_amd import gguf, pk, synth
+    import oracle
+    path = str(tmp_path / "t.gguf")
+    small_tdt(path)
+    B = 40
+    dev = pk.Decoder.from_gguf(path, n_slots=2 * B)
+    om = oracle.OracleModel.from_gguf(path, gguf)
+    rng = np.random.default_rng(17)
+    Ts = rng.integers(20, 401, size=B)
+    encs = [synth.encoder_frames(80 + u, int(Ts[u]), 128) for u in range(B)]
+    bb = np.array([0.0, 2.0, 4.0] * 14, np.float32)[:B]
+    print(f"ragged batch: B={B}, T in [{Ts.min()}, {Ts.max()}]", flush=True)
+    res = dev.decode(encs, slots=list(range(B)), trace=True, blank_bias=bb)
+    _alone_equal(dev, encs, res, B, blank_bias=bb)
+    for u in (int(np.argmax(Ts)), int(np.argmin(Ts))):
+        check_window(om, dev, u, encs[u], res[u], om.new_state(), 10, blank_bias=float(bb[u]))
+
+
+def test_ragged_eou_equals_alone(tmp_path):
+    """EOU ragged batch with per-utterance token bases: segments, tokens, state and
+    control words equal each utterance decoded alone."""
+    from parakeet_amd import pk, synth
+    path = str(tmp_path / "e.gguf")
+    w = small_eou(path)
+    bias = w["eou.joint.out.bias"].copy()
+    bias[33] += 1.5
+    small_eou(path, overrides={"eou.joint.out.bias": bias})
+    B = 36
+    dev = pk.Decoder.from_gguf(path, n_slots=2 * B)
+    rng = np.random.default_rng(18)
+    Ts = rng.integers(10, 300, size=B)
+    encs = [synth.encoder_frames(120 + u, int(Ts[u]), 64) for u in range(B)]
+    base = rng.integers(0, 50, size=B).astype(np.int32)
+    print(f"ragged EOU batch: B={B}", flush=True)
+    res = dev.decode(encs, slots=list(range(B)), trace=True, max_symbols=5, tokens_base=base)
+    _alone_equal(dev, encs, res, B, max_symbols=5, tokens_base=base)
+    assert sum(len(r["segments"]) for r in res) > 0
