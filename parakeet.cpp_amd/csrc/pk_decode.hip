@@ -7,7 +7,9 @@
 //   enc_proj_kernel     b_e + W_e . enc[t] for every frame of every utterance,
 //                       once per window (src/parakeet_tdt.cpp:433-483 computes
 //                       the same projection as a ggml graph; the CPU path
-//                       recomputes it per step at :167-168).
+//                       recomputes it per step at :167-168).  At most
+//                       kNarrowRows rows: enc_proj_narrow_kernel instead
+//                       (bit-identical outputs).
 //   decode_loop_kernel  all lockstep iterations of all utterances in one
 //                       launch (cooperative where the runtime grants it;
 //                       see launch_loop).  The batch is split into
@@ -78,6 +80,9 @@ constexpr size_t kEagerCopyBytes = 256 << 10;
 constexpr size_t kPinnedFrames = 64ull << 20;
 // windows shorter than this many frames do not fill the LDS weight cache
 constexpr int kCacheMinFrames = 16;
+// enc_proj over at most this many rows runs the narrow kernel (one wave per 16x16 block;
+// measured faster up to 256 rows, slower from 750 on)
+constexpr long long kNarrowRows = 256;
 
 thread_local std::string g_err;
 // set by an atexit handler: process teardown has begun
@@ -1221,11 +1226,23 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     float *d_encp = nullptr;
     if (rows > 0) {
         if ((rc = cs.get(dec->d_encp, (size_t)rows * J * 4, reinterpret_cast<void **>(&d_encp)))) return rc;
-        // tiles over the packed rows of all utterances; the kernel also clears the loop's words
-        dim3 grid((unsigned)((rows + pkdev::kEpTile - 1) / pkdev::kEpTile), 1, (J + pkdev::kEpTile - 1) / pkdev::kEpTile);
-        pkdev::enc_proj_kernel<<<grid, 256, 0, dec->stream>>>(dec->w_enc_hi, dec->w_enc_lo, J, dec->b_enc, enc, D,
-                                                              d_src, d_dst, m, rows, d_encp,
-                                                              static_cast<unsigned *>(d_clear), clear_words);
+        // tiles over the packed rows of all utterances; the kernel also clears the loop's words.
+        // Both kernels give bit-identical rows (PK_ENC_PROJ=tile / narrow forces one).
+        const char *ep_env = std::getenv("PK_ENC_PROJ");
+        const bool narrow = ep_env ? ep_env[0] == 'n' : rows <= kNarrowRows;
+        if (narrow) {
+            dim3 grid((unsigned)((rows + 15) / 16), 1, (J + 63) / 64);
+            pkdev::enc_proj_narrow_kernel<<<grid, 256, 0, dec->stream>>>(dec->w_enc_hi, dec->w_enc_lo, J, dec->b_enc,
+                                                                         enc, D, d_src, d_dst, m, rows, d_encp,
+                                                                         static_cast<unsigned *>(d_clear),
+                                                                         clear_words);
+        } else {
+            dim3 grid((unsigned)((rows + pkdev::kEpTile - 1) / pkdev::kEpTile), 1,
+                      (J + pkdev::kEpTile - 1) / pkdev::kEpTile);
+            pkdev::enc_proj_kernel<<<grid, 256, 0, dec->stream>>>(dec->w_enc_hi, dec->w_enc_lo, J, dec->b_enc, enc,
+                                                                  D, d_src, d_dst, m, rows, d_encp,
+                                                                  static_cast<unsigned *>(d_clear), clear_words);
+        }
         HIP_TRY(hipGetLastError());
     } else {
         pkdev::fill_zero_kernel<<<(unsigned)std::min<size_t>((clear_words + 255) / 256, 1024), 256, 0, dec->stream>>>(

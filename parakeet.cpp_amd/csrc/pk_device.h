@@ -437,6 +437,111 @@ __global__ void __launch_bounds__(256) enc_proj_kernel(const _Float16 *__restric
     }
 }
 
+// enc_proj for few rows (streaming chunks, short windows).  There the tiled
+// kernel above runs on a few dozen workgroups, each paying two workgroup
+// barriers and an LDS round trip per K step.  Here each wave owns one 16x16
+// output block and loads its operands straight into MFMA fragment registers,
+// kEnSteps K steps per batch, the next batch in flight while the current one is
+// multiplied: no LDS and no barrier.  Each block takes exactly the
+// instructions of enc_proj_kernel, in the same order: per K step of 32 the same
+// lane layout (row lane % 16, K slice 8 (lane / 16)), the same f16 hi / lo split
+// of the frames, hi.hi + lo.hi + hi.lo into one accumulator in K order, then +
+// bias.  So the two kernels' outputs are bit-identical, and the host chooses
+// between them by row count alone.  Workgroup: 4 waves, 16 rows x 64 outputs.
+constexpr int kEnSteps = 4;   // K steps per batch of the narrow kernel
+__global__ void __launch_bounds__(256) enc_proj_narrow_kernel(const _Float16 *__restrict whi,
+                                                              const _Float16 *__restrict wlo, int J,
+                                                              const float *__restrict bias,
+                                                              const float *__restrict enc, int d_enc,
+                                                              const long long *__restrict src_row,
+                                                              const long long *__restrict dst_row, int n_utts,
+                                                              long long rows, float *__restrict out,
+                                                              unsigned *__restrict clear, size_t clear_words) {
+    {
+        const size_t nthreads = (size_t)gridDim.x * gridDim.z * 256;
+        const size_t gtid = ((size_t)blockIdx.z * gridDim.x + blockIdx.x) * 256 + threadIdx.x;
+        for (size_t i = gtid; i < clear_words; i += nthreads) clear[i] = 0u;
+    }
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const long long m0 = (long long)blockIdx.x * 16;
+    const int n0 = (blockIdx.z * 4 + wave) * 16;
+    if (n0 >= J) return;
+    const long long r = m0 + (lane & 15);
+    const bool live = r < rows;
+    const float *src = enc;
+    if (live) {
+        int lo = 0, hi = n_utts - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (dst_row[mid] <= r) lo = mid;
+            else hi = mid - 1;
+        }
+        src = enc + (size_t)(src_row[lo] + (r - dst_row[lo])) * d_enc;
+    }
+    const int col = n0 + (lane & 15);
+    const bool cl = col < J;
+    const int ks = (lane >> 4) * 8;
+    const int nsteps = d_enc / kEpK, nb = (nsteps + kEnSteps - 1) / kEnSteps;
+    // Every lane loads: a row past the last reads frame row 0 and a column past J reads
+    // W_e row J - 1.  Row i of an MFMA product depends only on row i of A, and column j
+    // only on column j of B, so those lanes' values reach only outputs never stored.
+    const _Float16 *bhp = whi + (size_t)(cl ? col : J - 1) * d_enc + ks;
+    const _Float16 *blp = wlo + (size_t)(cl ? col : J - 1) * d_enc + ks;
+    src += ks;
+    struct Batch {
+        float4 a0[kEnSteps], a1[kEnSteps];
+        half8 bh[kEnSteps], bl[kEnSteps];
+    };
+    // batch b's operands (a batch past the last reloads the last one, so no load sits
+    // behind a branch and the compiler's wait counts stay exact)
+    auto load = [&](int b, Batch &x) {
+        b = b < nb ? b : nb - 1;
+#pragma unroll
+        for (int s = 0; s < kEnSteps; ++s) {
+            int st = b * kEnSteps + s;
+            st = st < nsteps ? st : nsteps - 1;
+            const int k = st * kEpK;
+            x.a0[s] = *reinterpret_cast<const float4 *>(src + k);
+            x.a1[s] = *reinterpret_cast<const float4 *>(src + k + 4);
+            x.bh[s] = *reinterpret_cast<const half8 *>(bhp + k);
+            x.bl[s] = *reinterpret_cast<const half8 *>(blp + k);
+        }
+    };
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto mul = [&](int b, const Batch &x) {
+#pragma unroll
+        for (int s = 0; s < kEnSteps; ++s) {
+            if (b * kEnSteps + s >= nsteps) break;
+            const float v[8] = {x.a0[s].x, x.a0[s].y, x.a0[s].z, x.a0[s].w,
+                                x.a1[s].x, x.a1[s].y, x.a1[s].z, x.a1[s].w};
+            half8 h, l;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                h[i] = (_Float16)v[i];
+                l[i] = (_Float16)(v[i] - (float)h[i]);
+            }
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, x.bh[s], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(l, x.bh[s], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(h, x.bl[s], acc, 0, 0, 0);
+        }
+    };
+    Batch X, Y;
+    load(0, X);
+    for (int b = 0; b < nb; b += 2) {
+        load(b + 1, Y);
+        mul(b, X);
+        load(b + 2, X);
+        if (b + 1 < nb) mul(b + 1, Y);
+    }
+    if (!cl) return;
+    const float bc = bias[col];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const long long row = m0 + (lane >> 4) * 4 + i;
+        if (row < rows) out[(size_t)row * J + col] = acc[i] + bc;
+    }
+}
+
 // ---------------------------------------------------------------- decode loop
 
 struct Ctl {                      // per-workgroup copy of its domain's control state
