@@ -88,7 +88,8 @@ def traffic_passes(args) -> tuple[list[str] | None, str | None]:
     if any(k.startswith("ROCPROF") for k in os.environ) or "rocprof" in os.environ.get("LD_PRELOAD", ""):
         return None, "already running under a profiler"
     out = tempfile.mkdtemp(prefix="pk_traffic_", dir="/tmp")
-    env = dict(os.environ, PK_LOOP_DISPATCH="1", TMPDIR="/tmp")
+    # (under the profiler the library launches the loop as an ordinary dispatch by itself)
+    env = dict(os.environ, TMPDIR="/tmp")
     csvs = []
     for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
         d = os.path.join(out, ctr)

@@ -1407,30 +1407,37 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     int *status = dec->h_pin.as<int>();   // read after the stream synchronisation below
     HIP_TRY(hipMemcpyAsync(status, p.status, 4 * sizeof(int), hipMemcpyDeviceToHost, dec->stream));
     if (host) {
-        // the counters of every utterance in one copy (n_tokens, steps, n_segments are
-        // consecutive), into pinned memory.  Small outputs (every row whole, up to
-        // kEagerCopyBytes) and the control words follow at once, so the call waits for the
-        // stream once; larger ones copy only each row's filled prefix after the counters.
-        std::vector<int> cnt_v;
-        int *cnt;
-        if (dec->pin_cnt + 12 * (size_t)m <= dec->h_pin.n) {   // (m <= n_slots: slots are distinct)
-            cnt = reinterpret_cast<int *>(dec->h_pin.as<uint8_t>() + dec->pin_cnt);
-        } else {
-            cnt_v.resize(3 * (size_t)m);
-            cnt = cnt_v.data();
-        }
-        HIP_TRY(hipMemcpyAsync(cnt, o_ntok, 12 * (size_t)m, hipMemcpyDeviceToHost, dec->stream));
-        const size_t tb = (size_t)m * tcap * 4, sb = bt->segments ? (size_t)m * scap * 4 : 0,
+        // The device staging is one block: tokens | n_tokens, steps, n_segments | segments |
+        // trace | control words.  Up to kEagerCopyBytes of rows it comes back whole in one
+        // copy, so the call waits for the stream once.  Larger outputs copy the counters and
+        // control words first, then only each row's filled prefix.
+        const size_t tb = (size_t)m * tcap * 4, sb_all = (size_t)m * scap * 4,
                      rb = o_trace ? (size_t)m * trcap * 8 : 0, cb = o_ctrl ? (size_t)m * PK_CTRL_N * 4 : 0;
-        const bool eager = tb + sb + rb <= kEagerCopyBytes;
-        if ((rc = dec->h_out.ensure(std::max<size_t>(cb + (eager ? tb + sb + rb : 0), 64)))) return rc;
-        int32_t *s_ctrl = dec->h_out.as<int32_t>();
-        int *e_tok = s_ctrl + cb / 4, *e_seg = e_tok + tb / 4, *e_tr = e_seg + sb / 4;
-        if (cb) HIP_TRY(hipMemcpyAsync(s_ctrl, o_ctrl, cb, hipMemcpyDeviceToHost, dec->stream));
+        const bool eager = tb + sb_all + rb <= kEagerCopyBytes;
+        std::vector<int> cnt_v;
+        int *cnt, *e_tok, *e_seg, *e_tr;
+        int32_t *s_ctrl;
         if (eager) {
-            if (tb) HIP_TRY(hipMemcpyAsync(e_tok, o_tok, tb, hipMemcpyDeviceToHost, dec->stream));
-            if (sb) HIP_TRY(hipMemcpyAsync(e_seg, o_seg, sb, hipMemcpyDeviceToHost, dec->stream));
-            if (rb) HIP_TRY(hipMemcpyAsync(e_tr, o_trace, rb, hipMemcpyDeviceToHost, dec->stream));
+            const size_t whole = tb + 12 * (size_t)m + sb_all + rb + cb;
+            if ((rc = dec->h_out.ensure(std::max<size_t>(whole, 64)))) return rc;
+            HIP_TRY(hipMemcpyAsync(dec->h_out.p, o_tok, whole, hipMemcpyDeviceToHost, dec->stream));
+            e_tok = dec->h_out.as<int>();
+            cnt = e_tok + tb / 4;
+            e_seg = cnt + 3 * (size_t)m;
+            e_tr = e_seg + sb_all / 4;
+            s_ctrl = e_tr + rb / 4;
+        } else {
+            if (dec->pin_cnt + 12 * (size_t)m <= dec->h_pin.n) {   // (m <= n_slots: slots are distinct)
+                cnt = reinterpret_cast<int *>(dec->h_pin.as<uint8_t>() + dec->pin_cnt);
+            } else {
+                cnt_v.resize(3 * (size_t)m);
+                cnt = cnt_v.data();
+            }
+            HIP_TRY(hipMemcpyAsync(cnt, o_ntok, 12 * (size_t)m, hipMemcpyDeviceToHost, dec->stream));
+            if ((rc = dec->h_out.ensure(std::max<size_t>(cb, 64)))) return rc;
+            s_ctrl = dec->h_out.as<int32_t>();
+            if (cb) HIP_TRY(hipMemcpyAsync(s_ctrl, o_ctrl, cb, hipMemcpyDeviceToHost, dec->stream));
+            e_tok = e_seg = e_tr = nullptr;
         }
         HIP_TRY(hipStreamSynchronize(dec->stream));
         const int *c_tok = cnt, *c_steps = c_tok + m, *c_seg = c_steps + m;
