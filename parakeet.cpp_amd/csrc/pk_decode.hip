@@ -1012,6 +1012,7 @@ struct LoopOrder {
     std::mutex mu;
     std::map<int, hipEvent_t> last;       // per device: recorded after the latest loop launch
     std::map<int, bool> coop_refused;     // per device: cooperative launches refused once
+    std::map<int, bool> coop_needed;      // per device: an ordinary dispatch was once not co-resident
 };
 LoopOrder g_loops;
 
@@ -1022,7 +1023,22 @@ LoopOrder g_loops;
 // no other loop running the grid fits, and the ordering above keeps this
 // process's loops apart.  If a loop of another process overlaps it, the
 // barrier's 2 s limit ends both launches with PK_ERR_TIMEOUT.
-int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds) {
+// Arrival limit of an ordinary dispatch's co-residency check (kernel start to the whole grid
+// arrived): a grid that has not arrived by then is relaunched cooperatively.
+constexpr unsigned kArriveLimitUs = 100;
+
+// The loop launch.  By default an ordinary dispatch whose workgroups first check that the
+// whole grid is resident (pkdev::coresident): a cooperative launch costs about 14 us more per
+// call, and under rocprofv3 (ROCm 7.2) any process that made one ends with SIGSEGV in the HIP
+// runtime's exit-time teardown.  A grid found not resident ends at once with
+// kStatusNotResident and the call is relaunched with coop = true (decode_impl); the device
+// then launches cooperatively from there on.  Where the runtime refuses a cooperative launch
+// (another process holds the device's cooperative queue), the loop runs as an ordinary
+// dispatch without the check, and its barriers' 2 s limit is the last guard.
+// PK_LOOP_DISPATCH=0 makes every launch cooperative, =1 every launch an ordinary dispatch;
+// PK_ARRIVE_US sets the arrival limit for tests of the relaunch: the first launch of a call is
+// then an ordinary dispatch whatever the device's history, and nothing is remembered.
+int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds, bool coop) {
     std::lock_guard<std::mutex> lk(g_loops.mu);
     hipEvent_t &last = g_loops.last[dec->device];
     if (!last) HIP_TRY(hipEventCreateWithFlags(&last, hipEventDisableTiming));
@@ -1030,23 +1046,15 @@ int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds) {
     void *args[] = {&p};
     const void *fn = dec->loop_fn[p.slots ? 1 : 0];   // one domain: the argmax-slot instantiation
     bool &refused = g_loops.coop_refused[dec->device];
-    // PK_LOOP_DISPATCH=1: ordinary dispatch from the first launch on.  For
-    // profiler runs: rocprofv3 (ROCm 7.2) ends with SIGSEGV in the HIP
-    // runtime's exit-time teardown of any process that made a cooperative
-    // launch, a one-kernel program included; the kernel is the same either way.
-    // Without PK_LOOP_DISPATCH the ordinary dispatch is also chosen when the process runs
-    // under rocprofv3 (its ROCPROF* environment, or its tool library preloaded), so the
-    // default path profiles and exits cleanly; PK_LOOP_DISPATCH=0 keeps the cooperative launch.
-    static const bool force_dispatch = [] {
+    static const int mode = [] {   // 0: cooperative, 1: ordinary dispatch, -1: default
         const char *v = std::getenv("PK_LOOP_DISPATCH");
-        if (v && v[0]) return v[0] == '1';
-        const char *pre = std::getenv("LD_PRELOAD");
-        if (pre && strstr(pre, "rocprof")) return true;
-        for (char **e = environ; e && *e; ++e)
-            if (strncmp(*e, "ROCPROF", 7) == 0) return true;
-        return false;
+        return v && v[0] ? (v[0] == '1' ? 1 : 0) : -1;
     }();
-    if (!refused && !force_dispatch) {
+    const char *lim = std::getenv("PK_ARRIVE_US");   // a test setting of the arrival limit
+    const bool cooperative =
+        mode == 0 || (mode == -1 && (coop || (!(lim && lim[0]) && g_loops.coop_needed[dec->device])));
+    if (cooperative && !refused) {
+        p.arrive_ticks = 0u;
         const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(nwg), dim3(kBlock), args, lds, dec->stream);
         if (e != hipErrorIllegalState) {
             HIP_TRY(e);
@@ -1056,8 +1064,27 @@ int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds) {
         (void)hipGetLastError();
         refused = true;
     }
+    const unsigned limit_us = lim && lim[0] ? (unsigned)std::min(std::max(0, atoi(lim)), 1000000) : kArriveLimitUs;
+    // 100 MHz clock; a refused cooperative relaunch runs without the check
+    p.arrive_ticks = cooperative ? 0u : std::max(1u, limit_us * 100u);
     HIP_TRY(hipLaunchKernel(fn, dim3(nwg), dim3(kBlock), args, lds, dec->stream));
     HIP_TRY(hipEventRecord(last, dec->stream));
+    return 0;
+}
+
+// A launch found not co-resident (kStatusNotResident): clear its status words and
+// remember, unless the arrival limit is a test setting, that this device launches
+// cooperatively.
+int after_not_resident(pk_decoder *dec, int *d_status) {
+    pkdev::fill_zero_kernel<<<1, 256, 0, dec->stream>>>(reinterpret_cast<unsigned *>(d_status), 16);
+    HIP_TRY(hipGetLastError());
+    if (!std::getenv("PK_ARRIVE_US")) {
+        std::lock_guard<std::mutex> lk(g_loops.mu);
+        g_loops.coop_needed[dec->device] = true;
+    }
+    static std::atomic<bool> noted{false};
+    if (!noted.exchange(true) || std::getenv("PK_ARRIVE_US"))
+        fprintf(stderr, "[parakeet_hip] decode loop grid not co-resident: relaunched cooperatively\n");
     return 0;
 }
 
@@ -1402,7 +1429,9 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     // process's decode loop on this GPU waits here instead of sharing the CUs
     DeviceLoopLock cross_process(dec->lock_fd);
     if ((rc = cross_process.acquire())) return rc;
-    if ((rc = launch_loop(dec, nwg, p, lds))) return rc;
+    bool coop_retry = false;   // set when an ordinary dispatch found its grid not co-resident
+relaunch:
+    if ((rc = launch_loop(dec, nwg, p, lds, coop_retry))) return rc;
     HIP_TRY(hipEventRecord(dec->ev[2], dec->stream));
     int *status = dec->h_pin.as<int>();   // read after the stream synchronisation below
     HIP_TRY(hipMemcpyAsync(status, p.status, 4 * sizeof(int), hipMemcpyDeviceToHost, dec->stream));
@@ -1440,6 +1469,11 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
             e_tok = e_seg = e_tr = nullptr;
         }
         HIP_TRY(hipStreamSynchronize(dec->stream));
+        if (status[0] == pkdev::kStatusNotResident && !coop_retry) {   // nothing was decoded: again
+            if ((rc = after_not_resident(dec, p.status))) return rc;
+            coop_retry = true;
+            goto relaunch;
+        }
         const int *c_tok = cnt, *c_steps = c_tok + m, *c_seg = c_steps + m;
         // rows of width wt / ws / wr (prefix copies) or of the full capacities (eager)
         int wt = tcap, ws = bt->segments ? scap : 0, wr = o_trace ? trcap : 0;
@@ -1498,7 +1532,13 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
         }
     } else {
         HIP_TRY(hipStreamSynchronize(dec->stream));
+        if (status[0] == pkdev::kStatusNotResident && !coop_retry) {   // nothing was decoded: again
+            if ((rc = after_not_resident(dec, p.status))) return rc;
+            coop_retry = true;
+            goto relaunch;
+        }
     }
+    if (status[0] == pkdev::kStatusNotResident) return fail(PK_ERR_DEVICE, "decode loop grid not co-resident");
     dec->last_iters = status[1];
     if (prof) {
         unsigned long long t[pkdev::kPrN];

@@ -25,6 +25,9 @@ constexpr int kIdxBits = 14;                // argmax key: index field
 constexpr int kStampShift = 46;             // argmax key: 14 index + 32 value bits below the stamp
 constexpr unsigned kMaxStamp = (1u << 18) - 1;
 constexpr int kFlagStride = 64;             // words between barrier flags (256 B)
+// error word of a launch whose ordinary dispatch was not co-resident (never returned to a caller:
+// the host relaunches the call cooperatively)
+constexpr int kStatusNotResident = 0x7001;
 constexpr int kShards = 32;                 // argmax keys: most max targets per utterance and head
 constexpr int kSlotCols = 2;                // one-domain launches with at most this many joint columns
                                             // exchange argmax keys through per-workgroup slots
@@ -128,7 +131,9 @@ struct KParams {
     unsigned *flags;             // [nwg * kFlagStride]
     unsigned long long *keys;    // [2][n_dom][kColCap][shards][2] best keys per joint column, by iteration parity
     int shards;                  // power of two <= kShards: ranks per shard ~ 8
-    int *status;                 // [0] error code, [1] iterations, [2] overflow, [3] trace overflow
+    int *status;                 // [0] error code, [1] iterations, [2] overflow, [3] trace overflow,
+                                 // [8] workgroups arrived, [9] co-residency decision (cleared per launch)
+    unsigned arrive_ticks;       // ordinary dispatch: limit of the arrival wait (100 MHz ticks); 0: none
     int spec;                    // blank-run columns: spare joint columns evaluate later frames
     int max_iter;
     int red_slots;               // LDS partial slots: a phase runs in passes of red_slots / (units per item) items
@@ -1780,10 +1785,50 @@ __device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp,
     if (p.logits) tap_copy(p, s);
 }
 
+// Co-residency of an ordinary dispatch.  The loop's barriers need every
+// workgroup of the grid resident at once, which a cooperative launch
+// guarantees and an ordinary dispatch does not (a long kernel on another
+// stream may hold CUs).  Each workgroup counts its arrival; the first to see
+// the whole grid arrived decides "go", the first to wait past p.arrive_ticks
+// decides "abort", and one compare-and-swap settles which.  Every workgroup
+// then follows that decision.  On "abort" no workgroup has written anything
+// but these words, the winner of the abort sets the error word to
+// kStatusNotResident, and the host relaunches the call cooperatively; a
+// workgroup that starts after the decision reads it and leaves.  Every wait is
+// bounded by the tick limit.
+constexpr unsigned kArriveGo = 1u, kArriveAbort = 2u;
+__device__ __forceinline__ bool coresident(const KParams &p) {
+    __shared__ unsigned s_dec;
+    if (threadIdx.x == 0) {
+        unsigned *cnt = reinterpret_cast<unsigned *>(p.status + 8), *dec = cnt + 1;
+        bool all = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u >= gridDim.x;
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        unsigned d = __hip_atomic_load(dec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        while (d == 0u) {
+            const bool late = !all && __builtin_amdgcn_s_memrealtime() - t0 > p.arrive_ticks;
+            if (all || late) {
+                unsigned z = 0u;
+                const unsigned want = all ? kArriveGo : kArriveAbort;
+                if (__hip_atomic_compare_exchange_strong(dec, &z, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT) &&
+                    want == kArriveAbort)
+                    __hip_atomic_store(p.status, kStatusNotResident, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                all = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= gridDim.x;
+            }
+            d = __hip_atomic_load(dec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        s_dec = d;
+    }
+    __syncthreads();
+    return s_dec == kArriveGo;
+}
+
 template <int WC, bool ONE>
 __global__ void __launch_bounds__(kBlock) decode_loop_kernel(KParams p) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
     __shared__ Ctl s;
+    if (p.arrive_ticks != 0u && !coresident(p)) return;
     const int wg = blockIdx.x;
     const int H = p.H, L = p.L, J = p.J, n_all = p.n_utts;
     unsigned epoch = 0;
