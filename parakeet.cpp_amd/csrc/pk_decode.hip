@@ -1035,7 +1035,8 @@ constexpr unsigned kArriveLimitUs = 100;
 // then launches cooperatively from there on.  Where the runtime refuses a cooperative launch
 // (another process holds the device's cooperative queue), the loop runs as an ordinary
 // dispatch without the check, and its barriers' 2 s limit is the last guard.
-// PK_LOOP_DISPATCH=0 makes every launch cooperative, =1 every launch an ordinary dispatch;
+// PK_LOOP_DISPATCH=0 makes every launch cooperative, =1 every launch an ordinary dispatch (a
+// relaunch then without the check), as under a profiler;
 // PK_ARRIVE_US sets the arrival limit for tests of the relaunch: the first launch of a call is
 // then an ordinary dispatch whatever the device's history, and nothing is remembered.
 int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds, bool coop) {
@@ -1046,9 +1047,16 @@ int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds, bool coop) {
     void *args[] = {&p};
     const void *fn = dec->loop_fn[p.slots ? 1 : 0];   // one domain: the argmax-slot instantiation
     bool &refused = g_loops.coop_refused[dec->device];
-    static const int mode = [] {   // 0: cooperative, 1: ordinary dispatch, -1: default
+    // 0: cooperative, 1: ordinary dispatch, -1: the default above.  Under a profiler (its
+    // ROCPROF* environment, or its tool library preloaded) always an ordinary dispatch.
+    static const int mode = [] {
         const char *v = std::getenv("PK_LOOP_DISPATCH");
-        return v && v[0] ? (v[0] == '1' ? 1 : 0) : -1;
+        if (v && v[0]) return v[0] == '1' ? 1 : 0;
+        const char *pre = std::getenv("LD_PRELOAD");
+        if (pre && strstr(pre, "rocprof")) return 1;
+        for (char **e = environ; e && *e; ++e)
+            if (strncmp(*e, "ROCPROF", 7) == 0) return 1;
+        return -1;
     }();
     const char *lim = std::getenv("PK_ARRIVE_US");   // a test setting of the arrival limit
     const bool cooperative =
@@ -1065,8 +1073,9 @@ int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds, bool coop) {
         refused = true;
     }
     const unsigned limit_us = lim && lim[0] ? (unsigned)std::min(std::max(0, atoi(lim)), 1000000) : kArriveLimitUs;
-    // 100 MHz clock; a refused cooperative relaunch runs without the check
-    p.arrive_ticks = cooperative ? 0u : std::max(1u, limit_us * 100u);
+    // 100 MHz clock; a relaunch that cannot be cooperative (refused, or ordinary dispatch
+    // forced) runs without the check
+    p.arrive_ticks = cooperative || coop ? 0u : std::max(1u, limit_us * 100u);
     HIP_TRY(hipLaunchKernel(fn, dim3(nwg), dim3(kBlock), args, lds, dec->stream));
     HIP_TRY(hipEventRecord(last, dec->stream));
     return 0;
