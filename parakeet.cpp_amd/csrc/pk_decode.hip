@@ -85,6 +85,21 @@ constexpr int kCacheMinFrames = 16;
 constexpr long long kNarrowRows = 256;
 
 thread_local std::string g_err;
+
+// Decode-loop launches of this process, per device: the loop's workgroups
+// wait on one another, so two loops must never share a device.  Every launch
+// waits for the previous one on the same device: on the same stream by stream
+// order, from another stream through an event recorded on the previous loop's
+// stream at this launch (its work so far, the loop included).
+struct LoopOrder {
+    std::mutex mu;
+    std::map<int, hipStream_t> last_stream;   // per device: the stream of the latest loop launch
+    std::map<int, hipEvent_t> last;       // per device: event for a wait across streams
+    std::map<int, bool> coop_refused;     // per device: cooperative launches refused once
+    std::map<int, int> coop_left;         // per device: launches still cooperative after a grid
+                                          // found not co-resident
+};
+LoopOrder g_loops;
 // set by an atexit handler: process teardown has begun
 std::atomic<bool> g_exiting{false};
 
@@ -771,7 +786,10 @@ PK_API int pk_decoder_create(const pk_decoder_desc *d, int32_t n_slots, pk_decod
     if (hipStreamCreateWithFlags(&dec->stream, hipStreamNonBlocking) != hipSuccess)
         return cleanup(fail(PK_ERR_DEVICE, "stream"));
     for (auto &e : dec->ev)
-        if (hipEventCreate(&e) != hipSuccess) return cleanup(fail(PK_ERR_DEVICE, "event"));
+        // timing only (pk_last_timing, after a stream synchronisation): no system-scope fences,
+        // which cost each call several microseconds
+        if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess)
+            return cleanup(fail(PK_ERR_DEVICE, "event"));
     *out = dec;
     return 0;
 }
@@ -789,6 +807,11 @@ PK_API int pk_decoder_destroy(pk_decoder *dec) {
     }
     (void)hipSetDevice(dec->device);
     if (dec->stream) (void)hipStreamSynchronize(dec->stream);
+    {   // its loops have completed: a later launch from another stream need not wait for them
+        std::lock_guard<std::mutex> lk(g_loops.mu);
+        auto it = g_loops.last_stream.find(dec->device);
+        if (it != g_loops.last_stream.end() && it->second == dec->stream) it->second = nullptr;
+    }
     for (auto &e : dec->ev) if (e) (void)hipEventDestroy(e);
     if (dec->stream) (void)hipStreamDestroy(dec->stream);
     if (dec->lock_fd >= 0) close(dec->lock_fd);
@@ -1005,16 +1028,6 @@ int open_loop_lock(int device) {
     return fd;
 }
 
-// Decode-loop launches of this process, per device: the loop's workgroups
-// wait on one another, so two loops must never share a device.  Every launch
-// waits for the previous one on the same device, whatever stream it was on.
-struct LoopOrder {
-    std::mutex mu;
-    std::map<int, hipEvent_t> last;       // per device: recorded after the latest loop launch
-    std::map<int, bool> coop_refused;     // per device: cooperative launches refused once
-    std::map<int, bool> coop_needed;      // per device: an ordinary dispatch was once not co-resident
-};
-LoopOrder g_loops;
 
 // A cooperative launch guarantees that the whole grid (one workgroup per CU,
 // checked at create) is resident at once.  The runtime refuses it
@@ -1023,16 +1036,19 @@ LoopOrder g_loops;
 // no other loop running the grid fits, and the ordering above keeps this
 // process's loops apart.  If a loop of another process overlaps it, the
 // barrier's 2 s limit ends both launches with PK_ERR_TIMEOUT.
-// Arrival limit of an ordinary dispatch's co-residency check (kernel start to the whole grid
-// arrived): a grid that has not arrived by then is relaunched cooperatively.
-constexpr unsigned kArriveLimitUs = 100;
+// Arrival limit of an ordinary dispatch's co-residency check (a workgroup's start to the whole
+// grid arrived): a grid that has not arrived by then is relaunched cooperatively, and the next
+// kCoopAfterAbort launches on that device are cooperative.  (The first launch after the GPU has
+// idled has been seen to take over 100 us to bring every workgroup up.)
+constexpr unsigned kArriveLimitUs = 1000;
+constexpr int kCoopAfterAbort = 256;
 
 // The loop launch.  By default an ordinary dispatch whose workgroups first check that the
 // whole grid is resident (pkdev::coresident): a cooperative launch costs about 14 us more per
 // call, and under rocprofv3 (ROCm 7.2) any process that made one ends with SIGSEGV in the HIP
 // runtime's exit-time teardown.  A grid found not resident ends at once with
-// kStatusNotResident and the call is relaunched with coop = true (decode_impl); the device
-// then launches cooperatively from there on.  Where the runtime refuses a cooperative launch
+// kStatusNotResident and the call is relaunched with coop = true (decode_impl); the device's
+// next kCoopAfterAbort launches are cooperative.  Where the runtime refuses a cooperative launch
 // (another process holds the device's cooperative queue), the loop runs as an ordinary
 // dispatch without the check, and its barriers' 2 s limit is the last guard.
 // PK_LOOP_DISPATCH=0 makes every launch cooperative, =1 every launch an ordinary dispatch (a
@@ -1041,9 +1057,14 @@ constexpr unsigned kArriveLimitUs = 100;
 // then an ordinary dispatch whatever the device's history, and nothing is remembered.
 int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds, bool coop) {
     std::lock_guard<std::mutex> lk(g_loops.mu);
-    hipEvent_t &last = g_loops.last[dec->device];
-    if (!last) HIP_TRY(hipEventCreateWithFlags(&last, hipEventDisableTiming));
-    HIP_TRY(hipStreamWaitEvent(dec->stream, last, 0));
+    hipStream_t &prev = g_loops.last_stream[dec->device];
+    if (prev && prev != dec->stream) {
+        hipEvent_t &last = g_loops.last[dec->device];
+        if (!last) HIP_TRY(hipEventCreateWithFlags(&last, hipEventDisableTiming | hipEventDisableSystemFence));
+        HIP_TRY(hipEventRecord(last, prev));
+        HIP_TRY(hipStreamWaitEvent(dec->stream, last, 0));
+    }
+    prev = dec->stream;
     void *args[] = {&p};
     const void *fn = dec->loop_fn[p.slots ? 1 : 0];   // one domain: the argmax-slot instantiation
     bool &refused = g_loops.coop_refused[dec->device];
@@ -1059,14 +1080,15 @@ int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds, bool coop) {
         return -1;
     }();
     const char *lim = std::getenv("PK_ARRIVE_US");   // a test setting of the arrival limit
-    const bool cooperative =
-        mode == 0 || (mode == -1 && (coop || (!(lim && lim[0]) && g_loops.coop_needed[dec->device])));
+    int &left = g_loops.coop_left[dec->device];
+    const bool after_abort = mode == -1 && !coop && !(lim && lim[0]) && left > 0;
+    if (after_abort) --left;
+    const bool cooperative = mode == 0 || (mode == -1 && (coop || after_abort));
     if (cooperative && !refused) {
         p.arrive_ticks = 0u;
         const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(nwg), dim3(kBlock), args, lds, dec->stream);
         if (e != hipErrorIllegalState) {
             HIP_TRY(e);
-            HIP_TRY(hipEventRecord(last, dec->stream));
             return 0;
         }
         (void)hipGetLastError();
@@ -1077,19 +1099,17 @@ int launch_loop(pk_decoder *dec, int nwg, KParams &p, size_t lds, bool coop) {
     // forced) runs without the check
     p.arrive_ticks = cooperative || coop ? 0u : std::max(1u, limit_us * 100u);
     HIP_TRY(hipLaunchKernel(fn, dim3(nwg), dim3(kBlock), args, lds, dec->stream));
-    HIP_TRY(hipEventRecord(last, dec->stream));
     return 0;
 }
 
-// A launch found not co-resident (kStatusNotResident): clear its status words and
-// remember, unless the arrival limit is a test setting, that this device launches
-// cooperatively.
+// A launch found not co-resident (kStatusNotResident): clear its status words and, unless the
+// arrival limit is a test setting, make the device's next kCoopAfterAbort launches cooperative.
 int after_not_resident(pk_decoder *dec, int *d_status) {
     pkdev::fill_zero_kernel<<<1, 256, 0, dec->stream>>>(reinterpret_cast<unsigned *>(d_status), 16);
     HIP_TRY(hipGetLastError());
     if (!std::getenv("PK_ARRIVE_US")) {
         std::lock_guard<std::mutex> lk(g_loops.mu);
-        g_loops.coop_needed[dec->device] = true;
+        g_loops.coop_left[dec->device] = kCoopAfterAbort;
     }
     static std::atomic<bool> noted{false};
     if (!noted.exchange(true) || std::getenv("PK_ARRIVE_US"))
