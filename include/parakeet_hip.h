@@ -201,8 +201,16 @@ PK_API int pk_window_split(int32_t n_utts, const int32_t *n_frames, int32_t max_
 PK_API int pk_decode_noalloc(pk_decoder *dec, const pk_batch *batch);
 /* Time, with HIP events on the handle's stream, the last pk_decode's
  * kernels: enc_proj GEMM and the decode loop (milliseconds), and its lockstep
- * iterations; summed over the launches of a call decoded in several. */
+ * iterations; summed over the launches of a call decoded in several.  The
+ * times are -1 when the handle's timing was off for that call (the iterations
+ * are always given).  The reference times its decode on the host clock
+ * (src/parakeet_tdt.cpp:983-1005, decode_ms). */
 PK_API int pk_last_timing(pk_decoder *dec, float *enc_proj_ms, float *loop_ms, int32_t *iterations);
+/* Record the timing events of pk_last_timing in this handle's calls (on: 1,
+ * the default) or not (0).  No counterpart in the reference: the three event
+ * records add a few microseconds to every call, which latency-bound callers
+ * that never read the times (the drop-in and C++ runtimes) leave out. */
+PK_API int pk_decoder_set_timing(pk_decoder *dec, int32_t on);
 /* Message of the last failure on this thread ("" if none). */
 PK_API const char *pk_last_error(void);
 /* Device facts used for launches: compute units, LDS bytes per block, wave size. */

@@ -90,6 +90,8 @@ int make_pool(const pk_decoder_desc &d, int n_slots, std::shared_ptr<SlotPool> &
         std::fprintf(stderr, "prepare_runtime: %s\n", pk_last_error());
         return rc;
     }
+    // these runtimes never read pk_last_timing: leave its per-call event records out
+    (void)pk_decoder_set_timing(pool->dec, 0);
     for (int s = n_slots - 1; s >= 0; --s) pool->free_slots.push_back(s);
     out = std::move(pool);
     return 0;

@@ -387,6 +387,8 @@ struct pk_decoder {
     size_t lds_fixed = 0;      // activation blocks + redundant layer-0 output
     hipStream_t stream = nullptr;
     hipEvent_t ev[3] = {};
+    bool timing = true;        // record ev[] in each call (pk_decoder_set_timing)
+    bool timed = false;        // the last call recorded them
     DevBuf arena;              // weights
     DevBuf eproj;              // [V1][4H] layer-0 input projection of every token
     DevBuf slots_h, slots_c, slots_pp, slots_r, slots_ctrl;
@@ -887,8 +889,20 @@ PK_API int pk_slot_copy(pk_decoder *dec, int32_t src, int32_t dst) {
     return 0;
 }
 
+PK_API int pk_decoder_set_timing(pk_decoder *dec, int32_t on) {
+    if (!dec) return fail(PK_ERR_ARG, "pk_decoder_set_timing: null");
+    dec->timing = on != 0;
+    return 0;
+}
+
 PK_API int pk_last_timing(pk_decoder *dec, float *enc_proj_ms, float *loop_ms, int32_t *iterations) {
     if (!dec) return fail(PK_ERR_ARG, "pk_last_timing: null");
+    if (!dec->timed) {
+        if (enc_proj_ms) *enc_proj_ms = -1.f;
+        if (loop_ms) *loop_ms = -1.f;
+        if (iterations) *iterations = dec->chained ? dec->chain_iters : dec->last_iters;
+        return 0;
+    }
     if (dec->chained) {
         if (enc_proj_ms) *enc_proj_ms = dec->chain_ep_ms;
         if (loop_ms) *loop_ms = dec->chain_loop_ms;
@@ -1120,6 +1134,7 @@ int after_not_resident(pk_decoder *dec, int *d_status) {
 int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratch cs) {
     if (!dec || !bt) return fail(PK_ERR_ARG, "pk_decode: null argument");
     dec->chained = false;   // (decode_chained sets it again after its last launch)
+    dec->timed = false;     // (set where the call records its first event)
     KParams &p = dec->kp;
     if (bt->d_enc != dec->desc.d_enc)
         return fail(PK_ERR_D_ENC, "encoder d_model mismatch (%d vs %d)", bt->d_enc, dec->desc.d_enc);
@@ -1278,7 +1293,8 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     // (one fill kernel, never a memset, so that the call may run under graph capture)
     const size_t clear_words = clear_bytes / 4;   // clear_bytes is a multiple of 32
 
-    HIP_TRY(hipEventRecord(dec->ev[0], dec->stream));
+    dec->timed = dec->timing;
+    if (dec->timed) HIP_TRY(hipEventRecord(dec->ev[0], dec->stream));
     float *d_encp = nullptr;
     if (rows > 0) {
         if ((rc = cs.get(dec->d_encp, (size_t)rows * J * 4, reinterpret_cast<void **>(&d_encp)))) return rc;
@@ -1305,7 +1321,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
             static_cast<unsigned *>(d_clear), clear_words);
         HIP_TRY(hipGetLastError());
     }
-    HIP_TRY(hipEventRecord(dec->ev[1], dec->stream));
+    if (dec->timed) HIP_TRY(hipEventRecord(dec->ev[1], dec->stream));
 
     // outputs: device arrays as given, or a device staging area copied back
     const int tcap = bt->token_cap, scap = std::max(bt->seg_cap, 0), trcap = bt->trace ? bt->trace_cap : 0;
@@ -1461,7 +1477,7 @@ int decode_impl(pk_decoder *dec, const pk_batch *bt, bool keep_empty, CallScratc
     bool coop_retry = false;   // set when an ordinary dispatch found its grid not co-resident
 relaunch:
     if ((rc = launch_loop(dec, nwg, p, lds, coop_retry))) return rc;
-    HIP_TRY(hipEventRecord(dec->ev[2], dec->stream));
+    if (dec->timed) HIP_TRY(hipEventRecord(dec->ev[2], dec->stream));
     int *status = dec->h_pin.as<int>();   // read after the stream synchronisation below
     HIP_TRY(hipMemcpyAsync(status, p.status, 4 * sizeof(int), hipMemcpyDeviceToHost, dec->stream));
     if (host) {
@@ -1688,8 +1704,8 @@ int decode_chained(pk_decoder *dec, const pk_batch *bt, int W, const std::vector
         const int rc = decode_impl(dec, &b, false);
         if (rc != 0 && rc != PK_ERR_OVERFLOW) return rc;   // capacity is judged on the totals below
         float a = 0.f, c = 0.f;
-        if (hipEventElapsedTime(&a, dec->ev[0], dec->ev[1]) == hipSuccess) ep_ms += a;
-        if (hipEventElapsedTime(&c, dec->ev[1], dec->ev[2]) == hipSuccess) loop_ms += c;
+        if (dec->timed && hipEventElapsedTime(&a, dec->ev[0], dec->ev[1]) == hipSuccess) ep_ms += a;
+        if (dec->timed && hipEventElapsedTime(&c, dec->ev[1], dec->ev[2]) == hipSuccess) loop_ms += c;
         iters += dec->last_iters;
         for (int i = 0; i < m; ++i) {
             const int u = idx[i];

@@ -70,7 +70,7 @@ class PkBatch(C.Structure):
 
 EXPORTED = ["pk_decoder_create", "pk_decoder_destroy", "pk_slot_init", "pk_slot_reset",
             "pk_slot_read", "pk_slot_copy", "pk_decode", "pk_decode_noalloc", "pk_last_timing", "pk_last_error",
-            "pk_device_info", "pk_window_split"]
+            "pk_device_info", "pk_window_split", "pk_decoder_set_timing"]
 
 _lib = None
 
@@ -92,6 +92,7 @@ def lib():
         L.pk_last_timing.argtypes = [C.c_void_p, C.POINTER(C.c_float), C.POINTER(C.c_float),
                                      C.POINTER(C.c_int32)]
         L.pk_last_error.restype = C.c_char_p
+        L.pk_decoder_set_timing.argtypes = [C.c_void_p, C.c_int32]
         L.pk_device_info.argtypes = [C.POINTER(C.c_int32)] * 3
         L.pk_window_split.argtypes = [C.c_int32, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
                                       C.POINTER(C.c_int32), C.c_void_p]
@@ -342,9 +343,15 @@ class Decoder:
         check((lib().pk_decode_noalloc if noalloc else lib().pk_decode)(self.h, C.byref(b)))
 
     def last_timing(self):
+        """Kernel times of the last call (ms; -1 when timing was off for it) and its
+        lockstep iterations."""
         a, b, it = C.c_float(), C.c_float(), C.c_int32()
         check(lib().pk_last_timing(self.h, C.byref(a), C.byref(b), C.byref(it)))
         return dict(enc_proj_ms=a.value, loop_ms=b.value, iterations=it.value)
+
+    def set_timing(self, on: bool):
+        """Record the timing events of last_timing in each call (the default) or not."""
+        check(lib().pk_decoder_set_timing(self.h, 1 if on else 0))
 
 
 def window_split(n_frames, max_symbols: int, joint_hidden: int, max_duration: int):

@@ -334,3 +334,26 @@ def test_python_decode_device_frames(tmp_path, kind):
         assert got[u]["steps"] == want[u]["steps"], u
         assert np.array_equal(got[u]["trace"], want[u]["trace"]), u
         assert got[u]["segments"].tolist() == want[u]["segments"].tolist(), u
+
+
+def test_timing_events_optional(tmp_path):
+    """pk_decoder_set_timing(0): calls record no timing events, pk_last_timing
+    gives -1 for the kernel times and still the lockstep iterations, and the
+    decode is the same bit for bit; turned on again, the times come back."""
+    from parakeet_amd import pk, synth
+    path = str(tmp_path / "t.gguf")
+    small_tdt(path)
+    dev = pk.Decoder.from_gguf(path, n_slots=8)
+    encs = [synth.encoder_frames(600 + u, 30 + 7 * u, 128) for u in range(3)]
+    a = dev.decode(encs, slots=[0, 1, 2], trace=True)
+    ta = dev.last_timing()
+    assert ta["loop_ms"] > 0 and ta["enc_proj_ms"] > 0 and ta["iterations"] > 0
+    dev.set_timing(False)
+    b = dev.decode(encs, slots=[3, 4, 5], trace=True)
+    tb = dev.last_timing()
+    assert tb["loop_ms"] == -1 and tb["enc_proj_ms"] == -1 and tb["iterations"] == ta["iterations"]
+    for u in range(3):
+        assert np.array_equal(a[u]["trace"], b[u]["trace"]), u
+    dev.set_timing(True)
+    dev.decode(encs, slots=[6, 7, 0], reset=np.ones(3, np.uint8))
+    assert dev.last_timing()["loop_ms"] > 0
