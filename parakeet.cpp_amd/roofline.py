@@ -29,8 +29,9 @@ BLOCK_BYTES = {8: 34, 6: 22, 2: 18}   # q8_0, q5_0, q4_0: bytes per 32 stored we
 
 
 def wbytes(rows: int, cols: int, ggml_type: int) -> int:
-    """Stored bytes of a matrix (the algorithmic weight bytes; q5_0 / q4_0 are read as
-    their exact q8_0 repacking, 34 bytes per block)."""
+    """Stored bytes of a matrix: the algorithmic weight bytes (q8_0 34, q5_0 22, q4_0 18
+    bytes per 32 weights).  The device reads q5_0 / q4_0 matrices as their exact q8_0
+    repacking, 34 bytes per 32 weights, so its weight reads for those types exceed these."""
     if ggml_type in BLOCK_BYTES:
         return rows * (cols // 32) * BLOCK_BYTES[ggml_type]
     return rows * cols * (2 if ggml_type == 1 else 4)
