@@ -132,7 +132,7 @@ struct KParams {
     unsigned long long *keys;    // [2][n_dom][kColCap][shards][2] best keys per joint column, by iteration parity
     int shards;                  // power of two <= kShards: ranks per shard ~ 8
     int *status;                 // [0] error code, [1] iterations, [2] overflow, [3] trace overflow,
-                                 // [8] workgroups arrived, [9] co-residency decision (cleared per launch)
+                                 // [9] co-residency decision (cleared per launch)
     unsigned arrive_ticks;       // ordinary dispatch: limit of the arrival wait (100 MHz ticks); 0: none
     int spec;                    // blank-run columns: spare joint columns evaluate later frames
     int max_iter;
@@ -1788,36 +1788,53 @@ __device__ __forceinline__ void decide(const KParams &p, Ctl &s, unsigned stamp,
 // Co-residency of an ordinary dispatch.  The loop's barriers need every
 // workgroup of the grid resident at once, which a cooperative launch
 // guarantees and an ordinary dispatch does not (a long kernel on another
-// stream may hold CUs).  Each workgroup counts its arrival; the first to see
-// the whole grid arrived decides "go", the first to wait past p.arrive_ticks
-// decides "abort", and one compare-and-swap settles which.  Every workgroup
-// then follows that decision.  On "abort" no workgroup has written anything
-// but these words, the winner of the abort sets the error word to
-// kStatusNotResident, and the host relaunches the call cooperatively; a
-// workgroup that starts after the decision reads it and leaves.  Every wait is
-// bounded by the tick limit.
+// stream may hold CUs).  Each workgroup stores an arrival flag (word 1 of its
+// barrier flag slot).  Workgroup 0 watches every flag, one thread per
+// workgroup, for up to p.arrive_ticks, and proposes "go" if all arrived,
+// "abort" if not; any other workgroup that has waited twice that long for a
+// decision proposes "abort" (workgroup 0 itself may be the one not resident).
+// One compare-and-swap on the decision word settles it, and every workgroup
+// follows it.  On "abort" no workgroup has written anything but these words;
+// the winner of the abort sets the error word to kStatusNotResident, and the
+// host relaunches the call cooperatively.  A workgroup that starts after the
+// decision reads it and leaves.  Every wait is bounded by the tick limit.
 constexpr unsigned kArriveGo = 1u, kArriveAbort = 2u;
+__device__ __forceinline__ void propose(const KParams &p, unsigned *dec, unsigned want) {
+    unsigned z = 0u;
+    if (__hip_atomic_compare_exchange_strong(dec, &z, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT) &&
+        want == kArriveAbort)
+        __hip_atomic_store(p.status, kStatusNotResident, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ bool coresident(const KParams &p) {
     __shared__ unsigned s_dec;
+    __shared__ int s_all;
+    unsigned *dec = reinterpret_cast<unsigned *>(p.status + 9);
     if (threadIdx.x == 0) {
-        unsigned *cnt = reinterpret_cast<unsigned *>(p.status + 8), *dec = cnt + 1;
-        bool all = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u >= gridDim.x;
-        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-        unsigned d = __hip_atomic_load(dec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        while (d == 0u) {
-            const bool late = !all && __builtin_amdgcn_s_memrealtime() - t0 > p.arrive_ticks;
-            if (all || late) {
-                unsigned z = 0u;
-                const unsigned want = all ? kArriveGo : kArriveAbort;
-                if (__hip_atomic_compare_exchange_strong(dec, &z, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT) &&
-                    want == kArriveAbort)
-                    __hip_atomic_store(p.status, kStatusNotResident, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            } else {
-                all = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= gridDim.x;
+        s_all = 1;
+        __hip_atomic_store(p.flags + (size_t)blockIdx.x * kFlagStride + 1, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (blockIdx.x == 0) {   // the decider (gridDim.x <= the block size)
+        __syncthreads();
+        if (threadIdx.x < gridDim.x) {
+            const unsigned *f = p.flags + (size_t)threadIdx.x * kFlagStride + 1;
+            const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+            while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+                if (__builtin_amdgcn_s_memrealtime() - t0 > p.arrive_ticks) {
+                    s_all = 0;
+                    break;
+                }
             }
-            d = __hip_atomic_load(dec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        __syncthreads();
+        if (threadIdx.x == 0) propose(p, dec, s_all ? kArriveGo : kArriveAbort);
+    }
+    if (threadIdx.x == 0) {
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        unsigned d;
+        while ((d = __hip_atomic_load(dec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0u)
+            if (__builtin_amdgcn_s_memrealtime() - t0 > 2ull * p.arrive_ticks) propose(p, dec, kArriveAbort);
         s_dec = d;
     }
     __syncthreads();
