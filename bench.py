@@ -15,6 +15,9 @@ other workload shapes (--no-extras skips them):
   b1                 B=1, T=125 on the same decoder: latency per step
   b1_cpp             the same utterance through the drop-in tdt_greedy_decode (the reference
                      CLI's call), wall time per call and per step, host overhead included
+  eou_stream_cpp     the EOU streaming workload below through the C++ API
+                     (eou_decode_batch_device over device frames, states carried), wall
+                     time per chunk call
   b1_blank4          the same with the blank logit raised by 4 (blank-dominated decoding, as a
                      trained model's is): latency per step with runs of blanks walked over
                      the joint tile's spare columns, and without them (PK_SPEC=0)
@@ -144,6 +147,40 @@ def cpp_b1(frames=125, reps=30):
             "note": "wall with the handle's timing events off, as the drop-in runs; kernel and host "
                     "shares from a second pass with them on",
             "reps": d["reps"]}
+
+
+def cpp_eou_stream(B=128, chunks=40, F=2):
+    """The EOU streaming workload of eou_stream_extra (EOU-120m shapes, q8_0, B
+    sessions x `chunks` chunks of F frames, the same frames) through the C++ API:
+    tests/cpp/decoder_api_main --bench-eou-stream, one eou_decode_batch_device call
+    per chunk over the encoder output in device memory, with the session states
+    carried, in a child process started before this process touches the GPU."""
+    import subprocess
+    exe = os.path.join(ROOT, "tests", "cpp", "decoder_api_main")
+    if not os.path.exists(exe):
+        return {"missing": "tests/cpp/decoder_api_main is not built"}
+    import __graft_entry__ as graft
+    graft.load_package()
+    from parakeet_amd import synth
+    tmp = tempfile.mkdtemp(prefix="pk_cpp_")
+    path = os.path.join(tmp, "eou-120m-q8_0.gguf")
+    synth.make_shape(path, "eou-120m")
+    D = 512
+    fpath = os.path.join(tmp, "frames.bin")
+    with open(fpath, "wb") as f:
+        np.array([B, chunks * F, D], np.int32).tofile(f)
+        for u in range(B):
+            synth.encoder_frames(u, chunks * F, D).astype(np.float32).tofile(f)
+    print("[bench] eou_stream_cpp: eou_decode_batch_device", file=sys.stderr, flush=True)
+    r = subprocess.run(["timeout", "-k", "10", "120", exe, "--bench-eou-stream", path, fpath, str(F)],
+                       capture_output=True, text=True, errors="replace")
+    if r.returncode != 0:
+        return {"missing": f"decoder_api_main --bench-eou-stream failed (status {r.returncode}): {r.stderr[-300:]}"}
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    return {"api": "C++ eou_decode_batch_device (device frames, host outputs, states carried)",
+            "sessions": d["sessions"], "chunks": d["chunks"], "frames_per_chunk": d["frames_per_chunk"],
+            "decode_steps": d["steps"], "tokens": d["tokens"], "us_per_chunk_call": d["call_us"],
+            "us_per_chunk_call_min": d["call_us_min"]}
 
 
 class Workload:
@@ -449,9 +486,10 @@ def main():
         traffic_csvs = list(args.traffic)
     elif not (args.no_traffic or args.no_extras or args.only):
         traffic_csvs, traffic_note = traffic_passes(args)
-    b1_cpp = None
+    b1_cpp = eou_cpp = None
     if not (args.no_extras or args.only):
         b1_cpp = cpp_b1()
+        eou_cpp = cpp_eou_stream()
     import __graft_entry__ as graft
     graft.load_package()
     from parakeet_amd import gguf, hipmem, pk, roofline, synth
@@ -596,6 +634,7 @@ def main():
             if name == "b1":
                 wl.free()   # the B=64 frames are not needed past here
         out["b1_cpp"] = b1_cpp
+        out["eou_stream_cpp"] = eou_cpp
     print(json.dumps(out), flush=True)
     # every device buffer is released before the interpreter exits (no HIP call
     # runs from a finaliser after the runtime has been torn down)

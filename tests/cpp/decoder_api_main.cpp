@@ -13,9 +13,11 @@
 //     and Engine::transcribe_device_batch on ragged windows, beside the same
 //     windows decoded from host memory, plus their argument checks.
 // Usage: decoder_api_main TDT.gguf TDT_FRAMES EOU.gguf EOU_FRAMES WINDOW
+//        decoder_api_main --bench-eou-stream EOU.gguf FRAMES CHUNK   (timing; see bench_eou_stream)
 // Frame files: int32 n, T, D, then n*T*D float32 (utterance-major).
 #include <cstdio>
 #include <algorithm>
+#include <chrono>
 #include <cstdlib>
 #include <memory>
 #include <string>
@@ -245,7 +247,73 @@ int device_section(const char *tdt_path, const char *eou_path, const Frames &ft,
     return 0;
 }
 
+// --bench-eou-stream EOU.gguf FRAMES CHUNK: the streaming form of the EOU decode
+// over an encoder output resident in device memory.  FRAMES holds n sessions of T
+// frames; every session is fed T / CHUNK chunks of CHUNK frames, all sessions of a
+// chunk in one eou_decode_batch_device call with their states carried (Mode 3 over
+// many sessions at once, src/parakeet_engine.cpp:753-886).  The stream runs twice
+// on fresh states (a warm-up, then the timed pass); one JSON line: wall time per
+// chunk call (outputs back in the caller's vectors), decode steps.
+int bench_eou_stream(int argc, char **argv) {
+    if (argc != 5) return 2;
+    using namespace parakeet_hip;
+    Frames fe;
+    if (!read_frames(argv[3], fe)) return fail("read frames", -1);
+    const int F = atoi(argv[4]);
+    if (F <= 0 || fe.T % F) return fail("chunk frames", -1);
+    const int chunks = fe.T / F;
+    DecoderModel eou;
+    int rc;
+    if ((rc = load_from_gguf(argv[2], eou)) != 0) return fail("load_from_gguf(eou)", rc);
+    EouRuntimeWeights ew;
+    if ((rc = eou_prepare_runtime(eou, ew, 2 * fe.n)) != 0) return fail("eou_prepare_runtime", rc);
+    EouDecodeOptions eopt;
+    eopt.max_symbols_per_step = eou.encoder_cfg.eou_max_symbols_per_step;
+    float *d = nullptr;
+    const size_t bytes = fe.data.size() * sizeof(float);
+    if (hipMalloc(reinterpret_cast<void **>(&d), bytes) != hipSuccess ||
+        hipMemcpy(d, fe.data.data(), bytes, hipMemcpyHostToDevice) != hipSuccess)
+        return fail("device frames", -1);
+    const DeviceEncoderOutput enc{d, (int64_t)fe.n * fe.T, fe.D};
+    std::vector<int> nf(fe.n, F);
+    std::vector<int64_t> rows(fe.n);
+    double wall = 0.0, wmin = 1e30;
+    long steps = 0, tokens = 0;
+    for (int pass = 0; pass < 2; ++pass) {
+        std::vector<EouDecodeState> st(fe.n);
+        std::vector<EouDecodeState *> sp(fe.n);
+        for (int u = 0; u < fe.n; ++u) {
+            eou_init_state(ew, st[u]);
+            sp[u] = &st[u];
+        }
+        for (int c = 0; c < chunks; ++c) {
+            for (int u = 0; u < fe.n; ++u) rows[u] = (int64_t)u * fe.T + (int64_t)c * F;
+            std::vector<std::vector<int32_t>> toks;
+            std::vector<std::vector<EouSegmentBoundary>> segs;
+            std::vector<int> stp;
+            const auto t0 = std::chrono::steady_clock::now();
+            if ((rc = eou_decode_batch_device(eou, ew, enc, rows, nf, eopt, sp, toks, segs, stp)) != 0)
+                return fail("eou_decode_batch_device", rc);
+            const double dt = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+            if (pass == 1) {
+                wall += dt;
+                wmin = std::min(wmin, dt);
+                for (int u = 0; u < fe.n; ++u) {
+                    steps += stp[u];
+                    tokens += (long)toks[u].size();
+                }
+            }
+        }
+    }
+    (void)hipFree(d);
+    printf("{\"call_us\":%.3f,\"call_us_min\":%.3f,\"steps\":%ld,\"tokens\":%ld,\"sessions\":%d,"
+           "\"chunks\":%d,\"frames_per_chunk\":%d}\n",
+           wall / chunks, wmin, steps, tokens, fe.n, chunks, F);
+    return 0;
+}
+
 int main(int argc, char **argv) {
+    if (argc > 1 && std::string(argv[1]) == "--bench-eou-stream") return bench_eou_stream(argc, argv);
     if (argc != 6) {
         fprintf(stderr, "usage: %s TDT.gguf TDT_FRAMES EOU.gguf EOU_FRAMES WINDOW\n", argv[0]);
         return 2;
