@@ -193,6 +193,38 @@ def test_dropin_matches_c_abi(tmp_path):
 
 
 @pytest.mark.gpu
+def test_dropin_window_past_the_stamp(tmp_path):
+    """A window longer than one launch of the decode loop takes, through the
+    drop-in: tdt_greedy_decode over 24,000 frames at the default symbol cap (past
+    the 23,830 frames of one launch, so pk_decode chains launches) returns the
+    same tokens and steps as the same utterance decoded by tdt_decode_window in
+    three 8,000-frame windows on one state, and as the C ABI.  The reference's
+    loop has no length limit (src/parakeet_tdt.cpp:917-967)."""
+    if not os.path.exists(DRIVER):
+        pytest.skip("the drop-in driver is built only where parakeet.cpp's sources are present")
+    from parakeet_amd import pk, synth
+    tdt_path, eou_path = str(tmp_path / "t.gguf"), str(tmp_path / "e.gguf")
+    small_tdt(tdt_path)
+    small_eou(eou_path)
+    T, W = 24000, 8000
+    _frames_file(tmp_path / "t.bin", [synth.encoder_frames(970, T, 128)])
+    _frames_file(tmp_path / "e.bin", [synth.encoder_frames(971, 10, 64)])
+    dt = pk.Decoder.from_gguf(tdt_path, n_slots=2)
+    _, k = pk.window_split([T], 10, dt.info.J, 5)
+    assert k[0] >= 2, k
+    print(f"dropin: tdt_greedy_decode over T={T} ({k[0]} launches), windows of {W}", flush=True)
+    r = subprocess.run([DRIVER, tdt_path, str(tmp_path / "t.bin"), eou_path, str(tmp_path / "e.bin"), str(W), "1"],
+                       capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stderr[-2000:]
+    t = json.loads(r.stdout)["tdt"]
+    ref = dt.decode([synth.encoder_frames(970, T, 128)], slots=[0])[0]
+    dt.close()
+    assert t["greedy"][0] == t["chunked"][0] == ref["tokens"].tolist()
+    assert t["steps"][0] == ref["steps"]
+    print(f"  {len(t['greedy'][0])} tokens, {ref['steps']} steps", flush=True)
+
+
+@pytest.mark.gpu
 def test_dropin_static_runtime_exits_cleanly(tmp_path):
     """The reference CLI keeps each runtime in a function-local static
     (src/main.cpp:746, :761) that is destroyed after main returns: the process
