@@ -1043,13 +1043,15 @@ int open_loop_lock(int device) {
 }
 
 
-// A cooperative launch guarantees that the whole grid (one workgroup per CU,
-// checked at create) is resident at once.  The runtime refuses it
-// (hipErrorIllegalState) while another process holds the device's
-// cooperative queue.  The loop is then an ordinary dispatch: on a device with
-// no other loop running the grid fits, and the ordering above keeps this
-// process's loops apart.  If a loop of another process overlaps it, the
-// barrier's 2 s limit ends both launches with PK_ERR_TIMEOUT.
+// The loop's grid (at most one workgroup per CU, checked at create) must be
+// resident at once.  A cooperative launch guarantees that; the runtime refuses
+// it (hipErrorIllegalState) while another process holds the device's
+// cooperative queue.  An ordinary dispatch checks it in the kernel
+// (pkdev::coresident).  Loops of this process are kept apart by the ordering
+// above, loops of other processes by the per-device lock (DeviceLoopLock); if
+// one overlaps anyway, the barriers' 2 s limit ends the launch with
+// PK_ERR_TIMEOUT.
+//
 // Arrival limit of an ordinary dispatch's co-residency check (a workgroup's start to the whole
 // grid arrived): a grid that has not arrived by then is relaunched cooperatively, and the next
 // kCoopAfterAbort launches on that device are cooperative.  (The first launch after the GPU has
