@@ -11,8 +11,9 @@
 //                       kNarrowRows rows: enc_proj_narrow_kernel instead
 //                       (bit-identical outputs).
 //   decode_loop_kernel  all lockstep iterations of all utterances in one
-//                       launch (cooperative where the runtime grants it;
-//                       see launch_loop).  The batch is split into
+//                       launch (an ordinary dispatch whose workgroups first
+//                       check that the whole grid is resident, relaunched
+//                       cooperatively if not; see launch_loop).  The batch is split into
 //                       independent domains (16 or 32 utterances, each on
 //                       nwg/C workgroups with its own barrier); one iteration
 //                       of a domain is
