@@ -129,12 +129,20 @@ class State:
 class OracleModel:
     def __init__(self, weights: dict, kind: str, H: int, L: int, J: int, D: int, vocab: int,
                  blank: int | None = None, durations=None, eou_id: int = -1, eob_id: int = -1,
-                 special=None):
+                 special=None, num_durations: int | None = None):
         p = "tdt" if kind == "tdt" else "eou"
         self.kind = TDT if kind == "tdt" else EOU
         self.H, self.L, self.J, self.D = H, L, J, D
         self.V1 = vocab + 1
-        self.Dn = len(durations) if (kind == "tdt" and durations is not None) else 0
+        # duration logits: num_durations (src/parakeet_tdt.cpp:592, from
+        # parakeet.tdt.num_durations), apart from the value table, which may be
+        # empty (duration = logit index, src/parakeet_tdt.cpp:938-940) or longer
+        if kind != "tdt":
+            self.Dn = 0
+        elif num_durations is not None:
+            self.Dn = int(num_durations)
+        else:
+            self.Dn = len(durations) if durations is not None else 0
         self.Vo = self.V1 + self.Dn
         self.blank = vocab if blank is None else blank
         self._keep = []
@@ -151,6 +159,11 @@ class OracleModel:
         m.eob = eob_id if eob_id >= 0 else vocab - 1
         self.eou, self.eob = m.eou, m.eob
         durs = list(durations or [])
+        if len(durs) > ORA_MAX_DUR or self.Dn > ORA_MAX_DUR:
+            raise ValueError(f"at most {ORA_MAX_DUR} durations")
+        if kind == "tdt" and 0 < len(durs) < self.Dn:
+            # the reference would index past its table; the device refuses it too
+            raise ValueError(f"durations table ({len(durs)}) shorter than num_durations ({self.Dn})")
         m.n_dur = len(durs) if kind == "tdt" else 0
         for i, d in enumerate(durs):
             m.durations[i] = int(d)
@@ -182,13 +195,15 @@ class OracleModel:
                             for s in pieces], np.uint8)
         if kind == "tdt":
             vocab = int(kv.get("parakeet.tdt.vocab_size", 8192))
+            # src/parakeet_ctc.cpp:428-439: the count defaults to 5, an absent
+            # table to {0, 1, 2, 3, 4}
             durs = kv.get("parakeet.tdt.durations")
             durs = [0, 1, 2, 3, 4] if durs is None else [int(x) for x in durs]
             return cls(weights, "tdt", int(kv.get("parakeet.tdt.pred_hidden", 640)),
                        int(kv.get("parakeet.tdt.pred_rnn_layers", 2)),
                        int(kv.get("parakeet.tdt.joint_hidden", 640)), D, vocab,
                        blank=int(kv.get("parakeet.tdt.blank_id", vocab)), durations=durs,
-                       special=special)
+                       special=special, num_durations=int(kv.get("parakeet.tdt.num_durations", 5)))
         vocab = int(kv.get("parakeet.eou.vocab_size", 1026))
         return cls(weights, "eou", int(kv.get("parakeet.eou.pred_hidden", 640)),
                    int(kv.get("parakeet.eou.pred_rnn_layers", 1)),

@@ -59,15 +59,25 @@ def vocab_pieces(kind: str, vocab: int, eou_id: int = -1, eob_id: int = -1) -> l
 def make_decoder_gguf(path: str, kind: str, H: int, L: int, J: int, D: int, vocab: int,
                       durations=None, eou_id: int = -1, eob_id: int = -1, max_symbols: int = 5,
                       quant: str = "q8_0", seed: int = WEIGHT_SEED, scale: float = 1.0,
-                      overrides: dict | None = None, meta_u32: dict | None = None) -> dict:
+                      overrides: dict | None = None, meta_u32: dict | None = None,
+                      num_durations: int | None = None) -> dict:
     """Write a decoder GGUF and return its float32 weights (dequantised from
     the stored bytes) keyed by tensor name.  ``overrides`` replaces named
     tensors (PyTorch layout) before quantisation -- used by scripted models;
-    ``meta_u32`` adds u32 metadata keys (e.g. parakeet.preproc.hop_length)."""
+    ``meta_u32`` adds u32 metadata keys (e.g. parakeet.preproc.hop_length).
+
+    TDT durations: ``num_durations`` (the duration logits, default the table's
+    length, or 5 without a table) is written apart from the table, as the
+    reference reads them (src/parakeet_ctc.cpp:428-439).  ``durations=None``
+    leaves the table key out (readers then use {0, 1, 2, 3, 4}); an empty list
+    writes an empty table (the duration is then the logit index)."""
     rng = np.random.default_rng(seed)
     p = "tdt" if kind == "tdt" else "eou"
     V1 = vocab + 1
-    n_dur = len(durations) if (kind == "tdt" and durations is not None) else 0
+    if kind == "tdt":
+        n_dur = num_durations if num_durations is not None else (5 if durations is None else len(durations))
+    else:
+        n_dur = 0
     Vo = V1 + n_dur
     G4 = 4 * H
 
@@ -103,7 +113,8 @@ def make_decoder_gguf(path: str, kind: str, H: int, L: int, J: int, D: int, voca
         w.add_u32("parakeet.tdt.pred_rnn_layers", L)
         w.add_u32("parakeet.tdt.joint_hidden", J)
         w.add_u32("parakeet.tdt.num_durations", n_dur)
-        w.add_arr("parakeet.tdt.durations", G.T_I32, list(durations or []))
+        if durations is not None:
+            w.add_arr("parakeet.tdt.durations", G.T_I32, list(durations))
     else:
         w.add_u32("parakeet.eou.vocab_size", vocab)
         w.add_u32("parakeet.eou.blank_id", vocab)

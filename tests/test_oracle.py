@@ -266,6 +266,89 @@ def test_tdt_blank_with_duration(tmp_path):
     assert r["steps"] == 4 and len(r["tokens"]) == 0
 
 
+def test_tdt_duration_table_closed_form(tmp_path):
+    """The duration is the table's value at the argmax index
+    (src/parakeet_tdt.cpp:938-940): table {0, 2, 3, 5, 8}."""
+    V1, table = 62, [0, 2, 3, 5, 8]
+    bias = np.zeros(V1 + 5, np.float32)
+    bias[61], bias[V1 + 3] = 1.0, 1.0                      # blank, index 3 -> 5 frames
+    om = _scripted(tmp_path, small_tdt, bias, durations=table)
+    st = om.new_state()
+    r = om.decode_window(np.zeros((12, 128), np.float32), st, 10)
+    assert r["steps"] == 3 and len(r["tokens"]) == 0 and st.st.carry_frames == 3
+    bias = np.zeros(V1 + 5, np.float32)
+    bias[7], bias[V1 + 1] = 1.0, 1.0                       # token 7, index 1 -> 2 frames
+    om = _scripted(tmp_path, small_tdt, bias, name="t.gguf", durations=table)
+    st = om.new_state()
+    r = om.decode_window(np.zeros((9, 128), np.float32), st, 10)
+    assert r["tokens"].tolist() == [7] * 5 and st.st.carry_frames == 1
+
+
+def test_tdt_three_durations_without_zero(tmp_path):
+    """num_durations 3, table {1, 4, 7}: V1 + 3 joint rows; a token at index 0
+    advances one frame, so the symbol cap is never reached."""
+    V1 = 62
+    bias = np.zeros(V1 + 3, np.float32)
+    bias[7], bias[V1] = 1.0, 1.0
+    om = _scripted(tmp_path, small_tdt, bias, durations=[1, 4, 7])
+    assert om.Dn == 3 and om.Vo == V1 + 3
+    r = om.decode_window(np.zeros((6, 128), np.float32), om.new_state(), 2)
+    assert r["tokens"].tolist() == [7] * 6 and r["steps"] == 6
+
+
+def test_tdt_empty_duration_table_uses_the_index(tmp_path):
+    """An empty table with num_durations 5: the duration is the argmax index."""
+    V1 = 62
+    bias = np.zeros(V1 + 5, np.float32)
+    bias[61], bias[V1 + 3] = 1.0, 1.0                      # blank, index 3 -> 3 frames
+    om = _scripted(tmp_path, small_tdt, bias, durations=[], num_durations=5)
+    assert om.Dn == 5
+    r = om.decode_window(np.zeros((10, 128), np.float32), om.new_state(), 10)
+    assert r["steps"] == 4 and len(r["tokens"]) == 0
+    bias = np.zeros(V1 + 5, np.float32)
+    bias[9], bias[V1] = 1.0, 1.0                           # token, index 0 -> symbol cap
+    om = _scripted(tmp_path, small_tdt, bias, name="t.gguf", durations=[], num_durations=5)
+    r = om.decode_window(np.zeros((4, 128), np.float32), om.new_state(), 3)
+    assert r["tokens"].tolist() == [9] * 12 and r["steps"] == 12
+
+
+@pytest.mark.parametrize("variant", [dict(durations=[], num_durations=5),
+                                     dict(durations=None, num_durations=5)])
+def test_tdt_index_tables_decode_alike(oracle_mod, tmp_path, variant):
+    """An empty table (duration = index) and an absent key (the {0, 1, 2, 3, 4}
+    default) decode a random model exactly as the explicit {0, 1, 2, 3, 4}."""
+    from parakeet_amd import gguf, synth
+    small_tdt(str(tmp_path / "a.gguf"))
+    small_tdt(str(tmp_path / "b.gguf"), **variant)
+    oa = oracle_mod.OracleModel.from_gguf(str(tmp_path / "a.gguf"), gguf)
+    ob = oracle_mod.OracleModel.from_gguf(str(tmp_path / "b.gguf"), gguf)
+    for u in range(3):
+        enc = synth.encoder_frames(60 + u, 40, 128)
+        ra = oa.decode_window(enc, oa.new_state(), 10, trace=True)
+        rb = ob.decode_window(enc, ob.new_state(), 10, trace=True)
+        assert np.array_equal(ra["trace"], rb["trace"]) and ra["steps"] == rb["steps"]
+        assert len(set(ra["trace"][:, 1].tolist())) >= 3      # several duration indices taken
+
+
+def test_tdt_table_longer_than_count(oracle_mod, tmp_path):
+    """num_durations 3 with a 5-entry table: only the first 3 entries exist as
+    logits, so the decode equals the one with table {0, 1, 2}; an index-3
+    entry of 9 is never taken.  A table shorter than the count is refused."""
+    from parakeet_amd import gguf, synth
+    small_tdt(str(tmp_path / "a.gguf"), durations=[0, 1, 2])
+    small_tdt(str(tmp_path / "b.gguf"), durations=[0, 1, 2, 9, 9], num_durations=3)
+    oa = oracle_mod.OracleModel.from_gguf(str(tmp_path / "a.gguf"), gguf)
+    ob = oracle_mod.OracleModel.from_gguf(str(tmp_path / "b.gguf"), gguf)
+    assert ob.Dn == 3 and ob.Vo == 62 + 3
+    enc = synth.encoder_frames(70, 40, 128)
+    ra = oa.decode_window(enc, oa.new_state(), 10, trace=True)
+    rb = ob.decode_window(enc, ob.new_state(), 10, trace=True)
+    assert np.array_equal(ra["trace"], rb["trace"]) and set(rb["trace"][:, 1].tolist()) == {0, 1, 2}
+    small_tdt(str(tmp_path / "c.gguf"), durations=[0, 1], num_durations=3)
+    with pytest.raises(ValueError):
+        oracle_mod.OracleModel.from_gguf(str(tmp_path / "c.gguf"), gguf)
+
+
 def test_eou_closed_forms(tmp_path):
     V1 = 36
     bias = np.zeros(V1, np.float32)
