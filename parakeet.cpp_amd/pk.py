@@ -109,6 +109,19 @@ def _ptr(a: np.ndarray | None):
     return None if a is None else C.c_void_p(a.ctypes.data)
 
 
+def _per_utt(v, n: int, dtype, name: str, scalar: bool = True):
+    """A per-utterance descriptor array of exactly n entries (the C ABI reads n
+    of them); a scalar is repeated for every utterance where ``scalar``."""
+    if v is None:
+        return None
+    a = np.asarray(v, dtype)
+    if a.ndim == 0 and scalar:
+        a = np.full(n, a, dtype)
+    if a.shape != (n,):
+        raise ValueError(f"{name}: shape {a.shape} for {n} utterances")
+    return np.ascontiguousarray(a)
+
+
 class DecoderInfo:
     """Decoder metadata as the reference loader reads it (src/parakeet_ctc.cpp:418-458)."""
 
@@ -267,8 +280,8 @@ class Decoder:
         pointer), read in place: utterance u decodes rows enc_row[u] ..
         enc_row[u] + n_frames[u] of the [rows, D] f32 array at enc_ptr.  The
         producer's stream must be synchronised first.  Returns what decode does."""
-        rows = np.ascontiguousarray(enc_row, np.int64)
-        T = np.ascontiguousarray(n_frames, np.int32)
+        T = np.ascontiguousarray(n_frames, np.int32).reshape(-1)
+        rows = _per_utt(enc_row, len(T), np.int64, "enc_row", scalar=False)
         return self._decode(MEM_DEVICE_FRAMES, C.c_void_p(enc_ptr), rows, T, self.info.D, slots, max_symbols,
                             blank_bias, tokens_base, trace, token_cap, logit_steps)
 
@@ -278,7 +291,7 @@ class Decoder:
         info = self.info
         n = len(T)
         max_symbols = info.max_symbols if max_symbols is None else max_symbols
-        slots = np.arange(n, dtype=np.int32) if slots is None else np.asarray(slots, np.int32)
+        slots = np.arange(n, dtype=np.int32) if slots is None else _per_utt(slots, n, np.int32, "slots", False)
         maxT = int(T.max()) if n else 0
         cap = token_cap if token_cap is not None else maxT * max(1, max_symbols) + 1
         toks = np.zeros((n, cap), np.int32)
@@ -288,8 +301,8 @@ class Decoder:
         nseg = np.zeros(n, np.int32)
         tcap = maxT * (max(1, max_symbols) + 1) + 1 if trace else 0
         tr = np.zeros((n, max(tcap, 1), 2), np.int32)
-        bb = None if blank_bias is None else np.ascontiguousarray(blank_bias, np.float32)
-        tb = None if tokens_base is None else np.ascontiguousarray(tokens_base, np.int32)
+        bb = _per_utt(blank_bias, n, np.float32, "blank_bias")
+        tb = _per_utt(tokens_base, n, np.int32, "tokens_base")
         b = PkBatch()
         b.n_utts, b.mem, b.d_enc, b.max_symbols = n, mem, d_enc, max_symbols
         b.enc, b.enc_row, b.n_frames, b.slot = enc, _ptr(rows), _ptr(T), _ptr(slots)
@@ -297,7 +310,7 @@ class Decoder:
         b.tokens, b.token_cap, b.n_tokens, b.steps = _ptr(toks), cap, _ptr(ntok), _ptr(steps)
         b.segments, b.seg_cap, b.n_segments = _ptr(segs), cap + 1, _ptr(nseg)
         b.trace, b.trace_cap = (_ptr(tr) if trace else None), tcap
-        rs = None if reset is None else np.ascontiguousarray(reset, np.uint8)
+        rs = _per_utt(reset, n, np.uint8, "reset")
         ctrl = np.zeros((n, PK_CTRL_N), np.int32)
         b.reset, b.ctrl_out = _ptr(rs), _ptr(ctrl)
         lg = None
@@ -323,15 +336,15 @@ class Decoder:
         addresses; the descriptor arrays (enc_row, n_frames, slots, blank_bias,
         tokens_base) are host arrays.  noalloc: pk_decode_noalloc (no device
         allocation; call scratch from the fixed per-device array)."""
-        n = len(n_frames)
-        rows = np.ascontiguousarray(enc_row, np.int64)
-        T = np.ascontiguousarray(n_frames, np.int32)
-        sl = np.ascontiguousarray(slots, np.int32)
-        bb = None if blank_bias is None else np.ascontiguousarray(blank_bias, np.float32)
+        T = np.ascontiguousarray(n_frames, np.int32).reshape(-1)
+        n = len(T)
+        rows = _per_utt(enc_row, n, np.int64, "enc_row", scalar=False)
+        sl = _per_utt(slots, n, np.int32, "slots", scalar=False)
+        bb = _per_utt(blank_bias, n, np.float32, "blank_bias")
         b = PkBatch()
         b.n_utts, b.mem, b.d_enc, b.max_symbols = n, MEM_DEVICE, self.info.D, max_symbols
         b.enc, b.enc_row, b.n_frames, b.slot = C.c_void_p(enc_ptr), _ptr(rows), _ptr(T), _ptr(sl)
-        tb = None if tokens_base is None else np.ascontiguousarray(tokens_base, np.int32)
+        tb = _per_utt(tokens_base, n, np.int32, "tokens_base")
         b.blank_bias, b.tokens_base = _ptr(bb), _ptr(tb)
         b.tokens, b.token_cap = C.c_void_p(out_ptrs["tokens"]), token_cap
         b.n_tokens, b.steps = C.c_void_p(out_ptrs["n_tokens"]), C.c_void_p(out_ptrs["steps"])

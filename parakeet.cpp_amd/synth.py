@@ -60,7 +60,7 @@ def make_decoder_gguf(path: str, kind: str, H: int, L: int, J: int, D: int, voca
                       durations=None, eou_id: int = -1, eob_id: int = -1, max_symbols: int = 5,
                       quant: str = "q8_0", seed: int = WEIGHT_SEED, scale: float = 1.0,
                       overrides: dict | None = None, meta_u32: dict | None = None,
-                      num_durations: int | None = None) -> dict:
+                      num_durations: int | None = None, blank_id: int | None = None) -> dict:
     """Write a decoder GGUF and return its float32 weights (dequantised from
     the stored bytes) keyed by tensor name.  ``overrides`` replaces named
     tensors (PyTorch layout) before quantisation -- used by scripted models;
@@ -70,7 +70,8 @@ def make_decoder_gguf(path: str, kind: str, H: int, L: int, J: int, D: int, voca
     length, or 5 without a table) is written apart from the table, as the
     reference reads them (src/parakeet_ctc.cpp:428-439).  ``durations=None``
     leaves the table key out (readers then use {0, 1, 2, 3, 4}); an empty list
-    writes an empty table (the duration is then the logit index)."""
+    writes an empty table (the duration is then the logit index).  ``blank_id``
+    defaults to ``vocab`` (the converter's choice; readers take any id)."""
     rng = np.random.default_rng(seed)
     p = "tdt" if kind == "tdt" else "eou"
     V1 = vocab + 1
@@ -108,7 +109,7 @@ def make_decoder_gguf(path: str, kind: str, H: int, L: int, J: int, D: int, voca
     w.add_u32("parakeet.encoder.d_model", D)
     if kind == "tdt":
         w.add_u32("parakeet.tdt.vocab_size", vocab)
-        w.add_u32("parakeet.tdt.blank_id", vocab)
+        w.add_u32("parakeet.tdt.blank_id", vocab if blank_id is None else blank_id)
         w.add_u32("parakeet.tdt.pred_hidden", H)
         w.add_u32("parakeet.tdt.pred_rnn_layers", L)
         w.add_u32("parakeet.tdt.joint_hidden", J)
@@ -117,7 +118,7 @@ def make_decoder_gguf(path: str, kind: str, H: int, L: int, J: int, D: int, voca
             w.add_arr("parakeet.tdt.durations", G.T_I32, list(durations))
     else:
         w.add_u32("parakeet.eou.vocab_size", vocab)
-        w.add_u32("parakeet.eou.blank_id", vocab)
+        w.add_u32("parakeet.eou.blank_id", vocab if blank_id is None else blank_id)
         w.add_i32("parakeet.eou.eou_id", eou_id)
         w.add_i32("parakeet.eou.eob_id", eob_id)
         w.add_u32("parakeet.eou.pred_hidden", H)

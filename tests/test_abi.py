@@ -53,3 +53,17 @@ def test_decoder_library_exports_device_handoff(pkg):
     for name in ("parakeet_hip::tdt_decode_batch_device(", "parakeet_hip::eou_decode_batch_device(",
                  "parakeet_hip::Engine::transcribe_device_batch("):
         assert name in syms, name
+
+
+def test_python_mirror_checks_per_utterance_arrays(pkg):
+    """pk_decode reads n_utts entries of every per-utterance array, so the
+    Python mirror repeats a scalar (offsets, token bases, reset flags) and
+    refuses an array of another length before any call."""
+    import numpy as np
+    from parakeet_amd import pk
+    assert pk._per_utt(None, 3, np.float32, "blank_bias") is None
+    assert pk._per_utt(2.0, 3, np.float32, "blank_bias").tolist() == [2.0, 2.0, 2.0]
+    assert pk._per_utt([1, 2], 2, np.int32, "slots", scalar=False).dtype == np.int32
+    for bad, scalar in (([1.0, 2.0], True), (5, False), ([[1], [2], [3]], True)):
+        with pytest.raises(ValueError):
+            pk._per_utt(bad, 3, np.float32, "x", scalar=scalar)

@@ -349,6 +349,71 @@ def test_tdt_table_longer_than_count(oracle_mod, tmp_path):
         oracle_mod.OracleModel.from_gguf(str(tmp_path / "c.gguf"), gguf)
 
 
+def test_tdt_blank_id_zero_closed_form(tmp_path):
+    """blank_id 0 (the reference takes any id from parakeet.tdt.blank_id): id 0
+    is the blank, id 61 (the converter's blank) an ordinary token."""
+    V1 = 62
+    bias = np.zeros(V1 + 5, np.float32)
+    bias[0], bias[V1 + 2] = 1.0, 1.0                       # id 0, index 2 -> blank, 2 frames
+    om = _scripted(tmp_path, small_tdt, bias, blank_id=0)
+    r = om.decode_window(np.zeros((10, 128), np.float32), om.new_state(), 10)
+    assert om.blank == 0 and r["steps"] == 5 and len(r["tokens"]) == 0
+    bias = np.zeros(V1 + 5, np.float32)
+    bias[61], bias[V1 + 1] = 1.0, 1.0                      # id 61, index 1 -> a token, 1 frame
+    om = _scripted(tmp_path, small_tdt, bias, name="t.gguf", blank_id=0)
+    r = om.decode_window(np.zeros((10, 128), np.float32), om.new_state(), 10)
+    assert r["tokens"].tolist() == [61] * 10
+
+
+def swap_blank(w, p, vocab, b):
+    """Tensor overrides that swap ids ``b`` and ``vocab`` (the blank) in the
+    embedding and the joint output: with blank_id ``b`` the model is the same
+    decoder with those two ids renamed."""
+    ov = {}
+    for name in (f"{p}.predict.embed.weight", f"{p}.joint.out.weight", f"{p}.joint.out.bias"):
+        a = np.array(w[name]).reshape(w[name].shape[0], -1) if w[name].ndim > 1 else np.array(w[name])
+        a[[b, vocab]] = a[[vocab, b]]
+        ov[name] = a
+    return ov
+
+
+@pytest.mark.parametrize("kind", ["tdt", "eou"])
+def test_blank_id_relabelling(oracle_mod, tmp_path, kind):
+    """Renaming the blank and an ordinary id (rows swapped, blank_id moved)
+    decodes the same: traces equal once the two ids are swapped back, segment
+    boundaries and step counts equal."""
+    from parakeet_amd import gguf, synth
+    writer, vocab, D, b = (small_tdt, 61, 128, 0) if kind == "tdt" else (small_eou, 35, 64, 5)
+    w = writer(str(tmp_path / "a.gguf"), quant="f32")
+    bias = w[f"{kind}.joint.out.bias"].copy()
+    bias[b] += 1.0                     # both renamed ids taken often
+    bias[vocab] += 2.0
+    w = writer(str(tmp_path / "a.gguf"), quant="f32", overrides={f"{kind}.joint.out.bias": bias})
+    shaped = dict(w)
+    shaped[f"{kind}.predict.embed.weight"] = w[f"{kind}.predict.embed.weight"].reshape(-1, 64)
+    shaped[f"{kind}.joint.out.weight"] = w[f"{kind}.joint.out.weight"].reshape(-1, 96)
+    writer(str(tmp_path / "b.gguf"), quant="f32", blank_id=b, overrides=swap_blank(shaped, kind, vocab, b))
+    oa = oracle_mod.OracleModel.from_gguf(str(tmp_path / "a.gguf"), gguf)
+    ob = oracle_mod.OracleModel.from_gguf(str(tmp_path / "b.gguf"), gguf)
+    assert ob.blank == b
+    ms = 10 if kind == "tdt" else 5
+    n_tok, n_b, n_blank = 0, 0, 0
+    for u in range(3):
+        enc = synth.encoder_frames(80 + u, 40, D)
+        ra = oa.decode_window(enc, oa.new_state(), ms, trace=True)
+        rb = ob.decode_window(enc, ob.new_state(), ms, trace=True)
+        tb = np.array(rb["trace"])
+        col = tb[:, 0] if tb.ndim == 2 else tb
+        col[:] = np.where(col == b, vocab, np.where(col == vocab, b, col))
+        assert np.array_equal(np.asarray(ra["trace"]), tb) and ra["steps"] == rb["steps"]
+        if kind == "eou":
+            assert np.array_equal(ra["segments"], rb["segments"])
+        n_tok += len(ra["tokens"])
+        ids = np.asarray(ra["trace"])[:, 0]
+        n_b, n_blank = n_b + int((ids == b).sum()), n_blank + int((ids == vocab).sum())
+    assert n_tok > 0 and n_b >= 5 and n_blank >= 5, (n_tok, n_b, n_blank)
+
+
 def test_eou_closed_forms(tmp_path):
     V1 = 36
     bias = np.zeros(V1, np.float32)
