@@ -33,6 +33,10 @@ SHAPES = [
     ("eou_L3_f32", dict(kind="eou", H=32, L=3, J=128, D=32, vocab=30, eou_id=28, eob_id=29, max_symbols=3,
                         quant="f32")),
     ("tdt_L8_h32", dict(kind="tdt", H=32, L=8, J=32, D=64, vocab=20, durations=[0, 1, 2], quant="q5_0")),
+    ("tdt_h1024", dict(kind="tdt", H=1024, L=2, J=1024, D=512, vocab=500, durations=[0, 1, 2, 3, 4],
+                       quant="q8_0")),
+    # near the LDS bound: one activation block of 16 rows x 2048 (hi + lo) takes 128.5 KB
+    ("tdt_j2048", dict(kind="tdt", H=64, L=2, J=2048, D=64, vocab=50, durations=[0, 1, 2, 3, 4], quant="q8_0")),
 ]
 
 
@@ -68,3 +72,15 @@ def test_shape_replay_and_batch_invariance(tmp_path, name, cfg):
         assert np.array_equal(small[u]["trace"], big[u]["trace"]), (name, u)
     print(f"  steps {sum(r['steps'] for r in big)}", flush=True)
     dev.close()
+
+
+def test_hidden_past_the_lds_is_refused(tmp_path):
+    """A joint_hidden whose activation block (16 rows x J, f16 hi + lo) does not fit
+    the LDS beside the loop's other buffers is refused at creation with
+    PK_ERR_UNSUPPORTED and a message, not decoded wrongly."""
+    from parakeet_amd import pk, synth
+    path = str(tmp_path / "j4096.gguf")
+    synth.make_decoder_gguf(path, kind="tdt", H=64, L=2, J=4096, D=64, vocab=50, durations=[0, 1, 2, 3, 4])
+    with pytest.raises(pk.PkError) as ei:
+        pk.Decoder.from_gguf(path, n_slots=1)
+    assert ei.value.rc == 5 and "LDS" in str(ei.value), ei.value
