@@ -152,7 +152,12 @@ typedef struct pk_batch {
 enum { PK_CTRL_INIT = 0, PK_CTRL_SYM, PK_CTRL_CARRY, PK_CTRL_LAST, PK_CTRL_SEGSTART,
        PK_CTRL_CUR, PK_CTRL_N = 8 };
 
-/* Upload the decoder and allocate n_slots state slots on the current device. */
+/* Upload the decoder and allocate n_slots state slots on the current device.
+ * Shapes: pred_hidden, joint_hidden and d_enc multiples of 32; 1 .. PK_MAX_LAYERS
+ * LSTM layers; vocab_size + 1 below 16383; 1 .. PK_MAX_DURATIONS TDT durations.
+ * The wider of pred_hidden and joint_hidden is staged as 16 rows of f16 hi + lo
+ * in one workgroup's LDS with the loop's other buffers, about 2,400 at most on
+ * gfx950; a wider decoder returns PK_ERR_UNSUPPORTED with the LDS figures. */
 PK_API int pk_decoder_create(const pk_decoder_desc *desc, int32_t n_slots, pk_decoder **out);
 PK_API int pk_decoder_destroy(pk_decoder *dec);
 /* tdt_init_state / eou_init_state: zero h, c, run the LSTM on embed[blank]. */
