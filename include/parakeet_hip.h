@@ -141,7 +141,11 @@ typedef struct pk_batch {
     /* [n_utts], nullable: 1 = start utterance u from a fresh state (zero h, c, one
      * LSTM step on embed[blank], counters reset -- what tdt_init_state /
      * eou_init_state do, src/parakeet_tdt.cpp:813-863) whatever its slot holds;
-     * the initial step runs inside the same launch. */
+     * the initial step runs inside the same launch.  A TDT window of 0 frames does
+     * not run at all (src/parakeet_tdt.cpp:879 returns before initialising): its
+     * slot keeps what it held, reset or not, its outputs are 0 and its ctrl_out
+     * reads as fresh when reset, so a caller passes the reset again with the slot's
+     * next window.  PK_MEM_DEVICE batches must not hold such windows (PK_ERR_ARG). */
     const uint8_t *reset;
     /* out [n_utts][PK_CTRL_N], nullable: each utterance's slot control words after
      * the call (as pk_slot_read returns them), copied back with the other outputs. */
