@@ -2,7 +2,10 @@
 slots, ragged windows, per-utterance blank offsets, a symbol cap drawn per
 call, some slots reset and the rest carrying their state from earlier calls
 (TDT symbols and carry_frames; EOU last token and segment start, with the
-segment indices counted from each session's running token total).  Every
+segment indices counted from each session's running token total), and a tenth
+of the windows empty (a TDT window of 0 frames returns before initialising,
+src/parakeet_tdt.cpp:879, and leaves its slot as it was; an EOU one
+initialises, src/parakeet_eou.cpp:246).  Every
 window of every call is replayed through the oracle carrying the same state
 per slot (teacher-forced, zero unexplained mismatches, final state within
 1e-3), so batch composition, domain planning (one domain at B <= 16, 16 or 32
@@ -41,11 +44,13 @@ def test_random_call_sequence(tmp_path, kind):
         slots = rng.choice(N_SLOTS, size=B, replace=False).astype(np.int32)
         sl = slots.tolist()
         T = rng.integers(1, 41, size=B).astype(np.int32)
+        T[rng.random(B) < 0.1] = 0   # empty windows: TDT returns before initialising, EOU initialises
         bias = rng.choice(np.array([0.0, 2.0, 4.0] if tdt else [0.0, 2.0], np.float32), size=B)
         ms = int(rng.choice([1, 2, 10] if tdt else [1, 3, 5]))
         reset = np.array([(s not in ost) or rng.random() < 0.2 for s in sl], np.uint8)
-        for s, r in zip(sl, reset):
-            if r:
+        for s, r, t in zip(sl, reset, T.tolist()):
+            # an empty TDT window leaves its slot as it was, a requested reset included
+            if (r and (not tdt or t > 0)) or s not in ost:
                 ost[s] = om.new_state()
                 tbase[s] = 0
         base = np.array([tbase[s] for s in sl], np.int32)
@@ -57,6 +62,9 @@ def test_random_call_sequence(tmp_path, kind):
                          reset=reset)
         for u in range(B):
             s = sl[u]
+            if tdt and T[u] == 0:
+                assert res[u]["steps"] == 0 and len(res[u]["tokens"]) == 0, (call, u)
+                continue
             check_window(om, dev, s, encs[u], res[u], ost[s], ms, blank_bias=float(bias[u]),
                          tokens_before=int(base[u]))
             tbase[s] += len(res[u]["tokens"])
